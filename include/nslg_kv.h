@@ -1,0 +1,179 @@
+/*
+ * nslg_kv.h — C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, element counts and an explicit hipStream_t
+ *     (pass torch.cuda.current_stream().cuda_stream from Python);
+ *   - is asynchronous on that stream and never synchronises the host;
+ *   - never allocates device memory: scratch space is caller-owned
+ *     ("workspace") and sized by the matching *_workspace_size() call;
+ *   - returns 0 on success and a negative NSLG_E* code on a bad argument,
+ *     an unsupported shape or a launch failure (nslg_last_error() gives text).
+ *
+ * KV pool layout (one layer): a flat array of token rows
+ *     pool[P * page_size][num_kv_heads][head_dim]
+ * i.e. [P, page_size, Hkv, D] with D fastest, token "slot id" = page * page_size + slot.
+ * The reference PagePool stores [L, P, ps, Hkv, D] per K and V
+ * (nanoslg/kv_cache.py:389-392); the layer-l slice of it is exactly this layout.
+ * The contiguous backend's [L, Bmax, Smax, Hkv, D] pool (kv_cache.py:229-232) is the
+ * same layout with P = Bmax, page_size = Smax and an identity block table.
+ *
+ * Block tables are CSR, as the reference builds them for FlashInfer
+ * (kv_cache.py:598-615): kv_indptr[B+1], kv_indices[kv_indptr[B]],
+ * kv_last_page_len[B] in [1, page_size].
+ */
+#ifndef NSLG_KV_H
+#define NSLG_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* nslg_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum nslg_dtype { NSLG_F16 = 0, NSLG_BF16 = 1, NSLG_F32 = 2 };
+
+enum nslg_status {
+  NSLG_OK = 0,
+  NSLG_EINVAL = -1,      /* bad pointer / size / stride */
+  NSLG_EUNSUPPORTED = -2,/* shape or dtype this build has no kernel for */
+  NSLG_ELAUNCH = -3,     /* the HIP launch itself failed */
+  NSLG_EWORKSPACE = -4   /* workspace too small */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nslg_version(void);
+
+/* Human-readable text of the last error seen on the calling thread. */
+const char* nslg_last_error(void);
+
+/*
+ * K/V append (scatter of the new tokens' rows into the pool).
+ * Replaces the per-run slice copies of FlashInferCacheContext._write_kv
+ * (nanoslg/kv_cache.py:661-674) and the decode index-put of
+ * ContiguousCacheContext.attend (kv_cache.py:301-303, 305-310).
+ *
+ *   k_src, v_src      [num_tokens] rows of Hkv*D elements; row i starts at
+ *                     element i*k_src_stride (resp. v_src_stride); D contiguous,
+ *                     heads at stride D inside a row.
+ *   slot_mapping      int32[num_tokens]: destination slot id (page*page_size+slot);
+ *                     a negative entry skips that row (padding), an entry
+ *                     >= pool_slots is rejected on the device (row skipped).
+ *   k_pool, v_pool    layer base pointers, pool_slots rows of Hkv*D elements.
+ * Bit-exact copy.
+ */
+int nslg_append_kv(const void* k_src, const void* v_src,
+                   int64_t k_src_stride, int64_t v_src_stride,
+                   const int32_t* slot_mapping, int32_t num_tokens,
+                   void* k_pool, void* v_pool, int64_t pool_slots,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                   nslg_stream_t stream);
+
+/*
+ * Zero whole pages across all layers (the zero-on-alloc of PagePool.alloc,
+ * nanoslg/kv_cache.py:411, and of ContiguousKVCache.allocate_sequence, :340),
+ * batched into one launch.
+ *   k_pool, v_pool    base of the [L, P, page_size, Hkv, D] pools
+ *   page_ids          int32[n] device array; ids outside [0, P) are skipped
+ */
+int nslg_zero_pages(void* k_pool, void* v_pool, int32_t num_layers,
+                    int64_t num_pages, int32_t page_size, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t dtype,
+                    const int32_t* page_ids, int32_t n, nslg_stream_t stream);
+
+/*
+ * Copy whole pages across all layers and all page slots: dst <- src for K and V
+ * (the copy-on-write of PagePool.cow, nanoslg/kv_cache.py:429-436), batched.
+ *   src_ids, dst_ids  int32[n] device arrays; a pair with an id outside [0, P)
+ *                     is skipped. dst ids must be distinct from every src id.
+ */
+int nslg_copy_pages(void* k_pool, void* v_pool, int32_t num_layers,
+                    int64_t num_pages, int32_t page_size, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t dtype,
+                    const int32_t* src_ids, const int32_t* dst_ids, int32_t n,
+                    nslg_stream_t stream);
+
+/*
+ * Gather paged K/V into a contiguous [B, max_len, Hkv, D] buffer per K and V
+ * (the slice read of ContiguousCacheContext.attend, nanoslg/kv_cache.py:312-314,
+ * without the transpose). Rows past a sequence's length are written as zeros.
+ * Bit-exact.
+ */
+int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
+                   int32_t page_size, const int32_t* kv_indptr,
+                   const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                   int32_t batch, int32_t max_len, int32_t num_kv_heads,
+                   int32_t head_dim, int32_t dtype, void* k_out, void* v_out,
+                   nslg_stream_t stream);
+
+/*
+ * Paged GQA decode attention, one query token per sequence, split-K over the
+ * sequence's pages with an fp32 log-sum-exp merge.
+ * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run
+ * (nanoslg/kv_cache.py:617-621, 650) and, with an identity block table, the
+ * contiguous decode SDPA (kv_cache.py:312-321).
+ *
+ *   q        [batch] rows of Hq*D elements at element stride q_stride
+ *   out      [batch] rows of Hq*D elements at element stride out_stride (q's dtype)
+ *   k_pool, v_pool, num_pages, page_size: one layer of the pool (see above)
+ *   kv_indptr/kv_indices/kv_last_page_len: CSR block table (device)
+ *   total_pages       host copy of kv_indptr[batch] (sizes the launch)
+ *   sm_scale          softmax scale (1/sqrt(D) for the reference)
+ *   workspace         caller-owned device scratch of at least
+ *                     nslg_paged_decode_workspace_size(...) bytes
+ * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16;
+ * D in {64, 128, 256}; 1 <= Hq/Hkv <= 16.
+ */
+size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                        int32_t head_dim, int64_t total_pages,
+                                        int32_t page_size);
+
+int nslg_paged_decode(const void* q, int64_t q_stride,
+                      const void* k_pool, const void* v_pool, int64_t num_pages,
+                      int32_t page_size, const int32_t* kv_indptr,
+                      const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                      int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                      int32_t dtype, void* out, int64_t out_stride,
+                      void* workspace, size_t workspace_bytes,
+                      nslg_stream_t stream);
+
+/*
+ * Paged causal prefill attention over a ragged batch of new tokens whose K/V
+ * are already appended to the pool (chunked prefill).
+ * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with
+ * causal=True (nanoslg/kv_cache.py:622-632, 654) and the contiguous
+ * masked/causal SDPA (kv_cache.py:317-321).
+ *
+ *   q           [T = qo_indptr[batch]] rows of Hq*D elements at stride q_stride
+ *   qo_indptr   int32[batch+1] (device): new tokens of sequence b are rows
+ *               [qo_indptr[b], qo_indptr[b+1]) and sit at the LAST positions of
+ *               that sequence's L_b tokens (bottom-right causal alignment):
+ *               row t of b attends to keys j <= L_b - n_b + t.
+ *   total_q     host copy of qo_indptr[batch]; max_q: host max of n_b
+ *   out         [T] rows of Hq*D elements at stride out_stride
+ * Supported: f16, bf16; D in {64, 128}; 1 <= Hq/Hkv <= 16.
+ */
+size_t nslg_paged_prefill_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                         int32_t head_dim, int64_t total_q,
+                                         int32_t max_q);
+
+int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                       int64_t total_q, int32_t max_q,
+                       const void* k_pool, const void* v_pool, int64_t num_pages,
+                       int32_t page_size, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                       int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                       int32_t head_dim, float sm_scale, int32_t dtype,
+                       void* out, int64_t out_stride,
+                       void* workspace, size_t workspace_bytes,
+                       nslg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSLG_KV_H */

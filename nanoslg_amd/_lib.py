@@ -1,0 +1,86 @@
+"""ctypes binding of libnslg_kv.so (declared in include/nslg_kv.h).
+
+The library must be built in-tree (``python -m nanoslg_amd._build`` or
+``__graft_entry__.build()``). There is no fallback: if the library is missing
+or fails to load, every kernel call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p, c_char_p, POINTER
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime first, so the library binds to it)
+
+LIB_PATH = Path(__file__).resolve().parent / "libnslg_kv.so"
+
+NSLG_F16, NSLG_BF16, NSLG_F32 = 0, 1, 2
+
+_I32P = POINTER(c_int32)
+
+# name -> (restype, argtypes); mirrors include/nslg_kv.h one to one.
+SIGNATURES = {
+    "nslg_version": (c_int32, []),
+    "nslg_last_error": (c_char_p, []),
+    "nslg_append_kv": (c_int32, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32,
+                                 c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p]),
+    "nslg_zero_pages": (c_int32, [c_void_p, c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32,
+                                  c_int32, c_void_p, c_int32, c_void_p]),
+    "nslg_copy_pages": (c_int32, [c_void_p, c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32,
+                                  c_int32, c_void_p, c_void_p, c_int32, c_void_p]),
+    "nslg_gather_kv": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p,
+                                 c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                 c_void_p]),
+    "nslg_paged_decode_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int64, c_int32]),
+    "nslg_paged_decode": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
+                                    c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                    c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,
+                                    c_void_p]),
+    "nslg_paged_prefill_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int64, c_int32]),
+    "nslg_paged_prefill": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_int32,
+                                     c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,
+                                     c_void_p, c_int32, c_int32, c_int32, c_int32, c_float, c_int32,
+                                     c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class KernelLibraryError(RuntimeError):
+    """The HIP kernel library is missing, failed to load, or a call failed."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once and attach the declared signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise KernelLibraryError(
+                f"{LIB_PATH} is not built; run `python -m nanoslg_amd._build` "
+                "(or __graft_entry__.build()) first — there is no CPU fallback")
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as e:
+            raise KernelLibraryError(f"failed to load {LIB_PATH}: {e}") from e
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().nslg_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise KernelLibraryError(f"{what} failed with status {rc}: {last_error()}")

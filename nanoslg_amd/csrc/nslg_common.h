@@ -1,0 +1,92 @@
+// Internal helpers shared by the gfx950 KV-cache kernels: error reporting,
+// dtype traits, 16-bit vector types for the MFMA builtins, wave primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/nslg_kv.h"
+
+namespace nslg {
+
+// ---- error reporting (thread-local text, integer status) -------------------
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+inline int elem_bytes(int dtype) {
+  switch (dtype) {
+    case NSLG_F16: return 2;
+    case NSLG_BF16: return 2;
+    case NSLG_F32: return 4;
+    default: return 0;
+  }
+}
+
+inline hipStream_t as_stream(nslg_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- vector types -------------------------------------------------------------
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// 16-bit element tags. Kernels move raw 16-bit words and only reinterpret them
+// at the MFMA / conversion boundary.
+struct F16 {
+  static constexpr int kDtype = NSLG_F16;
+  __device__ static inline float to_f32(unsigned short u) {
+    return (float)__builtin_bit_cast(_Float16, u);
+  }
+  __device__ static inline unsigned short from_f32(float x) {
+    return __builtin_bit_cast(unsigned short, (_Float16)x);
+  }
+  // D[16x16] += A[16x32] * B[32x16]   (8 elements per lane per operand)
+  __device__ static inline f32x4 mma_k32(u16x8 a, u16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // D[16x16] += A[16x16] * B[16x16]   (4 elements per lane per operand)
+  __device__ static inline f32x4 mma_k16(u16x4 a, u16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+
+struct BF16 {
+  static constexpr int kDtype = NSLG_BF16;
+  __device__ static inline float to_f32(unsigned short u) {
+    return __builtin_bit_cast(float, (unsigned int)u << 16);
+  }
+  __device__ static inline unsigned short from_f32(float x) {
+    return __builtin_bit_cast(unsigned short, (__bf16)x);
+  }
+  __device__ static inline f32x4 mma_k32(u16x8 a, u16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mma_k16(u16x4 a, u16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                     __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+  }
+};
+
+// ---- wave helpers ---------------------------------------------------------------
+__device__ inline float wave_xor_max(float x, int mask) {
+  return fmaxf(x, __shfl_xor(x, mask, 64));
+}
+__device__ inline float wave_xor_sum(float x, int mask) {
+  return x + __shfl_xor(x, mask, 64);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace nslg

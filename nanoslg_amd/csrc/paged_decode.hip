@@ -1,0 +1,487 @@
+// Split-K paged GQA decode attention for gfx950 (CDNA4), plus the fp32
+// log-sum-exp merge of the splits.
+//
+// Work decomposition
+//   The sequences' tokens are cut into chunks of `chunk_tokens` (a multiple of
+//   16). Workgroup x = global chunk id, workgroup y = group of KV heads; each
+//   wave owns one (chunk, kv head) and works alone: no LDS, no barriers. A
+//   sequence of L tokens gets ceil(L / chunk_tokens) chunks, so a 32k-token
+//   sequence gets 64x the waves of a 512-token one and the grid stays balanced
+//   under log-uniform lengths. Each wave finds its sequence by a wave-wide
+//   prefix sum over the per-sequence chunk counts (kv_indptr is a few hundred
+//   bytes and L2-resident), so no separate planning launch is needed.
+//
+// Per 16-token tile (one page at page_size 16), for the G query heads of the
+// wave's KV head (G = Hq/Hkv <= 16):
+//   S[16 tok x 16 col] = K[16 tok x D] * Q^T[D x 16 col]   (v_mfma 16x16x32, D/32 steps)
+//     A = K rows straight from HBM (lane l: token l%16, 16 B at d = 32s + 8(l/16)),
+//     B = Q^T held in registers for the whole chunk; columns >= G are zero.
+//   online softmax in fp32 on the accumulator layout (lane l holds tokens
+//     4(l/16)+j of head l%16); max over the 16 tokens = 3 in-lane max + 2 xor-shuffles.
+//   O^T[D x 16 col] += V^T[D x 16 tok] * P^T[16 tok x 16 col]  (v_mfma 16x16x16, D/16 tiles)
+//     B = P^T is exactly the S accumulator layout, converted to 16 bit;
+//     A = V^T: lane l loads tokens 4(l/16)+j (j=0..3), 16 B at d = (D/16)*(l%16), so each
+//     load instruction reads 4 whole 256 B rows; output tile n then holds
+//     d = (D/16)*row + n, a permutation undone when the result is stored.
+// K and V of the next tile are loaded before the current tile is computed.
+//
+// HBM traffic per (token, kv head): 2*D*2 bytes (K and V, read once).
+#include "nslg_common.h"
+
+#include <math.h>
+
+namespace nslg {
+namespace {
+
+constexpr int kMaxWaves = 4;  // waves (KV heads) per workgroup
+
+struct DecodeParams {
+  const uint16_t* q;
+  int64_t q_stride;  // elements between batch rows
+  const uint16_t* k_pool;
+  const uint16_t* v_pool;
+  int64_t num_pages;
+  int32_t page_size;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* last_len;
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t group;  // Hq / Hkv
+  float scale_log2;
+  int32_t chunk_tokens;
+  int32_t max_chunks;
+  uint16_t* out;
+  int64_t out_stride;
+  float* part_o;   // [max_chunks, Hq, D]
+  float* part_ml;  // [max_chunks, Hq, 2]
+};
+
+__device__ inline int seq_len_of(const int32_t* indptr, const int32_t* last_len, int s,
+                                 int page_size) {
+  const int np = indptr[s + 1] - indptr[s];
+  if (np <= 0) return 0;
+  int lpl = last_len[s];
+  lpl = lpl < 1 ? 1 : (lpl > page_size ? page_size : lpl);
+  return (np - 1) * page_size + lpl;
+}
+
+// Wave-wide search for the sequence owning global chunk `g`.
+__device__ inline bool locate_chunk(const int32_t* indptr, const int32_t* last_len, int batch,
+                                    int page_size, int chunk_tokens, int g, int& b, int& cstart,
+                                    int& nchunks) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  for (int s0 = 0; s0 < batch; s0 += 64) {
+    const int s = s0 + lane;
+    int nc = 0;
+    if (s < batch) {
+      const int len = seq_len_of(indptr, last_len, s, page_size);
+      nc = (len + chunk_tokens - 1) / chunk_tokens;
+    }
+    int incl = nc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int excl = incl - nc;
+    const bool hit = nc > 0 && g >= base + excl && g < base + incl;
+    const unsigned long long m = __ballot(hit);
+    if (m) {
+      const int src = __ffsll((long long)m) - 1;
+      b = s0 + src;
+      cstart = base + __shfl(excl, src, 64);
+      nchunks = __shfl(nc, src, 64);
+      return true;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  return false;
+}
+
+template <int N>
+struct RowVec {
+  typedef unsigned short type __attribute__((ext_vector_type(N)));
+};
+
+template <int D>
+struct Tile {
+  static constexpr int kSteps = D / 32;  // QK k-steps of 32
+  static constexpr int kNT = D / 16;     // PV output tiles; V elements per lane per token
+  u16x8 k[kSteps];
+  typename RowVec<kNT>::type v[4];
+};
+
+// Address of token `tok` (clamped into [0, len)) for kv head h.
+__device__ inline const uint16_t* token_row(const uint16_t* pool, const int32_t* idx, int64_t num_pages,
+                                            int page_size, int64_t row_elems, int head_off, int tok) {
+  int32_t pid = idx[tok / page_size];
+  if (pid < 0 || (int64_t)pid >= num_pages) pid = 0;
+  return pool + ((int64_t)pid * page_size + (tok % page_size)) * row_elems + head_off;
+}
+
+template <int D, bool kTileInPage>
+__device__ inline void load_tile(const DecodeParams& p, const int32_t* idx, int head_off,
+                                 int t0, int t_last, Tile<D>& t) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int gq = lane >> 4;
+  const int64_t row_elems = (int64_t)p.num_kv_heads * D;
+  constexpr int NT = D / 16;
+  typedef typename RowVec<NT>::type VT;
+  if constexpr (kTileInPage) {
+    // The 16 tokens of the tile share one page; slot0 is its first slot.
+    int32_t pid = idx[t0 / p.page_size];
+    if (pid < 0 || (int64_t)pid >= p.num_pages) pid = 0;
+    const int slot0 = t0 % p.page_size;
+    const int64_t page_base = (int64_t)pid * p.page_size;
+    int tk = t0 + r;
+    tk = tk > t_last ? t_last : tk;
+    const uint16_t* krow = p.k_pool + (page_base + slot0 + (tk - t0)) * row_elems + head_off;
+#pragma unroll
+    for (int s = 0; s < Tile<D>::kSteps; ++s)
+      t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int tv = t0 + 4 * gq + j;
+      tv = tv > t_last ? t_last : tv;
+      const uint16_t* vrow = p.v_pool + (page_base + slot0 + (tv - t0)) * row_elems + head_off;
+      t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
+    }
+  } else {
+    int tk = t0 + r;
+    tk = tk > t_last ? t_last : tk;
+    const uint16_t* krow = token_row(p.k_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tk);
+#pragma unroll
+    for (int s = 0; s < Tile<D>::kSteps; ++s)
+      t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int tv = t0 + 4 * gq + j;
+      tv = tv > t_last ? t_last : tv;
+      const uint16_t* vrow = token_row(p.v_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tv);
+      t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
+    }
+  }
+}
+
+template <typename T, int D, bool kTileInPage>
+__global__ void __launch_bounds__(64 * kMaxWaves)
+paged_decode_kernel(DecodeParams p) {
+  constexpr int kSteps = D / 32;
+  constexpr int NT = D / 16;
+  constexpr bool kSplitP = T::kDtype == NSLG_BF16;  // P = hi + lo for bf16's 8-bit mantissa
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = blockIdx.y * (blockDim.x >> 6) + wave;
+  if (h >= p.num_kv_heads) return;
+
+  int b = 0, cstart = 0, nchunks = 0;
+  if (!locate_chunk(p.indptr, p.last_len, p.batch, p.page_size, p.chunk_tokens, blockIdx.x, b,
+                    cstart, nchunks))
+    return;
+  const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+  const int t_begin = (blockIdx.x - cstart) * p.chunk_tokens;
+  int t_end = t_begin + p.chunk_tokens;
+  t_end = t_end > len ? len : t_end;
+  const int t_last = t_end - 1;
+  const int32_t* idx = p.indices + p.indptr[b];
+
+  const int r = lane & 15;
+  const int gq = lane >> 4;
+  const int hq = h * p.group + r;
+  const bool head_ok = r < p.group;
+
+  // Q^T operand: lane l holds Q[head l%16][32s + 8(l/16) .. +8]; zero for padding heads.
+  u16x8 qb[kSteps];
+  if (head_ok) {
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_stride + (int64_t)hq * D;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) qb[s] = *reinterpret_cast<const u16x8*>(qrow + 32 * s + 8 * gq);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) qb[s] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  const int head_off = h * D;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x4 o[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  Tile<D> cur, nxt;
+  load_tile<D, kTileInPage>(p, idx, head_off, t_begin, t_last, cur);
+  for (int t0 = t_begin; t0 < t_end; t0 += 16) {
+    const bool has_next = t0 + 16 < t_end;
+    if (has_next) load_tile<D, kTileInPage>(p, idx, head_off, t0 + 16, t_last, nxt);
+
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(cur.k[ks], qb[ks], s);
+
+    float sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sv[j] = (t0 + 4 * gq + j < t_end) ? s[j] * p.scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = wave_xor_max(mx, 16);
+    mx = wave_xor_max(mx, 32);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float pj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pj[j] = fast_exp2(sv[j] - m_new);
+    l_run = l_run * alpha + ((pj[0] + pj[1]) + (pj[2] + pj[3]));
+    m_run = m_new;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[n] *= alpha;
+
+    u16x4 pb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pb[j] = T::from_f32(pj[j]);
+    u16x4 pb_lo;
+    if constexpr (kSplitP) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pb_lo[j] = T::from_f32(pj[j] - T::to_f32(pb[j]));
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      u16x4 a = {cur.v[0][n], cur.v[1][n], cur.v[2][n], cur.v[3][n]};
+      o[n] = T::mma_k16(a, pb, o[n]);
+      if constexpr (kSplitP) o[n] = T::mma_k16(a, pb_lo, o[n]);
+    }
+    if (has_next) cur = nxt;
+  }
+
+  float l_tot = wave_xor_sum(l_run, 16);
+  l_tot = wave_xor_sum(l_tot, 32);
+  if (!head_ok) return;
+
+  // Lane l holds O[head r][d = NT*(4*gq + i) + n] in o[n][i].
+  if (nchunks == 1) {
+    const float inv = 1.f / l_tot;
+    uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      typename RowVec<NT>::type w;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) w[n] = T::from_f32(o[n][i] * inv);
+      *reinterpret_cast<typename RowVec<NT>::type*>(orow + NT * (4 * gq + i)) = w;
+    }
+  } else {
+    const int64_t slot = (int64_t)blockIdx.x * p.num_qo_heads + hq;
+    float* prow = p.part_o + slot * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int n4 = 0; n4 < NT; n4 += 4) {
+        f32x4 w = {o[n4][i], o[n4 + 1][i], o[n4 + 2][i], o[n4 + 3][i]};
+        *reinterpret_cast<f32x4*>(prow + NT * (4 * gq + i) + n4) = w;
+      }
+    }
+    if (gq == 0) {
+      float2 ml = make_float2(m_run, l_tot);
+      *reinterpret_cast<float2*>(p.part_ml + slot * 2) = ml;
+    }
+  }
+}
+
+struct MergeParams {
+  const int32_t* indptr;
+  const int32_t* last_len;
+  int32_t batch;
+  int32_t page_size;
+  int32_t num_qo_heads;
+  int32_t chunk_tokens;
+  int32_t max_chunks;
+  const float* part_o;
+  const float* part_ml;
+  uint16_t* out;
+  int64_t out_stride;
+};
+
+// One workgroup per sequence; sequences with several chunks are merged, empty
+// sequences get zero rows, single-chunk ones were finished by the decode kernel.
+// Thread -> (head, 4 consecutive d).
+template <typename T, int D>
+__global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+  int nchunks = (len + p.chunk_tokens - 1) / p.chunk_tokens;
+  constexpr int DV = D / 4;
+  const int total = p.num_qo_heads * DV;
+  if (nchunks == 0) {
+    // A sequence with no tokens attends to nothing: its output rows are zero.
+    for (int it = threadIdx.x; it < total; it += blockDim.x)
+      *reinterpret_cast<u16x4*>(p.out + (int64_t)b * p.out_stride + (int64_t)(it / DV) * D +
+                                4 * (it % DV)) = u16x4{0, 0, 0, 0};
+    return;
+  }
+  if (nchunks == 1) return;
+  int before = 0;
+  for (int s = lane; s < b; s += 64) {
+    const int ls = seq_len_of(p.indptr, p.last_len, s, p.page_size);
+    before += (ls + p.chunk_tokens - 1) / p.chunk_tokens;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off, 64);
+  const int cstart = before;
+  if (cstart >= p.max_chunks) return;
+  if (cstart + nchunks > p.max_chunks) nchunks = p.max_chunks - cstart;
+
+  for (int it = threadIdx.x; it < total; it += blockDim.x) {
+    const int hq = it / DV;
+    const int d4 = it % DV;
+    float mmax = -INFINITY;
+    for (int c = 0; c < nchunks; ++c)
+      mmax = fmaxf(mmax, p.part_ml[((int64_t)(cstart + c) * p.num_qo_heads + hq) * 2]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+      const int64_t slot = (int64_t)(cstart + c) * p.num_qo_heads + hq;
+      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + slot * 2);
+      const float w = fast_exp2(ml.x - mmax);
+      const f32x4 oc = *reinterpret_cast<const f32x4*>(p.part_o + slot * D + 4 * d4);
+      acc += w * oc;
+      lsum += w * ml.y;
+    }
+    const float inv = 1.f / lsum;
+    u16x4 w16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(acc[j] * inv);
+    *reinterpret_cast<u16x4*>(p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + 4 * d4) = w16;
+  }
+}
+
+// Tokens per split: about 1024 splits over the whole batch, at least 64 tokens,
+// a multiple of 16.
+inline int choose_chunk_tokens(int64_t total_tokens) {
+  int64_t c = (total_tokens + 1023) / 1024;
+  c = ((c + 15) / 16) * 16;
+  if (c < 64) c = 64;
+  if (c > (1 << 20)) c = 1 << 20;
+  return (int)c;
+}
+
+inline int64_t max_chunks_for(int32_t batch, int64_t total_tokens, int chunk_tokens) {
+  return (total_tokens + chunk_tokens - 1) / chunk_tokens + batch;
+}
+
+template <typename T, int D>
+int launch_decode(const DecodeParams& p, const MergeParams& mp, hipStream_t s) {
+  const int waves = p.num_kv_heads < kMaxWaves ? p.num_kv_heads : kMaxWaves;
+  dim3 grid(p.max_chunks, (p.num_kv_heads + waves - 1) / waves);
+  if (p.page_size % 16 == 0)
+    paged_decode_kernel<T, D, true><<<grid, 64 * waves, 0, s>>>(p);
+  else
+    paged_decode_kernel<T, D, false><<<grid, 64 * waves, 0, s>>>(p);
+  int rc = check_launch("paged_decode");
+  if (rc) return rc;
+  decode_merge_kernel<T, D><<<p.batch, 256, 0, s>>>(mp);
+  return check_launch("paged_decode_merge");
+}
+
+}  // namespace
+}  // namespace nslg
+
+using namespace nslg;
+
+extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                                   int32_t head_dim, int64_t total_pages,
+                                                   int32_t page_size) {
+  if (batch <= 0 || num_qo_heads <= 0 || head_dim <= 0 || total_pages < 0 || page_size <= 0) return 0;
+  const int64_t total_tokens = total_pages * page_size;
+  const int ct = choose_chunk_tokens(total_tokens);
+  const int64_t mc = max_chunks_for(batch, total_tokens, ct);
+  return (size_t)(mc * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
+}
+
+extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_pool,
+                                 const void* v_pool, int64_t num_pages, int32_t page_size,
+                                 const int32_t* kv_indptr, const int32_t* kv_indices,
+                                 const int32_t* kv_last_page_len, int64_t total_pages,
+                                 int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                 int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                 nslg_stream_t stream) {
+  if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
+      num_pages <= 0 || total_pages < 0)
+    return fail(NSLG_EINVAL, "paged_decode: bad sizes");
+  if (batch == 0) return NSLG_OK;
+  if (!q || !k_pool || !v_pool || !kv_indptr || !kv_indices || !kv_last_page_len || !out)
+    return fail(NSLG_EINVAL, "paged_decode: null pointer");
+  if (num_qo_heads % num_kv_heads != 0)
+    return fail(NSLG_EINVAL, "paged_decode: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
+  const int group = num_qo_heads / num_kv_heads;
+  if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_decode: GQA group %d > 16", group);
+  if (dtype != NSLG_F16 && dtype != NSLG_BF16)
+    return fail(NSLG_EUNSUPPORTED, "paged_decode: dtype %d (f16/bf16 only)", dtype);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(NSLG_EUNSUPPORTED, "paged_decode: head_dim %d", head_dim);
+  if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
+    return fail(NSLG_EINVAL, "paged_decode: row stride smaller than Hq*D");
+  if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) & 15 ||
+      (q_stride * 2) % 16 || (out_stride * 2) % 16)
+    return fail(NSLG_EINVAL, "paged_decode: q/pool/out must be 16-byte aligned");
+  const int64_t total_tokens = total_pages * page_size;
+  if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
+  const int ct = choose_chunk_tokens(total_tokens);
+  const int64_t mc = max_chunks_for(batch, total_tokens, ct);
+  const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, head_dim, total_pages, page_size);
+  if (!workspace || workspace_bytes < need)
+    return fail(NSLG_EWORKSPACE, "paged_decode: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (((uintptr_t)workspace) & 255) return fail(NSLG_EINVAL, "paged_decode: workspace must be 256-byte aligned");
+
+  DecodeParams p;
+  p.q = (const uint16_t*)q;
+  p.q_stride = q_stride;
+  p.k_pool = (const uint16_t*)k_pool;
+  p.v_pool = (const uint16_t*)v_pool;
+  p.num_pages = num_pages;
+  p.page_size = page_size;
+  p.indptr = kv_indptr;
+  p.indices = kv_indices;
+  p.last_len = kv_last_page_len;
+  p.batch = batch;
+  p.num_qo_heads = num_qo_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = group;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.chunk_tokens = ct;
+  p.max_chunks = (int32_t)mc;
+  p.out = (uint16_t*)out;
+  p.out_stride = out_stride;
+  float* ws = (float*)workspace;
+  p.part_o = ws;
+  p.part_ml = ws + mc * num_qo_heads * head_dim;
+
+  MergeParams mp;
+  mp.indptr = kv_indptr;
+  mp.last_len = kv_last_page_len;
+  mp.batch = batch;
+  mp.page_size = page_size;
+  mp.num_qo_heads = num_qo_heads;
+  mp.chunk_tokens = ct;
+  mp.max_chunks = (int32_t)mc;
+  mp.part_o = p.part_o;
+  mp.part_ml = p.part_ml;
+  mp.out = p.out;
+  mp.out_stride = out_stride;
+
+  hipStream_t s = as_stream(stream);
+  if (dtype == NSLG_F16) {
+    switch (head_dim) {
+      case 64: return launch_decode<F16, 64>(p, mp, s);
+      case 128: return launch_decode<F16, 128>(p, mp, s);
+      default: return launch_decode<F16, 256>(p, mp, s);
+    }
+  }
+  switch (head_dim) {
+    case 64: return launch_decode<BF16, 64>(p, mp, s);
+    case 128: return launch_decode<BF16, 128>(p, mp, s);
+    default: return launch_decode<BF16, 256>(p, mp, s);
+  }
+}

@@ -1,0 +1,237 @@
+"""Tensor-level wrappers over the C ABI of libnslg_kv.so.
+
+Each function validates shapes, dtypes, devices and strides on the host, then
+passes raw device pointers and the current HIP stream to the library. Nothing
+here computes on the CPU: a missing library or a non-HIP tensor raises.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float16: _lib.NSLG_F16, torch.bfloat16: _lib.NSLG_BF16, torch.float32: _lib.NSLG_F32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise TypeError(f"unsupported KV dtype {dt}") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    dev = None
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("HIP kernels need device tensors (got a CPU tensor); there is no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor (got {t.dtype})")
+    return t
+
+
+def _rows(x: torch.Tensor, name: str) -> Tuple[int, int, int]:
+    """(num_rows, row_stride, heads) for a [..., H, D] tensor with a dense [H, D] block
+    whose leading dims collapse to a single row stride."""
+    if x.dim() < 2:
+        raise ValueError(f"{name} must have at least 2 dims")
+    H, D = x.shape[-2], x.shape[-1]
+    try:
+        v = x.view(-1, H, D)
+    except RuntimeError:
+        raise ValueError(f"{name}: leading dims do not collapse to one row stride") from None
+    if v.stride(2) != 1 or (H > 1 and v.stride(1) != D):
+        raise ValueError(f"{name}: the trailing [H, D] block must be contiguous")
+    n = v.shape[0]
+    return n, (v.stride(0) if n > 1 else H * D), H
+
+
+def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: torch.Tensor,
+              k_pool: torch.Tensor, v_pool: torch.Tensor) -> None:
+    """Scatter rows of k_new/v_new ([..., Hkv, D]) into one layer of the pool.
+
+    slot_mapping: int32 with one entry per row (page*page_size + slot; <0 = skip).
+    k_pool/v_pool: one layer, [P, page_size, Hkv, D] (or any contiguous [..., Hkv, D]).
+    """
+    _require_gpu(k_new, v_new, slot_mapping, k_pool, v_pool)
+    _i32(slot_mapping, "slot_mapping")
+    if k_new.dtype != k_pool.dtype or v_new.dtype != v_pool.dtype or k_pool.dtype != v_pool.dtype:
+        raise TypeError("append_kv: k/v dtypes must match the pool dtype")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("append_kv: pool layer must be contiguous")
+    Hkv, D = k_pool.shape[-2], k_pool.shape[-1]
+    if tuple(k_new.shape[-2:]) != (Hkv, D) or tuple(v_new.shape[-2:]) != (Hkv, D):
+        raise ValueError("append_kv: k_new/v_new trailing dims must be [Hkv, D] of the pool")
+    nk, ks, _ = _rows(k_new, "k_new")
+    nv, vs, _ = _rows(v_new, "v_new")
+    T = slot_mapping.numel()
+    if nk != T or nv != T:
+        raise ValueError(f"append_kv: {T} slots for {nk} k rows / {nv} v rows")
+    slots = k_pool.numel() // (Hkv * D)
+    rc = _lib.load().nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(),
+                                    T, k_pool.data_ptr(), v_pool.data_ptr(), slots, Hkv, D,
+                                    dtype_code(k_pool.dtype), _stream(k_pool))
+    _lib.check(rc, "nslg_append_kv")
+
+
+def _pool_geom(k_pool: torch.Tensor, v_pool: torch.Tensor):
+    if k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype:
+        raise ValueError("k/v pools must have the same shape and dtype")
+    if k_pool.dim() != 5 or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous [L, P, page_size, Hkv, D]")
+    return k_pool.shape
+
+
+def zero_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, page_ids: torch.Tensor) -> None:
+    """Zero pages `page_ids` of a [L, P, ps, Hkv, D] pool pair, all layers."""
+    _require_gpu(k_pool, v_pool, page_ids)
+    _i32(page_ids, "page_ids")
+    L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
+    rc = _lib.load().nslg_zero_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D,
+                                     dtype_code(k_pool.dtype), page_ids.data_ptr(), page_ids.numel(),
+                                     _stream(k_pool))
+    _lib.check(rc, "nslg_zero_pages")
+
+
+def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_ids: torch.Tensor,
+               dst_ids: torch.Tensor) -> None:
+    """pool[:, dst] <- pool[:, src] for K and V, all layers and slots."""
+    _require_gpu(k_pool, v_pool, src_ids, dst_ids)
+    _i32(src_ids, "src_ids")
+    _i32(dst_ids, "dst_ids")
+    if src_ids.numel() != dst_ids.numel():
+        raise ValueError("copy_pages: src/dst length mismatch")
+    L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
+    rc = _lib.load().nslg_copy_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D,
+                                     dtype_code(k_pool.dtype), src_ids.data_ptr(), dst_ids.data_ptr(),
+                                     src_ids.numel(), _stream(k_pool))
+    _lib.check(rc, "nslg_copy_pages")
+
+
+def _layer_geom(k_layer: torch.Tensor, v_layer: torch.Tensor):
+    if k_layer.dim() != 4 or k_layer.shape != v_layer.shape or k_layer.dtype != v_layer.dtype:
+        raise ValueError("pool layer must be [P, page_size, Hkv, D] for both K and V")
+    if not (k_layer.is_contiguous() and v_layer.is_contiguous()):
+        raise ValueError("pool layer must be contiguous")
+    return k_layer.shape
+
+
+def gather_kv(k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
+              kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, max_len: int
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Paged -> contiguous [B, max_len, Hkv, D] K and V (zeros past each length)."""
+    _require_gpu(k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, n)
+    P, ps, Hkv, D = _layer_geom(k_layer, v_layer)
+    B = kv_indptr.numel() - 1
+    k_out = torch.empty((B, max_len, Hkv, D), dtype=k_layer.dtype, device=k_layer.device)
+    v_out = torch.empty_like(k_out)
+    rc = _lib.load().nslg_gather_kv(k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                                    kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, max_len, Hkv, D,
+                                    dtype_code(k_layer.dtype), k_out.data_ptr(), v_out.data_ptr(),
+                                    _stream(k_layer))
+    _lib.check(rc, "nslg_gather_kv")
+    return k_out, v_out
+
+
+class Workspace:
+    """Caller-owned device scratch for the attention kernels; grows on demand."""
+
+    def __init__(self, device: torch.device, nbytes: int = 0):
+        self.device = torch.device(device)
+        self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf.numel() < nbytes:
+            self.buf = torch.empty(int(nbytes * 1.25) + 256, dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def paged_decode_workspace_size(batch: int, num_qo_heads: int, head_dim: int, total_pages: int,
+                                page_size: int) -> int:
+    return int(_lib.load().nslg_paged_decode_workspace_size(batch, num_qo_heads, head_dim, total_pages,
+                                                            page_size))
+
+
+def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                 total_pages: int, sm_scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None
+                 ) -> torch.Tensor:
+    """Decode attention. q: [B, Hq, D] (rows may be strided); returns [B, Hq, D]."""
+    _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, n)
+    P, ps, Hkv, D = _layer_geom(k_layer, v_layer)
+    if q.dim() != 3 or q.shape[2] != D:
+        raise ValueError(f"paged_decode: q must be [B, Hq, {D}]")
+    if q.dtype != k_layer.dtype:
+        raise TypeError("paged_decode: q dtype must match the pool")
+    B, Hq, _ = q.shape
+    if q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError("paged_decode: q's [Hq, D] block must be contiguous")
+    if kv_indptr.numel() != B + 1 or kv_last_page_len.numel() < B:
+        raise ValueError("paged_decode: kv_indptr must have B+1 entries and kv_last_page_len B")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    if out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D or out.dtype != q.dtype:
+        raise ValueError("paged_decode: bad out tensor")
+    lib = _lib.load()
+    need = int(lib.nslg_paged_decode_workspace_size(B, Hq, D, int(total_pages), ps))
+    ws = (workspace or Workspace(q.device)).get(need)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
+                               kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                               int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
+                               out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+    _lib.check(rc, "nslg_paged_decode")
+    return out
+
+
+def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
+                  k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
+                  kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                  sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                  workspace: Optional[Workspace] = None) -> torch.Tensor:
+    """Causal (bottom-right) prefill attention. q: ragged [T, Hq, D]; returns [T, Hq, D]."""
+    _require_gpu(q, qo_indptr, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
+    for t, n in ((qo_indptr, "qo_indptr"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                 (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, n)
+    P, ps, Hkv, D = _layer_geom(k_layer, v_layer)
+    if q.dim() != 3 or q.shape[2] != D or q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError(f"paged_prefill: q must be [T, Hq, {D}] with a contiguous [Hq, D] block")
+    if q.dtype != k_layer.dtype:
+        raise TypeError("paged_prefill: q dtype must match the pool")
+    T, Hq, _ = q.shape
+    B = kv_indptr.numel() - 1
+    if qo_indptr.numel() != B + 1 or T < total_q:
+        raise ValueError("paged_prefill: qo_indptr must have B+1 entries and q at least total_q rows")
+    if out is None:
+        out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    need = int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q)))
+    ws = (workspace or Workspace(q.device)).get(need)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    rc = lib.nslg_paged_prefill(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), int(total_q), int(max_q),
+                                k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                                kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale,
+                                dtype_code(q.dtype), out.data_ptr(), out.stride(0), ws.data_ptr(),
+                                ws.numel(), _stream(q))
+    _lib.check(rc, "nslg_paged_prefill")
+    return out

@@ -1,0 +1,942 @@
+"""KV cache for MI355X: paged pool + radix prefix sharing + contiguous fallback.
+
+Drop-in for nanoslg/kv_cache.py. The public surface keeps the reference's names
+and call shapes so the model code is unchanged:
+
+  KVCacheConfig            kv_cache.py:59-145
+  CacheContext (ABC)       kv_cache.py:149-163   get_position_ids / attend / get_start_pos
+  KVCacheManager (ABC)     kv_cache.py:166-189   allocate/extend/begin/end/release/...
+  PagePool                 kv_cache.py:382-442
+  RadixTree                kv_cache.py:445-531
+  PagedKVCache             kv_cache.py:694-777   (the reference's FlashInferPagedKVCache)
+  PagedCacheContext        kv_cache.py:545-691   (the reference's FlashInferCacheContext)
+  ContiguousKVCache        kv_cache.py:328-379
+  ContiguousCacheContext   kv_cache.py:247-325
+  create_cache_manager     kv_cache.py:780-805
+
+Below `attend` every byte of K/V is moved and every attention output computed
+by the hand-written gfx950 kernels in libnslg_kv.so (see ``kernels``): the
+append scatter, the batched zero/copy of pages, split-K paged decode and the
+MFMA chunked-prefill kernel. The host side here only keeps integer bookkeeping
+(free list, refcounts, block tables, radix tree) and builds each forward's plan
+(slot mapping, CSR block table, positions) with numpy, uploaded in one pinned
+host-to-device copy. There is no CPU attention path.
+"""
+from __future__ import annotations
+
+import math
+import threading
+from abc import ABC, abstractmethod
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+_BACKENDS = ("paged", "contiguous")
+
+
+def _default_kernels():
+    from . import kernels
+    return kernels
+
+
+# --------------------------------------------------------------------------------------
+# configuration
+# --------------------------------------------------------------------------------------
+
+
+@dataclass
+class KVCacheConfig:
+    """Pool geometry and backend choice (kv_cache.py:59-145).
+
+    backend: "auto" and "flashinfer" select the paged HIP backend; "contiguous"
+    selects the [L, Bmax, Smax, Hkv, D] pool. Heads are per tensor-parallel rank."""
+    num_layers: int
+    num_kv_heads: int
+    num_qo_heads: int
+    head_dim: int
+    page_size: int = 16
+    max_pages: int = 0            # 0 = size from free device memory (paged)
+    max_batch_size: int = 8       # contiguous
+    max_seq_len: int = 4096       # contiguous
+    memory_fraction: float = 0.30
+    dtype: torch.dtype = torch.bfloat16
+    device: torch.device = None
+    enable_prefix_caching: bool = True
+    backend: str = "auto"
+    max_pages_cap: int = 65536    # the reference's auto-size cap (kv_cache.py:97)
+
+    def __post_init__(self):
+        if self.backend in ("auto", "flashinfer"):
+            self.backend = "paged"
+        if self.backend not in _BACKENDS:
+            raise ValueError(f"unknown KV backend {self.backend!r}; use auto|paged|contiguous")
+        if self.num_qo_heads % self.num_kv_heads:
+            raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
+        if self.backend == "paged" and self.max_pages <= 0:
+            self.max_pages = self._auto_pages()
+        if self.backend == "contiguous":
+            self._auto_seq_len()
+
+    def _elem_bytes(self) -> int:
+        return {torch.float16: 2, torch.bfloat16: 2, torch.float32: 4}.get(self.dtype, 2)
+
+    def _device_mem(self) -> Optional[Tuple[int, int]]:
+        if self.device is None:
+            return None
+        dev = torch.device(self.device)
+        if dev.type != "cuda" or not torch.cuda.is_available():
+            return None
+        return torch.cuda.mem_get_info(dev)
+
+    def _auto_pages(self) -> int:
+        """kv_cache.py:88-102: budget = (free - max(2 GiB, 15% total)) * fraction."""
+        mem = self._device_mem()
+        if mem is None:
+            return 256
+        free, total = mem
+        headroom = max(2 << 30, int(total * 0.15))
+        budget = int(max(0, free - headroom) * self.memory_fraction)
+        per_page = (2 * self.num_layers * self.page_size * self.num_kv_heads * self.head_dim
+                    * self._elem_bytes())
+        return max(64, min(budget // max(per_page, 1), self.max_pages_cap))
+
+    def _auto_seq_len(self):
+        """kv_cache.py:104-117."""
+        mem = self._device_mem()
+        if mem is None:
+            return
+        free, _ = mem
+        budget = int(free * self.memory_fraction * 0.5)
+        per_tok = 2 * self.num_layers * self.num_kv_heads * self.head_dim * self._elem_bytes()
+        cap = budget // max(per_tok, 1) // max(self.max_batch_size, 1)
+        self.max_seq_len = min(self.max_seq_len, max(512, cap))
+
+    @classmethod
+    def from_hf_config(cls, hf_config, parallel_config=None, device=None, **kw) -> "KVCacheConfig":
+        """kv_cache.py:119-145 (heads divided by tp; PP layer split if configured)."""
+        nl = getattr(hf_config, "num_hidden_layers", getattr(hf_config, "num_layers", 32))
+        nkv = getattr(hf_config, "num_key_value_heads",
+                      getattr(hf_config, "multi_query_group_num",
+                              getattr(hf_config, "num_attention_heads", 32)))
+        nq = getattr(hf_config, "num_attention_heads", 32)
+        hd = getattr(hf_config, "head_dim",
+                     getattr(hf_config, "kv_channels", hf_config.hidden_size // nq))
+        if parallel_config is not None:
+            tp = getattr(parallel_config, "tp_size", 1)
+            if tp > 1:
+                nkv //= tp
+                nq //= tp
+            splits = getattr(parallel_config, "pp_layer_splits", None)
+            rank = getattr(parallel_config, "pp_rank", None)
+            if getattr(parallel_config, "pp_size", 1) > 1 and splits and rank in splits:
+                nl = len(splits[rank])
+        return cls(num_layers=nl, num_kv_heads=nkv, num_qo_heads=nq, head_dim=hd, device=device, **kw)
+
+
+# --------------------------------------------------------------------------------------
+# the drop-in ABCs (kv_cache.py:149-189)
+# --------------------------------------------------------------------------------------
+
+
+class CacheContext(ABC):
+    seq_ids: List[str]
+    new_token_counts: List[int]
+    input_offsets: List[int]
+    batch_size: int
+    seq_lens: List[int]
+
+    @abstractmethod
+    def get_position_ids(self, max_input_len: int) -> torch.Tensor: ...
+
+    @abstractmethod
+    def attend(self, layer_idx: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+               n_heads: int, n_kv_heads: int) -> torch.Tensor: ...
+
+    @abstractmethod
+    def get_start_pos(self, batch_idx: int = 0) -> int: ...
+
+    def get_position(self, max_input_len: int) -> torch.Tensor:
+        """Alias of get_position_ids (the name used in the reference's README)."""
+        return self.get_position_ids(max_input_len)
+
+
+class KVCacheManager(ABC):
+    cfg: KVCacheConfig
+
+    @abstractmethod
+    def allocate_sequence(self, seq_id: str, token_ids: Optional[List[int]] = None,
+                          num_tokens: int = 0) -> int: ...
+
+    @abstractmethod
+    def extend_sequence(self, seq_id: str, num_new: int = 1): ...
+
+    @abstractmethod
+    def begin_forward(self, seq_ids: List[str], new_token_counts: List[int],
+                      input_offsets: Optional[List[int]] = None) -> CacheContext: ...
+
+    @abstractmethod
+    def end_forward(self, ctx: CacheContext): ...
+
+    @abstractmethod
+    def release_sequence(self, seq_id: str): ...
+
+    @abstractmethod
+    def append_token_ids(self, seq_id: str, new_ids: List[int]): ...
+
+    @abstractmethod
+    def reset(self): ...
+
+    @property
+    @abstractmethod
+    def stats(self) -> Dict: ...
+
+
+# --------------------------------------------------------------------------------------
+# host -> device plan upload
+# --------------------------------------------------------------------------------------
+
+
+def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Tensor]:
+    """Concatenate int32 arrays, copy once host->device (pinned, async), return views."""
+    sizes = [int(p.size) for p in parts]
+    flat = np.concatenate([np.asarray(p, dtype=np.int32).reshape(-1) for p in parts]) if parts else \
+        np.zeros(0, np.int32)
+    host = torch.from_numpy(flat)
+    if device.type == "cuda":
+        dev = host.pin_memory().to(device, non_blocking=True)
+    else:
+        dev = host.clone()
+    out, off = [], 0
+    for n in sizes:
+        out.append(dev[off:off + n])
+        off += n
+    return out
+
+
+def _positions(start_positions, new_token_counts, input_offsets, iw) -> np.ndarray:
+    """[B, iw] positions: pos[b, off+t] = start_b + t, zeros elsewhere (kv_cache.py:267-278)."""
+    B = len(start_positions)
+    pos = np.zeros((B, iw), np.int32)
+    for b in range(B):
+        o, n = input_offsets[b], new_token_counts[b]
+        if n > 0:
+            pos[b, o:o + n] = np.arange(start_positions[b], start_positions[b] + n, dtype=np.int32)
+    return pos
+
+
+class _ForwardPlan:
+    """Device-side metadata of one forward, shared by every layer's attend()."""
+
+    def __init__(self, device, batch, iw, slot_grid, positions, indptr, indices, lpl, qo_indptr,
+                 q_rows, cow_src, cow_dst):
+        (self.slot, self.pos_i32, self.indptr, self.indices, self.lpl, self.qo_indptr, self.q_rows,
+         self.cow_src, self.cow_dst) = _upload_i32(
+            [slot_grid, positions, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst], device)
+        self.batch, self.iw = batch, iw
+        self.total_pages = int(indptr[-1]) if len(indptr) else 0
+        self.total_q = int(qo_indptr[-1]) if len(qo_indptr) else 0
+        self._slot_by_S: Dict[int, torch.Tensor] = {iw: self.slot}
+        self._pos_long: Optional[torch.Tensor] = None
+
+    def slots_for(self, S: int) -> torch.Tensor:
+        s = self._slot_by_S.get(S)
+        if s is None:
+            grid = self.slot.view(self.batch, self.iw)
+            if S < self.iw:
+                s = grid[:, :S].contiguous().view(-1)
+            else:
+                pad = torch.full((self.batch, S - self.iw), -1, dtype=torch.int32, device=grid.device)
+                s = torch.cat([grid, pad], 1).view(-1)
+            self._slot_by_S[S] = s
+        return s
+
+    def positions_long(self) -> torch.Tensor:
+        if self._pos_long is None:
+            self._pos_long = self.pos_i32.view(self.batch, self.iw).long()
+        return self._pos_long
+
+
+def _get_positions(plan: _ForwardPlan, batch: int, iw: int, S: int) -> torch.Tensor:
+    pos = plan.positions_long()
+    if S <= iw:
+        return pos[:, :S]
+    return torch.cat([pos, pos.new_zeros(batch, S - iw)], 1)
+
+
+# --------------------------------------------------------------------------------------
+# page pool (kv_cache.py:382-442)
+# --------------------------------------------------------------------------------------
+
+
+class PagePool:
+    """K and V pools [L, P, page_size, Hkv, D] on the device; page 0 is the permanent
+    null/sink page. Host state: int32 refcounts and tokens_used, a LIFO free stack
+    (lowest ids first on a fresh pool). Zero-on-alloc and copy-on-write are batched
+    device launches."""
+
+    def __init__(self, cfg: KVCacheConfig, kernels=None):
+        self.cfg = cfg
+        self.kernels = kernels or _default_kernels()
+        P = cfg.max_pages
+        if P < 2:
+            raise ValueError("max_pages must be >= 2 (page 0 is reserved)")
+        shape = (cfg.num_layers, P, cfg.page_size, cfg.num_kv_heads, cfg.head_dim)
+        dev = torch.device(cfg.device) if cfg.device is not None else torch.device("cpu")
+        self.device = dev
+        self.k = torch.zeros(shape, dtype=cfg.dtype, device=dev)
+        self.v = torch.zeros(shape, dtype=cfg.dtype, device=dev)
+        self.ref_count = np.zeros(P, np.int64)
+        self.tokens_used = np.zeros(P, np.int64)
+        self.ref_count[0] = 1
+        self._is_free = np.zeros(P, bool)
+        self._is_free[1:] = True
+        self._free: List[int] = list(range(P - 1, 0, -1))
+        self._lock = threading.Lock()
+
+    # -- allocation --------------------------------------------------------------------
+    def alloc(self, n: int = 1, zero: bool = True) -> Optional[List[int]]:
+        """All-or-nothing allocation of n pages (refcount 1, tokens_used 0).
+        Returns None when fewer than n are free. zero=True zeroes them on the device
+        (all layers, K and V) in one launch."""
+        with self._lock:
+            if len(self._free) < n:
+                return None
+            out = [self._free.pop() for _ in range(n)]
+            idx = np.asarray(out, np.int64)
+            self.ref_count[idx] = 1
+            self.tokens_used[idx] = 0
+            self._is_free[idx] = False
+        if zero and out:
+            self.zero(out)
+        return out
+
+    def zero(self, page_ids: List[int]) -> None:
+        if not page_ids:
+            return
+        (ids,) = _upload_i32([np.asarray(page_ids, np.int32)], self.device)
+        self.kernels.zero_pages(self.k, self.v, ids)
+
+    def release(self, pid: int) -> None:
+        if pid <= 0:
+            return
+        with self._lock:
+            self.ref_count[pid] -= 1
+            if self.ref_count[pid] <= 0:
+                self.ref_count[pid] = 0
+                self.tokens_used[pid] = 0
+                if not self._is_free[pid]:
+                    self._is_free[pid] = True
+                    self._free.append(pid)
+
+    def add_ref(self, pid: int) -> None:
+        with self._lock:
+            self.ref_count[pid] += 1
+
+    def is_shared(self, pid: int) -> bool:
+        return bool(self.ref_count[pid] > 1)
+
+    def cow_alloc(self, pid: int) -> Optional[int]:
+        """Host half of copy-on-write (kv_cache.py:429-436): a new page with the source's
+        tokens_used; the device copy is issued by copy(). Does not release pid."""
+        new = self.alloc(1, zero=False)
+        if new is None:
+            return None
+        d = new[0]
+        self.tokens_used[d] = self.tokens_used[pid]
+        return d
+
+    def copy(self, src_ids, dst_ids) -> None:
+        if len(src_ids) == 0:
+            return
+        src, dst = _upload_i32([np.asarray(src_ids, np.int32), np.asarray(dst_ids, np.int32)], self.device)
+        self.kernels.copy_pages(self.k, self.v, src, dst)
+
+    def cow(self, pid: int) -> Optional[int]:
+        """Single-page copy-on-write: allocate, copy all layers and slots, return the id."""
+        d = self.cow_alloc(pid)
+        if d is not None:
+            self.copy([pid], [d])
+        return d
+
+    @property
+    def num_free(self) -> int:
+        return len(self._free)
+
+    @property
+    def utilization(self) -> float:
+        return 1.0 - self.num_free / max(self.cfg.max_pages - 1, 1)
+
+
+# --------------------------------------------------------------------------------------
+# radix prefix tree (kv_cache.py:445-531), page granular
+# --------------------------------------------------------------------------------------
+
+
+class _RNode:
+    __slots__ = ("children", "page_id", "ref", "last_access", "depth")
+
+    def __init__(self, depth=0):
+        self.children: Dict[tuple, "_RNode"] = {}
+        self.page_id = -1
+        self.ref = 0
+        self.last_access = 0
+        self.depth = depth
+
+
+class RadixTree:
+    """Prefix tree over full pages of token ids. Node depth is in pages; each edge is the
+    tuple of page_size token ids of one page; a node may hold the id of a pool page with
+    those tokens' K/V. Only full pages are ever shared (as in the reference, whose match
+    returns whole pages only, kv_cache.py:459-472).
+
+    Differences from the reference's per-token trie, on purpose:
+      * match stops at the first page node without a page (after an interior
+        eviction), so the returned pages always cover tokens [0, 16*len(pages)) with no
+        gap (the reference can skip a page there);
+      * access times come from a counter, so ties only arise within one call, as
+        with the reference's monotonic clock (LRU ties keep DFS pre-order)."""
+
+    def __init__(self, ps: int, pool: PagePool):
+        self.root = _RNode()
+        self.ps = ps
+        self.pool = pool
+        self._lock = threading.Lock()
+        self._clock = 0
+
+    def _now(self) -> int:
+        self._clock += 1
+        return self._clock
+
+    def _keys(self, tokens):
+        ps = self.ps
+        for i in range(len(tokens) // ps):
+            yield tuple(tokens[i * ps:(i + 1) * ps])
+
+    def match(self, tokens) -> Tuple[int, List[int]]:
+        with self._lock:
+            node, pages, now = self.root, [], self._now()
+            for key in self._keys(tokens):
+                ch = node.children.get(key)
+                if ch is None:
+                    break
+                node = ch
+                node.last_access = now
+                if node.page_id < 0:
+                    break
+                if self.pool.ref_count[node.page_id] > 0:
+                    pages.append(node.page_id)
+                else:
+                    node.page_id = -1
+                    break
+            return len(pages) * self.ps, pages
+
+    def insert(self, tokens, page_ids) -> None:
+        with self._lock:
+            node, now = self.root, self._now()
+            for i, key in enumerate(self._keys(tokens)):
+                ch = node.children.get(key)
+                if ch is None:
+                    ch = _RNode(i + 1)
+                    node.children[key] = ch
+                node = ch
+                node.last_access = now
+                if i < len(page_ids) and node.page_id < 0:
+                    node.page_id = page_ids[i]
+                    self.pool.add_ref(page_ids[i])
+
+    def add_refs(self, tokens, n: int = 1) -> None:
+        with self._lock:
+            node = self.root
+            for key in self._keys(tokens):
+                ch = node.children.get(key)
+                if ch is None:
+                    break
+                node = ch
+                node.ref += n
+
+    def dec_refs(self, tokens, n: int = 1) -> None:
+        with self._lock:
+            node = self.root
+            for key in self._keys(tokens):
+                ch = node.children.get(key)
+                if ch is None:
+                    break
+                node = ch
+                node.ref = max(0, node.ref - n)
+
+    def evict_lru(self, need: int) -> int:
+        """Release unpinned cached pages, least recently used first (stable: DFS
+        pre-order on ties), dropping emptied leaves. Returns pages released."""
+        with self._lock:
+            cands: list = []
+            self._collect(self.root, cands)
+            cands.sort(key=lambda x: x[0])
+            freed = 0
+            for _, nd, par, edge in cands:
+                if freed >= need:
+                    break
+                if nd.ref > 0:
+                    continue
+                if nd.page_id >= 0:
+                    self.pool.release(nd.page_id)
+                    nd.page_id = -1
+                    freed += 1
+                if not nd.children and par is not None:
+                    par.children.pop(edge, None)
+            return freed
+
+    def _collect(self, node, out, par=None, edge=None):
+        stack = [(node, par, edge)]
+        while stack:
+            nd, pa, ed = stack.pop()
+            if nd.page_id >= 0 and nd.ref == 0:
+                out.append((nd.last_access, nd, pa, ed))
+            for t, ch in reversed(list(nd.children.items())):
+                stack.append((ch, nd, t))
+
+    @property
+    def cached_pages(self) -> int:
+        c, stack = 0, [self.root]
+        while stack:
+            n = stack.pop()
+            if n.page_id >= 0:
+                c += 1
+            stack.extend(n.children.values())
+        return c
+
+
+# --------------------------------------------------------------------------------------
+# paged backend
+# --------------------------------------------------------------------------------------
+
+
+class _PagedSeqState:
+    """Per-sequence state (kv_cache.py:534-542); the block table is an int32 array."""
+    __slots__ = ("seq_id", "bt", "n_pages", "num_tokens", "prefix_len", "token_ids")
+
+    def __init__(self, sid, prefix_pages=None, plen=0, tids=None):
+        self.seq_id = sid
+        pages = list(prefix_pages or [])
+        self.bt = np.zeros(max(16, 2 * len(pages)), np.int32)
+        self.bt[:len(pages)] = pages
+        self.n_pages = len(pages)
+        self.num_tokens = plen
+        self.prefix_len = plen
+        self.token_ids = list(tids or [])
+
+    @property
+    def block_table(self) -> List[int]:
+        return self.bt[:self.n_pages].tolist()
+
+    def extend(self, pages: List[int]) -> None:
+        need = self.n_pages + len(pages)
+        if need > self.bt.size:
+            nb = np.zeros(max(need, 2 * self.bt.size), np.int32)
+            nb[:self.n_pages] = self.bt[:self.n_pages]
+            self.bt = nb
+        self.bt[self.n_pages:need] = pages
+        self.n_pages = need
+
+
+class PagedCacheContext(CacheContext):
+    """Per-forward context (kv_cache.py:545-691): positions, the write plan with
+    copy-on-write, the CSR block table; attend() = append kernel + paged attention."""
+
+    def __init__(self, cache: "PagedKVCache", seq_ids, new_token_counts, input_offsets,
+                 zero_pages: Optional[List[int]] = None):
+        self.cache = cache
+        self.seq_ids = list(seq_ids)
+        self.new_token_counts = list(new_token_counts)
+        self.input_offsets = list(input_offsets) if input_offsets else [0] * len(seq_ids)
+        self.batch_size = B = len(seq_ids)
+        cfg, pool, ps = cache.cfg, cache.pool, cache.cfg.page_size
+        states = [cache.seqs[s] for s in self.seq_ids]
+        self.start_positions = [st.num_tokens for st in states]
+        self.seq_lens = [self.start_positions[i] + self.new_token_counts[i] for i in range(B)]
+        self.max_kv_len = max(self.seq_lens) if self.seq_lens else 0
+        self._is_decode = B > 0 and all(n == 1 for n in self.new_token_counts)
+        self._iw = max(o + n for o, n in zip(self.input_offsets, self.new_token_counts)) if B else 1
+        iw = self._iw
+
+        # write plan + copy-on-write, in batch order (kv_cache.py:575-594): a shared page
+        # is copied by every writer but the last remaining sharer, which writes in place.
+        slot = np.full((B, iw), -1, np.int32)
+        cow_src: List[int] = []
+        cow_dst: List[int] = []
+        for b, st in enumerate(states):
+            n = self.new_token_counts[b]
+            if n <= 0:
+                continue
+            ap = np.arange(st.num_tokens, st.num_tokens + n, dtype=np.int64)
+            pi = ap // ps
+            for p in range(int(pi[0]), min(int(pi[-1]) + 1, st.n_pages)):
+                pid = int(st.bt[p])
+                if pool.is_shared(pid):
+                    new = pool.cow_alloc(pid)
+                    if new is None:
+                        raise RuntimeError("KV OOM during CoW")
+                    cow_src.append(pid)
+                    cow_dst.append(new)
+                    st.bt[p] = new
+                    pool.release(pid)
+            ok = pi < st.n_pages
+            pids = np.where(ok, st.bt[np.minimum(pi, max(st.n_pages - 1, 0))] if st.n_pages else 0, 0)
+            sls = np.where(ok, ap % ps, 0)
+            o = self.input_offsets[b]
+            slot[b, o:o + n] = (pids * ps + sls).astype(np.int32)
+            if ok.any():
+                np.maximum.at(pool.tokens_used, pids[ok], sls[ok] + 1)
+        self.cow_pairs = list(zip(cow_src, cow_dst))
+
+        # CSR block table (kv_cache.py:598-615)
+        lens = np.asarray(self.seq_lens, np.int64)
+        npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
+        indptr = np.zeros(B + 1, np.int64)
+        np.cumsum(npg, out=indptr[1:])
+        parts = []
+        for b, st in enumerate(states):
+            k = int(npg[b])
+            have = min(k, st.n_pages)
+            parts.append(st.bt[:have])
+            if k > have:
+                parts.append(np.zeros(k - have, np.int32))
+        indices = np.concatenate(parts) if parts else np.zeros(0, np.int32)
+        if indices.size == 0:
+            indices = np.zeros(1, np.int32)
+        lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
+        if B == 0:
+            lpl = np.zeros(1, np.int64)
+
+        qn = np.asarray(self.new_token_counts, np.int64)
+        qo = np.zeros(B + 1, np.int64)
+        np.cumsum(qn, out=qo[1:])
+        self._max_q = int(qn.max()) if B else 0
+        # rows of the [B*S] input grid that carry new tokens, in ragged order
+        self._uniform_rows = all(o == 0 for o in self.input_offsets) and all(n == iw for n in self.new_token_counts)
+        rows = [np.arange(b * iw + self.input_offsets[b], b * iw + self.input_offsets[b] + self.new_token_counts[b])
+                for b in range(B)]
+        q_rows = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+
+        if zero_pages:
+            pool.zero(zero_pages)
+        self._plan = _ForwardPlan(pool.device, B, iw, slot.reshape(-1), _positions(
+            self.start_positions, self.new_token_counts, self.input_offsets, iw).reshape(-1),
+            indptr, indices, lpl, qo, q_rows, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32))
+        if cow_src:
+            cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
+
+    # ---- CacheContext -----------------------------------------------------------------
+    def get_position_ids(self, S: int) -> torch.Tensor:
+        return _get_positions(self._plan, self.batch_size, self._iw, S)
+
+    def get_start_pos(self, idx: int = 0) -> int:
+        return self.start_positions[idx]
+
+    def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
+        """Write k_new/v_new into the pages of `layer_idx`, then attend.
+        q [B,S,Hq,D], k_new/v_new [B,S,Hkv,D] -> [B,S,Hq*D] in q's dtype."""
+        cache, pool, plan = self.cache, self.cache.pool, self._plan
+        kern = cache.kernels
+        B, S = q.shape[0], q.shape[1]
+        k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+        kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
+        if self._is_decode and S == 1:
+            out = kern.paged_decode(q[:, 0], k_layer, v_layer, plan.indptr, plan.indices, plan.lpl,
+                                    plan.total_pages, workspace=cache.workspace)
+            return out.reshape(B, 1, -1)
+        Hq, D = q.shape[2], q.shape[3]
+        if self._uniform_rows and S == self._iw:
+            q_rag = q.reshape(B * S, Hq, D)
+        else:
+            q_rag = q.reshape(B * S, Hq, D).index_select(0, plan.q_rows.long())
+        o_rag = kern.paged_prefill(q_rag, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace)
+        if self._uniform_rows and S == self._iw:
+            return o_rag.reshape(B, S, Hq * D)
+        out = q.new_zeros(B * S, Hq * D)
+        out.index_copy_(0, plan.q_rows.long(), o_rag.reshape(-1, Hq * D))
+        return out.view(B, S, Hq * D)
+
+    # ---- introspection used by tests and the bench -------------------------------------
+    @property
+    def plan(self) -> _ForwardPlan:
+        return self._plan
+
+
+class PagedKVCache(KVCacheManager):
+    """Paged KV cache manager (kv_cache.py:694-777) on the HIP kernels."""
+
+    def __init__(self, cfg: KVCacheConfig, kernels=None):
+        self.cfg = cfg
+        self.kernels = kernels or _default_kernels()
+        self.pool = PagePool(cfg, self.kernels)
+        self.tree = RadixTree(cfg.page_size, self.pool) if cfg.enable_prefix_caching else None
+        self.seqs: Dict[str, _PagedSeqState] = {}
+        self.workspace = self.kernels.Workspace(self.pool.device, 128 << 20)
+        self._pending_zero: List[int] = []
+
+    def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
+        """kv_cache.py:707-722: radix match (full pages), pin, allocate the rest."""
+        tids = list(token_ids or [])
+        total = len(tids) if tids else num_tokens
+        plen, ppages = 0, []
+        if self.tree and len(tids) >= self.cfg.page_size:
+            plen, ppages = self.tree.match(tids)
+            for p in ppages:
+                self.pool.add_ref(p)
+            if ppages:
+                self.tree.add_refs(tids[:plen])
+        st = _PagedSeqState(seq_id, ppages, plen, tids)
+        new = total - plen
+        if new > 0:
+            st.extend(self._alloc(math.ceil(new / self.cfg.page_size)))
+        self.seqs[seq_id] = st
+        return plen
+
+    def extend_sequence(self, seq_id, num_new=1):
+        st = self.seqs[seq_id]
+        need = math.ceil((st.num_tokens + num_new) / self.cfg.page_size)
+        if need > st.n_pages:
+            st.extend(self._alloc(need - st.n_pages, defer_zero=True))
+
+    def begin_forward(self, seq_ids, ntoks, offsets=None):
+        for s, n in zip(seq_ids, ntoks):
+            self.extend_sequence(s, n)
+        zero, self._pending_zero = self._pending_zero, []
+        return PagedCacheContext(self, seq_ids, ntoks, offsets, zero_pages=zero)
+
+    def end_forward(self, ctx):
+        for b in range(ctx.batch_size):
+            self.seqs[ctx.seq_ids[b]].num_tokens += ctx.new_token_counts[b]
+
+    def release_sequence(self, seq_id):
+        """kv_cache.py:739-751: cache full pages in the tree, unpin, release."""
+        st = self.seqs.get(seq_id)
+        if st is None:
+            return
+        ps = self.cfg.page_size
+        if self.tree and st.token_ids:
+            nf = min(st.num_tokens // ps, st.n_pages)
+            if nf:
+                self.tree.insert(st.token_ids[:nf * ps], st.block_table[:nf])
+            if st.prefix_len:
+                self.tree.dec_refs(st.token_ids[:st.prefix_len])
+        for p in st.bt[:st.n_pages].tolist():
+            self.pool.release(p)
+        del self.seqs[seq_id]
+
+    def append_token_ids(self, seq_id, ids):
+        if seq_id in self.seqs:
+            self.seqs[seq_id].token_ids.extend(ids)
+
+    def reset(self):
+        for s in list(self.seqs):
+            self.release_sequence(s)
+
+    def _alloc(self, n, defer_zero=False):
+        """kv_cache.py:760-768: pool, else LRU-evict from the tree and retry, else OOM."""
+        pages = self.pool.alloc(n, zero=not defer_zero)
+        if pages is None and self.tree and self.tree.evict_lru(n) > 0:
+            pages = self.pool.alloc(n, zero=not defer_zero)
+        if pages is None:
+            raise RuntimeError(f"KV OOM: need {n}, free {self.pool.num_free}")
+        if defer_zero:
+            self._pending_zero.extend(pages)
+        return pages
+
+    @property
+    def stats(self):
+        return {"backend": "paged",
+                "active_seqs": len(self.seqs),
+                "pages_used": self.cfg.max_pages - 1 - self.pool.num_free,
+                "pages_free": self.pool.num_free,
+                "util": f"{self.pool.utilization:.1%}",
+                "radix": self.tree.cached_pages if self.tree else 0}
+
+
+# --------------------------------------------------------------------------------------
+# contiguous backend: the same kernels with one Smax-token "page" per slot
+# --------------------------------------------------------------------------------------
+
+
+class _ContigSeqState:
+    __slots__ = ("seq_id", "slot", "num_tokens", "token_ids")
+
+    def __init__(self, seq_id, slot):
+        self.seq_id = seq_id
+        self.slot = slot
+        self.num_tokens = 0
+        self.token_ids: List[int] = []
+
+
+class ContiguousCacheContext(CacheContext):
+    """kv_cache.py:247-325. The [L, Bmax, Smax, Hkv, D] pool is a paged pool whose pages
+    are whole slots (page_size = Smax) with an identity block table, so the append
+    and attention kernels are the paged ones. Rows are addressed by the sequence's
+    slot (the reference indexes by batch row; identical while slots are 0..B-1)."""
+
+    def __init__(self, cache: "ContiguousKVCache", seq_ids, new_token_counts, input_offsets):
+        self.cache = cache
+        self.seq_ids = list(seq_ids)
+        self.new_token_counts = list(new_token_counts)
+        self.input_offsets = list(input_offsets) if input_offsets else [0] * len(seq_ids)
+        self.batch_size = B = len(seq_ids)
+        cfg = cache.cfg
+        Smax = cfg.max_seq_len
+        self.slots = [cache.states[s].slot for s in self.seq_ids]
+        self.start_positions = [cache.states[s].num_tokens for s in self.seq_ids]
+        self.seq_lens = [self.start_positions[i] + self.new_token_counts[i] for i in range(B)]
+        self.max_kv_len = max(self.seq_lens) if self.seq_lens else 0
+        self._is_decode = B > 0 and all(n == 1 for n in self.new_token_counts)
+        self._iw = max(o + n for o, n in zip(self.input_offsets, self.new_token_counts)) if B else 1
+        iw = self._iw
+        slot = np.full((B, iw), -1, np.int32)
+        for b in range(B):
+            o, n, s = self.input_offsets[b], self.new_token_counts[b], self.start_positions[b]
+            if n > 0:
+                slot[b, o:o + n] = self.slots[b] * Smax + np.arange(s, s + n)
+        indptr = np.arange(B + 1, dtype=np.int64)
+        indices = np.asarray(self.slots or [0], np.int32)
+        lpl = np.asarray(self.seq_lens or [0], np.int64)
+        # a zero-length sequence gets no page
+        if B and any(L == 0 for L in self.seq_lens):
+            npg = np.asarray([1 if L > 0 else 0 for L in self.seq_lens])
+            indptr = np.zeros(B + 1, np.int64)
+            np.cumsum(npg, out=indptr[1:])
+            indices = np.asarray([s for s, L in zip(self.slots, self.seq_lens) if L > 0] or [0], np.int32)
+        qn = np.asarray(self.new_token_counts, np.int64)
+        qo = np.zeros(B + 1, np.int64)
+        np.cumsum(qn, out=qo[1:])
+        self._max_q = int(qn.max()) if B else 0
+        self._uniform_rows = all(o == 0 for o in self.input_offsets) and all(n == iw for n in self.new_token_counts)
+        rows = [np.arange(b * iw + self.input_offsets[b], b * iw + self.input_offsets[b] + self.new_token_counts[b])
+                for b in range(B)]
+        q_rows = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+        self._plan = _ForwardPlan(cache.device, B, iw, slot.reshape(-1), _positions(
+            self.start_positions, self.new_token_counts, self.input_offsets, iw).reshape(-1),
+            indptr, indices, lpl, qo, q_rows, np.zeros(0, np.int32), np.zeros(0, np.int32))
+
+    def get_position_ids(self, S: int) -> torch.Tensor:
+        return _get_positions(self._plan, self.batch_size, self._iw, S)
+
+    def get_start_pos(self, idx: int = 0) -> int:
+        return self.start_positions[idx]
+
+    def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
+        cache, plan = self.cache, self._plan
+        kern = cache.kernels
+        B, S = q.shape[0], q.shape[1]
+        k_layer, v_layer = cache.paged_view(layer_idx)
+        kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
+        if self._is_decode and S == 1:
+            out = kern.paged_decode(q[:, 0], k_layer, v_layer, plan.indptr, plan.indices, plan.lpl,
+                                    plan.total_pages, workspace=cache.workspace)
+            return out.reshape(B, 1, -1)
+        Hq, D = q.shape[2], q.shape[3]
+        if self._uniform_rows and S == self._iw:
+            q_rag = q.reshape(B * S, Hq, D)
+        else:
+            q_rag = q.reshape(B * S, Hq, D).index_select(0, plan.q_rows.long())
+        o_rag = kern.paged_prefill(q_rag, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace)
+        if self._uniform_rows and S == self._iw:
+            return o_rag.reshape(B, S, Hq * D)
+        out = q.new_zeros(B * S, Hq * D)
+        out.index_copy_(0, plan.q_rows.long(), o_rag.reshape(-1, Hq * D))
+        return out.view(B, S, Hq * D)
+
+
+class ContiguousKVCache(KVCacheManager):
+    """Pre-allocated [L, Bmax, Smax, Hkv, D] cache, no paging or prefix caching
+    (kv_cache.py:328-379)."""
+
+    def __init__(self, cfg: KVCacheConfig, kernels=None):
+        self.cfg = cfg
+        self.kernels = kernels or _default_kernels()
+        self.device = torch.device(cfg.device) if cfg.device is not None else torch.device("cpu")
+        shape = (cfg.num_layers, cfg.max_batch_size, cfg.max_seq_len, cfg.num_kv_heads, cfg.head_dim)
+        self.k = torch.zeros(shape, dtype=cfg.dtype, device=self.device)
+        self.v = torch.zeros(shape, dtype=cfg.dtype, device=self.device)
+        self.states: Dict[str, _ContigSeqState] = {}
+        self._slot = 0
+        self.workspace = self.kernels.Workspace(self.device, 16 << 20)
+
+    def paged_view(self, layer_idx):
+        return self.k[layer_idx], self.v[layer_idx]
+
+    def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
+        s = self._slot
+        self._slot += 1
+        assert s < self.cfg.max_batch_size, "Exceeded max_batch_size"
+        (ids,) = _upload_i32([np.asarray([s], np.int32)], self.device)
+        self.kernels.zero_pages(self.k, self.v, ids)
+        st = _ContigSeqState(seq_id, s)
+        if token_ids:
+            st.token_ids = list(token_ids)
+        self.states[seq_id] = st
+        return 0
+
+    def extend_sequence(self, seq_id, num_new=1):
+        st = self.states[seq_id]
+        assert st.num_tokens + num_new <= self.cfg.max_seq_len
+
+    def begin_forward(self, seq_ids, ntoks, offsets=None):
+        for sid, n in zip(seq_ids, ntoks):
+            self.extend_sequence(sid, n)
+        return ContiguousCacheContext(self, seq_ids, ntoks, offsets)
+
+    def end_forward(self, ctx):
+        for b in range(ctx.batch_size):
+            self.states[ctx.seq_ids[b]].num_tokens += ctx.new_token_counts[b]
+
+    def release_sequence(self, seq_id):
+        if seq_id in self.states:
+            del self.states[seq_id]
+            if not self.states:
+                self._slot = 0
+
+    def append_token_ids(self, seq_id, ids):
+        if seq_id in self.states:
+            self.states[seq_id].token_ids.extend(ids)
+
+    def reset(self):
+        for s in list(self.states):
+            self.release_sequence(s)
+
+    @property
+    def stats(self):
+        return {"backend": "contiguous",
+                "active_seqs": len(self.states),
+                "slots": f"{self._slot}/{self.cfg.max_batch_size}",
+                "max_seq": self.cfg.max_seq_len}
+
+
+def create_cache_manager(hf_config, parallel_config, device, dtype, model_config,
+                         max_batch_size=4) -> KVCacheManager:
+    """kv_cache.py:780-805: backend from model_config.kv_backend (auto -> paged)."""
+    dev = torch.device(device)
+    if dev.type == "cuda":
+        torch.cuda.synchronize(dev)
+        torch.cuda.empty_cache()
+    backend = getattr(model_config, "kv_backend", "auto")
+    kv_cfg = KVCacheConfig.from_hf_config(
+        hf_config, parallel_config=parallel_config, device=dev,
+        page_size=getattr(model_config, "page_size", 16),
+        max_pages=getattr(model_config, "max_kv_pages", 0),
+        max_batch_size=max_batch_size,
+        max_seq_len=getattr(model_config, "max_seq_len", 4096),
+        memory_fraction=getattr(model_config, "kv_memory_fraction", 0.30),
+        dtype=dtype,
+        enable_prefix_caching=getattr(model_config, "enable_prefix_caching", True),
+        backend=backend,
+    )
+    if kv_cfg.backend == "paged":
+        return PagedKVCache(kv_cfg)
+    return ContiguousKVCache(kv_cfg)
+
+
+# the reference's class names, for callers that import them directly
+FlashInferPagedKVCache = PagedKVCache
+FlashInferCacheContext = PagedCacheContext

@@ -1,0 +1,95 @@
+"""CPU stand-in for nanoslg_amd.kernels, used only to test the host layer
+(bookkeeping, plans, copy-on-write order) without a GPU. It implements the
+same functions with plain torch indexing and the oracle's fp32 attention.
+The product never uses it: nanoslg_amd.kv_cache gets it only when a test
+passes it in explicitly."""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from oracle import kv_oracle
+
+CALLS = []  # (name, summary) log of launches, for tests that count them
+
+
+class Workspace:
+    def __init__(self, device, nbytes=0):
+        self.device = device
+
+    def get(self, nbytes):
+        return None
+
+
+def append_kv(k_new, v_new, slot_mapping, k_pool, v_pool):
+    CALLS.append(("append_kv", int(slot_mapping.numel())))
+    Hkv, D = k_pool.shape[-2], k_pool.shape[-1]
+    kr = k_new.reshape(-1, Hkv, D)
+    vr = v_new.reshape(-1, Hkv, D)
+    kp = k_pool.view(-1, Hkv, D)
+    vp = v_pool.view(-1, Hkv, D)
+    for i, s in enumerate(slot_mapping.tolist()):
+        if 0 <= s < kp.shape[0]:
+            kp[s] = kr[i]
+            vp[s] = vr[i]
+
+
+def zero_pages(k_pool, v_pool, page_ids):
+    CALLS.append(("zero_pages", int(page_ids.numel())))
+    for p in page_ids.tolist():
+        if 0 <= p < k_pool.shape[1]:
+            k_pool[:, p] = 0
+            v_pool[:, p] = 0
+
+
+def copy_pages(k_pool, v_pool, src_ids, dst_ids):
+    CALLS.append(("copy_pages", int(src_ids.numel())))
+    for s, d in zip(src_ids.tolist(), dst_ids.tolist()):
+        k_pool[:, d] = k_pool[:, s]
+        v_pool[:, d] = v_pool[:, s]
+
+
+def gather_kv(k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, max_len):
+    ps = k_layer.shape[1]
+    kr = k_layer.reshape(-1, *k_layer.shape[2:]).numpy()
+    vr = v_layer.reshape(-1, *v_layer.shape[2:]).numpy()
+    k = kv_oracle.gather_rows(kr, ps, kv_indptr.numpy(), kv_indices.numpy(), kv_last_page_len.numpy(), max_len)
+    v = kv_oracle.gather_rows(vr, ps, kv_indptr.numpy(), kv_indices.numpy(), kv_last_page_len.numpy(), max_len)
+    return torch.from_numpy(k), torch.from_numpy(v)
+
+
+def _attend(q_list, qo_lens, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, sm_scale):
+    ps = k_layer.shape[1]
+    kr = k_layer.reshape(-1, *k_layer.shape[2:])
+    vr = v_layer.reshape(-1, *v_layer.shape[2:])
+    return kv_oracle.paged_attention_ref(q_list, kr, vr, ps, kv_indptr.tolist(), kv_indices.tolist(),
+                                         kv_last_page_len.tolist(), qo_lens, sm_scale)
+
+
+def paged_decode(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                 sm_scale=None, out=None, workspace=None):
+    CALLS.append(("paged_decode", int(q.shape[0])))
+    B = q.shape[0]
+    outs = _attend([q[b:b + 1] for b in range(B)], [1] * B, k_layer, v_layer, kv_indptr, kv_indices,
+                   kv_last_page_len, sm_scale)
+    res = torch.stack([o[0] for o in outs]).to(q.dtype)
+    if out is not None:
+        out.copy_(res)
+        return out
+    return res
+
+
+def paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,
+                  sm_scale=None, out=None, workspace=None):
+    CALLS.append(("paged_prefill", int(total_q)))
+    qo = qo_indptr.tolist()
+    B = len(qo) - 1
+    qs = [q[qo[b]:qo[b + 1]] for b in range(B)]
+    outs = _attend(qs, [qo[b + 1] - qo[b] for b in range(B)], k_layer, v_layer, kv_indptr, kv_indices,
+                   kv_last_page_len, sm_scale)
+    res = torch.cat(outs, 0).to(q.dtype) if outs else q.new_zeros(0, q.shape[1], q.shape[2])
+    if out is not None:
+        out[:res.shape[0]].copy_(res)
+        return out
+    return res

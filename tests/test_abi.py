@@ -1,0 +1,69 @@
+"""The C ABI library: it builds, loads, exports every symbol include/nslg_kv.h
+declares, and rejects bad arguments on the host (no device work needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "nslg_kv.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nslg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    syms = declared_symbols()
+    for name in ["nslg_append_kv", "nslg_zero_pages", "nslg_copy_pages", "nslg_gather_kv",
+                 "nslg_paged_decode", "nslg_paged_decode_workspace_size", "nslg_paged_prefill",
+                 "nslg_paged_prefill_workspace_size", "nslg_version", "nslg_last_error"]:
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+    assert lib.nslg_version() >= 100
+
+
+def test_host_side_argument_checks():
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    # bad dtype, negative sizes, null pointers: rejected before any device work
+    assert lib.nslg_append_kv(None, None, 0, 0, None, 4, None, None, 16, 8, 128, 9, None) == -1
+    assert lib.nslg_append_kv(None, None, 0, 0, None, 0, None, None, 16, 8, 128, 0, None) == 0
+    assert lib.nslg_zero_pages(None, None, 1, 4, 16, 8, 128, 0, None, 3, None) == -1
+    assert lib.nslg_copy_pages(None, None, 0, 4, 16, 8, 128, 0, None, None, 1, None) == -1
+    assert "copy_pages" in _lib.last_error()
+    rc = lib.nslg_paged_decode(1, 4096, 1, 1, 100, 16, 1, 1, 1, 10, 2, 32, 8, 100, 0.1, 0, 1, 4096,
+                               None, 0, None)
+    assert rc == -2  # head_dim 100 unsupported
+    rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 32, 8, 128, 0.1, 0, 256, 4096,
+                               None, 0, None)
+    assert rc == -4  # no workspace
+    rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 34, 8, 128, 0.1, 0, 256, 4096,
+                               None, 0, None)
+    assert rc == -1  # Hq not a multiple of Hkv
+
+
+def test_decode_workspace_size_monotone():
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    a = lib.nslg_paged_decode_workspace_size(4, 32, 128, 640, 16)
+    b = lib.nslg_paged_decode_workspace_size(64, 32, 128, 44000, 16)
+    assert 0 < a < b < (64 << 20)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from nanoslg_amd import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    with pytest.raises(_lib.KernelLibraryError):
+        _lib.load()
