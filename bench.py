@@ -1,0 +1,363 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged decode attention + append hot path on one MI355X.
+
+Default workload (kv_pressure): one Llama-3.1-8B attention layer (32 query / 8 KV
+heads, head_dim 128, fp16, page size 16), batch 64, context lengths log-uniform
+in [2048, 32768], pool sized to 90 % occupancy with pages shuffled across
+sequences, 10 % of pages released and re-allocated mid-run. One step = one decode
+step of that layer through the drop-in API (begin_forward -> attend -> end_forward):
+plan upload, K/V append kernel, split-K decode kernel and merge.
+
+Prints ONE JSON line. `value` = algorithmic HBM bytes per step / wall time per
+step (GB/s). `roofline` = the decode kernel alone, timed with HIP events on its
+stream. `cpu_baseline` = the CPU restatement of the reference's contiguous SDPA
+path on a bounded sample of the same workload, on this host's cores.
+
+  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch|radix|prefill]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HQ, HKV, D, PS = 32, 8, 128, 16
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", default="kv_pressure",
+                    choices=["kv_pressure", "small_batch", "radix", "prefill"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    return ap.parse_args()
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------- workloads
+
+
+class DecodeWorkload:
+    """A batch of sequences with random K/V already resident in a paged pool."""
+
+    def __init__(self, name, lens, pool_pages, seed, churn_frac=0.0, shuffle=True):
+        import torch
+        from nanoslg_amd.kv_cache import KVCacheConfig, PagedKVCache
+        self.torch = torch
+        self.name = name
+        self.lens0 = list(lens)
+        self.B = len(lens)
+        self.seed = seed
+        self.churn_frac = churn_frac
+        self.rng = np.random.default_rng(seed)
+        cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
+                            max_pages=pool_pages, dtype=torch.float16, device=torch.device("cuda:0"),
+                            enable_prefix_caching=False, backend="paged")
+        self.mgr = PagedKVCache(cfg)
+        pool = self.mgr.pool
+        if shuffle:
+            free = np.array(pool._free, np.int64)
+            self.rng.shuffle(free)
+            pool._free = free.tolist()
+        self.ids = [f"s{b}" for b in range(self.B)]
+        for sid, L in zip(self.ids, lens):
+            self._admit(sid, L)
+        # prefill content: every page (allocated ones were zeroed on allocation) ~ N(0,1)
+        g = torch.Generator(device="cuda:0").manual_seed(seed)
+        pool.k.normal_(generator=g)
+        pool.v.normal_(generator=g)
+        # per-step inputs: a ring of seeded N(0,1) q/k/v, [B, 1, H, D]
+        ring = 8
+        self.q = torch.randn(ring, self.B, 1, HQ, D, generator=g, device="cuda:0", dtype=torch.float16)
+        self.kn = torch.randn(ring, self.B, 1, HKV, D, generator=g, device="cuda:0", dtype=torch.float16)
+        self.vn = torch.randn(ring, self.B, 1, HKV, D, generator=g, device="cuda:0", dtype=torch.float16)
+        self.step_idx = 0
+        self.last_ctx = None
+
+    def _admit(self, sid, L):
+        """Allocate a sequence of L tokens whose pages already hold N(0,1) K/V."""
+        mgr = self.mgr
+        mgr.allocate_sequence(sid, num_tokens=L)
+        st = mgr.seqs[sid]
+        st.num_tokens = L
+        pages = st.bt[:st.n_pages]
+        for i, p in enumerate(pages.tolist()):
+            mgr.pool.tokens_used[p] = PS if i < len(pages) - 1 else L - PS * (len(pages) - 1)
+
+    def churn(self):
+        """Release whole sequences until >= churn_frac of the used pages are free, then
+        re-admit them at the same lengths on freshly shuffled pages with fresh K/V."""
+        torch = self.torch
+        mgr = self.mgr
+        used = sum(mgr.seqs[s].n_pages for s in self.ids)
+        order = self.rng.permutation(self.B)
+        freed, victims = 0, []
+        for b in order:
+            if freed >= self.churn_frac * used:
+                break
+            sid = self.ids[b]
+            victims.append((sid, mgr.seqs[sid].num_tokens))
+            freed += mgr.seqs[sid].n_pages
+            mgr.release_sequence(sid)
+        free = np.array(mgr.pool._free, np.int64)
+        self.rng.shuffle(free)
+        mgr.pool._free = free.tolist()
+        for sid, L in victims:
+            self._admit(sid, L)
+            pages = torch.from_numpy(mgr.seqs[sid].bt[:mgr.seqs[sid].n_pages].astype(np.int64)).cuda()
+            mgr.pool.k[0].index_copy_(0, pages, torch.randn(len(pages), PS, HKV, D, device="cuda:0",
+                                                            dtype=torch.float16))
+            mgr.pool.v[0].index_copy_(0, pages, torch.randn(len(pages), PS, HKV, D, device="cuda:0",
+                                                            dtype=torch.float16))
+        return freed
+
+    def seq_lens(self):
+        return [self.mgr.seqs[s].num_tokens for s in self.ids]
+
+    def step(self):
+        i = self.step_idx % self.q.shape[0]
+        self.step_idx += 1
+        ctx = self.mgr.begin_forward(self.ids, [1] * self.B)
+        out = ctx.attend(0, self.q[i], self.kn[i], self.vn[i], HQ, HKV)
+        self.mgr.end_forward(ctx)
+        self.last_ctx = ctx
+        return out
+
+
+def step_bytes(lens_after, B, total_pages):
+    """Algorithmic HBM bytes of one decode+append step (fp16, one layer)."""
+    kv = sum(lens_after) * HKV * D * 2 * 2
+    append = B * HKV * D * 2 * 2 * 2
+    qo = B * HQ * D * 2 * 2
+    csr = 4 * (total_pages + 2 * B + 1)
+    return kv, append, qo, csr
+
+
+def kv_pressure_lens(seed, B=64):
+    rng = np.random.default_rng(seed)
+    return [int(round(math.exp(x))) for x in rng.uniform(math.log(2048), math.log(32768), size=B)]
+
+
+# --------------------------------------------------------------------------- measurement
+
+
+def time_decode_kernel(w: DecodeWorkload, reps: int):
+    """Average duration of one paged_decode call (split-K kernel + merge) on the last
+    step's plan, with HIP events recorded on the launch stream."""
+    torch = w.torch
+    from nanoslg_amd import kernels
+    ctx = w.last_ctx
+    plan = ctx.plan
+    pool = w.mgr.pool
+    q = w.q[0][:, 0]
+    out = torch.empty(w.B, HQ, D, dtype=torch.float16, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        kernels.paged_decode(q, pool.k[0], pool.v[0], plan.indptr, plan.indices, plan.lpl, plan.total_pages,
+                             out=out, workspace=w.mgr.workspace)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        kernels.paged_decode(q, pool.k[0], pool.v[0], plan.indptr, plan.indices, plan.lpl, plan.total_pages,
+                             out=out, workspace=w.mgr.workspace)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in evs]
+    lens = [int(x) for x in ctx.seq_lens]
+    kv = sum(lens) * HKV * D * 2 * 2
+    qo = w.B * HQ * D * 2 * 2
+    csr = 4 * (plan.total_pages + 2 * w.B + 1)
+    return float(np.median(ms)), float(np.mean(ms)), kv + qo + csr
+
+
+def stream_read_ceiling():
+    """Measured HBM read rate of a plain reduction over 4 GiB (context for the roofline)."""
+    import torch
+    x = torch.empty(2 << 30, dtype=torch.float16, device="cuda:0").fill_(1.0)
+    torch.cuda.synchronize()
+    x.sum()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(5):
+        x.sum()
+    e.record()
+    torch.cuda.synchronize()
+    gbs = 5 * x.numel() * 2 / (s.elapsed_time(e) * 1e-3) / 1e9
+    del x
+    torch.cuda.empty_cache()
+    return gbs
+
+
+def cpu_baseline_sample(lens, seed, budget_s=12.0, max_steps=32):
+    """The reference's contiguous SDPA decode path restated on the CPU (fp32): a bounded
+    sample of the workload — its first 4 sequences, stepped until `budget_s` seconds."""
+    import torch
+    from oracle import kv_oracle as O
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    torch.set_num_threads(threads)
+    sample = list(lens[:4])
+    B = len(sample)
+    g = torch.Generator().manual_seed(seed)
+    Smax = max(sample) + max_steps + 4
+    cache = O.ContiguousRef(1, B, Smax, HKV, D, torch.float32)
+    ids = [f"c{b}" for b in range(B)]
+    for b, (sid, L) in enumerate(zip(ids, sample)):
+        cache.allocate_sequence(sid)
+        cache.k[0, b, :L] = torch.randn(L, HKV, D, generator=g)
+        cache.v[0, b, :L] = torch.randn(L, HKV, D, generator=g)
+        cache.states[sid]["num_tokens"] = L
+    q = torch.randn(B, 1, HQ, D, generator=g) / math.sqrt(D)
+    kn = torch.randn(B, 1, HKV, D, generator=g)
+    vn = torch.randn(B, 1, HKV, D, generator=g)
+    # warm up once
+    ctx = cache.begin_forward(ids, [1] * B)
+    ctx.attend(0, q, kn, vn, HQ, HKV)
+    cache.end_forward(ctx)
+    steps, nbytes = 0, 0
+    t0 = time.perf_counter()
+    while steps < max_steps and time.perf_counter() - t0 < budget_s:
+        ctx = cache.begin_forward(ids, [1] * B)
+        ctx.attend(0, q, kn, vn, HQ, HKV)
+        cache.end_forward(ctx)
+        lens_after = ctx.seq_lens
+        nbytes += sum(lens_after) * HKV * D * 4 * 2 + B * HKV * D * 4 * 4 + B * HQ * D * 4 * 2
+        steps += 1
+    dt = time.perf_counter() - t0
+    try:
+        model = open("/proc/cpuinfo").read().split("model name")[1].split(":")[1].split("\n")[0].strip()
+    except Exception:
+        model = "unknown"
+    return {
+        "value": round(nbytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "tok_s_layer": round(B * steps / dt, 2),
+        "ms_per_step": round(dt / steps * 1e3, 3),
+        "cores": threads,
+        "kind": "port",
+        "cpu": model,
+        "sample": (f"contiguous SDPA path (write, slice read, transpose copy, masked SDPA) in fp32, "
+                   f"sequences 0-3 of the workload (lengths {sample}), {steps} decode steps"),
+    }
+
+
+# --------------------------------------------------------------------------- main
+
+
+def run_decode(args):
+    import torch
+    if args.workload == "kv_pressure":
+        lens = kv_pressure_lens(args.seed)
+        total_steps = args.warmup + args.steps
+        npages = sum(math.ceil(L / PS) for L in lens)
+        pool_pages = int(math.ceil(npages / 0.9)) + 1
+        # room for the steps' growth inside the 10 % headroom
+        grow = len(lens) * (math.ceil(total_steps / PS) + 1)
+        assert pool_pages - 1 - npages >= grow, "pool headroom too small for the run"
+        w = DecodeWorkload("kv_pressure", lens, pool_pages, args.seed, churn_frac=0.10)
+        cfg = {"workload": "kv_pressure_decode_append", "batch": 64, "ctx": "log-uniform[2048,32768]",
+               "pool_occupancy": 0.9, "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D,
+               "layers": 1, "churn": "10% of pages at mid-run", "seed": args.seed}
+    else:  # small_batch
+        rng = np.random.default_rng(args.seed)
+        lens = [int(x) for x in rng.integers(1024, 4097, size=4)]
+        w = DecodeWorkload("small_batch", lens, 65536, args.seed)
+        cfg = {"workload": "small_batch_decode_append", "batch": 4, "ctx": "uniform[1024,4096]",
+               "pool_pages": 65536, "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D,
+               "layers": 1, "seed": args.seed}
+    _log(f"workload {w.name}: B={w.B} pages={w.mgr.cfg.max_pages} sum(L)={sum(lens)}")
+    for _ in range(args.warmup):
+        w.step()
+    torch.cuda.synchronize()
+    lens_before = w.seq_lens()
+    churn_at = args.steps // 2 if w.churn_frac > 0 else -1
+    nbytes = [0, 0, 0, 0]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        if i == churn_at:
+            w.churn()
+        lens_i = [L + 1 for L in w.seq_lens()]
+        tp = sum(math.ceil(L / PS) for L in lens_i)
+        for j, x in enumerate(step_bytes(lens_i, w.B, tp)):
+            nbytes[j] += x
+        w.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall / args.steps * 1e3
+    total_bytes = sum(nbytes)
+    value = total_bytes / wall / 1e9
+    _log(f"{args.steps} steps in {wall*1e3:.1f} ms -> {ms_step:.3f} ms/step, {value:.1f} GB/s")
+
+    med_ms, mean_ms, kbytes = time_decode_kernel(w, args.kernel_reps)
+    achieved = kbytes / (mean_ms * 1e-3) / 1e9
+    _log(f"decode kernel: mean {mean_ms*1e3:.1f} us, median {med_ms*1e3:.1f} us, {achieved:.1f} GB/s")
+    ceiling = stream_read_ceiling()
+    res = {
+        "metric": "paged decode attn+append: achieved HBM GB/s (% of peak) and decode tok/s/layer",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic: K/V/Q ~ N(0,1), seeded",
+        "config": cfg,
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "decode_tok_s_layer": round(w.B * args.steps / wall, 1),
+        "bytes_per_step": {k: int(v / args.steps) for k, v in zip(["kv_read", "append", "q_out", "csr"], nbytes)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "nslg_paged_decode (split-K decode kernel + LSE merge kernel)",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(mean_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": int(kbytes),
+        },
+        "measured_stream_read_GBs": round(ceiling, 1),
+    }
+    return res, lens
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    if args.workload in ("kv_pressure", "small_batch"):
+        res, lens = run_decode(args)
+    else:
+        print(f"workload {args.workload} is not implemented yet", file=sys.stderr)
+        sys.exit(2)
+    if not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline_sample(lens, args.seed)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -30,6 +30,8 @@ HIPCC_FLAGS = [
     # Packed fp32 VALU ops stay disabled in all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    # keep MFMA accumulators in ordinary VGPRs (no per-tile AGPR copies)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

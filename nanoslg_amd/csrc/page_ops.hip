@@ -29,39 +29,44 @@ append_rows_kernel(const char* __restrict__ k_src, const char* __restrict__ v_sr
   for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
 }
 
-// One workgroup per (page, layer, K|V): page_bytes contiguous bytes.
+// Flat grid over (page list entry, 16-byte word of the page) for one layer
+// (blockIdx.y) and one of K|V (blockIdx.z): each thread moves one word, so even
+// a handful of pages spreads over many workgroups.
 template <typename V>
 __global__ void __launch_bounds__(256)
 zero_pages_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_pages,
-                  int64_t page_bytes, const int32_t* __restrict__ ids, int32_t num_layers) {
-  const int i = blockIdx.x;
-  const int layer = blockIdx.y;
+                  int64_t page_bytes, const int32_t* __restrict__ ids, int32_t n) {
+  const int64_t nvec = page_bytes / (int64_t)sizeof(V);
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= nvec * n) return;
+  const int i = (int)(idx / nvec);
+  const int64_t w = idx - (int64_t)i * nvec;
   const int32_t pid = ids[i];
   if (pid < 0 || (int64_t)pid >= num_pages) return;
-  char* base = (blockIdx.z ? v_pool : k_pool) + ((int64_t)layer * num_pages + pid) * page_bytes;
-  V* dst = reinterpret_cast<V*>(base);
-  const int64_t nvec = page_bytes / (int64_t)sizeof(V);
+  char* base = (blockIdx.z ? v_pool : k_pool) + ((int64_t)blockIdx.y * num_pages + pid) * page_bytes;
   V z;
   __builtin_memset(&z, 0, sizeof(V));
-  for (int64_t j = threadIdx.x; j < nvec; j += blockDim.x) dst[j] = z;
-  (void)num_layers;
+  reinterpret_cast<V*>(base)[w] = z;
 }
 
 template <typename V>
 __global__ void __launch_bounds__(256)
 copy_pages_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_pages,
                   int64_t page_bytes, const int32_t* __restrict__ src_ids,
-                  const int32_t* __restrict__ dst_ids) {
-  const int i = blockIdx.x;
-  const int layer = blockIdx.y;
+                  const int32_t* __restrict__ dst_ids, int32_t n) {
+  const int64_t nvec = page_bytes / (int64_t)sizeof(V);
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= nvec * n) return;
+  const int i = (int)(idx / nvec);
+  const int64_t w = idx - (int64_t)i * nvec;
   const int32_t s = src_ids[i];
   const int32_t d = dst_ids[i];
   if (s < 0 || (int64_t)s >= num_pages || d < 0 || (int64_t)d >= num_pages) return;
   char* pool = blockIdx.z ? v_pool : k_pool;
-  const V* src = reinterpret_cast<const V*>(pool + ((int64_t)layer * num_pages + s) * page_bytes);
-  V* dst = reinterpret_cast<V*>(pool + ((int64_t)layer * num_pages + d) * page_bytes);
-  const int64_t nvec = page_bytes / (int64_t)sizeof(V);
-  for (int64_t j = threadIdx.x; j < nvec; j += blockDim.x) dst[j] = src[j];
+  const int64_t layer_off = (int64_t)blockIdx.y * num_pages;
+  const V* src = reinterpret_cast<const V*>(pool + (layer_off + s) * page_bytes);
+  V* dst = reinterpret_cast<V*>(pool + (layer_off + d) * page_bytes);
+  dst[w] = src[w];
 }
 
 // grid (max_len, batch, 2): row t of sequence b, K or V.
@@ -180,15 +185,17 @@ extern "C" int nslg_zero_pages(void* k_pool, void* v_pool, int32_t num_layers, i
   if (n == 0) return NSLG_OK;
   if (!k_pool || !v_pool || !page_ids) return fail(NSLG_EINVAL, "zero_pages: null pointer");
   const int w = pick_vec({pb, (int64_t)(uintptr_t)k_pool, (int64_t)(uintptr_t)v_pool});
-  dim3 grid(n, num_layers, 2);
+  const int64_t blocks = ((pb / w) * n + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(NSLG_EINVAL, "zero_pages: too many pages in one call");
+  dim3 grid((unsigned)blocks, num_layers, 2);
   hipStream_t s = as_stream(stream);
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
   switch (w) {
-    case 16: zero_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, num_layers); break;
-    case 8: zero_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, num_layers); break;
-    case 4: zero_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, num_layers); break;
-    default: zero_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, num_layers); break;
+    case 16: zero_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
+    case 8: zero_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
+    case 4: zero_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
+    default: zero_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
   }
   return check_launch("zero_pages");
 }
@@ -205,15 +212,17 @@ extern "C" int nslg_copy_pages(void* k_pool, void* v_pool, int32_t num_layers, i
   if (n == 0) return NSLG_OK;
   if (!k_pool || !v_pool || !src_ids || !dst_ids) return fail(NSLG_EINVAL, "copy_pages: null pointer");
   const int w = pick_vec({pb, (int64_t)(uintptr_t)k_pool, (int64_t)(uintptr_t)v_pool});
-  dim3 grid(n, num_layers, 2);
+  const int64_t blocks = ((pb / w) * n + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(NSLG_EINVAL, "copy_pages: too many pages in one call");
+  dim3 grid((unsigned)blocks, num_layers, 2);
   hipStream_t s = as_stream(stream);
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
   switch (w) {
-    case 16: copy_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids); break;
-    case 8: copy_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids); break;
-    case 4: copy_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids); break;
-    default: copy_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids); break;
+    case 16: copy_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
+    case 8: copy_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
+    case 4: copy_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
+    default: copy_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
   }
   return check_launch("copy_pages");
 }

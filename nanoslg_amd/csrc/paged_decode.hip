@@ -114,7 +114,7 @@ struct Tile {
   typename RowVec<kNT>::type v[4];
 };
 
-// Address of token `tok` (clamped into [0, len)) for kv head h.
+// Address of token `tok` (clamped into [0, len)) for kv head h (any page size).
 __device__ inline const uint16_t* token_row(const uint16_t* pool, const int32_t* idx, int64_t num_pages,
                                             int page_size, int64_t row_elems, int head_off, int tok) {
   int32_t pid = idx[tok / page_size];
@@ -122,59 +122,68 @@ __device__ inline const uint16_t* token_row(const uint16_t* pool, const int32_t*
   return pool + ((int64_t)pid * page_size + (tok % page_size)) * row_elems + head_off;
 }
 
-template <int D, bool kTileInPage>
-__device__ inline void load_tile(const DecodeParams& p, const int32_t* idx, int head_off,
-                                 int t0, int t_last, Tile<D>& t) {
+// Loads of one tile whose 16 token rows are consecutive in one page, for the
+// lane's MFMA operand positions. kbase/vbase: wave-uniform byte address of the
+// tile's first row (head offset included); rows past `last` repeat row `last`.
+//   K: lane l reads row l%16, 16 B at d = 32 s + 8 (l/16)
+//   V: lane l reads rows 4 (l/16) + j, D/16 elements at d = (D/16) (l%16)
+template <int D>
+__device__ inline void load_tile_rows(const char* kbase, const char* vbase, int row_bytes, int last,
+                                      Tile<D>& t) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int gq = lane >> 4;
+  constexpr int NT = D / 16;
+  typedef typename RowVec<NT>::type VT;
+  const char* kp = kbase + (r < last ? r : last) * row_bytes + 16 * gq;
+#pragma unroll
+  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = *reinterpret_cast<const u16x8*>(kp + 64 * s);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int vr = 4 * gq + j;
+    t.v[j] = *reinterpret_cast<const VT*>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
+  }
+}
+
+// Same operand positions, each lane resolving its own token's page (page sizes that
+// are not a multiple of 16, where a tile can straddle pages).
+template <int D>
+__device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, int head_off, int t0,
+                                     int t_last, Tile<D>& t) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int gq = lane >> 4;
   const int64_t row_elems = (int64_t)p.num_kv_heads * D;
   constexpr int NT = D / 16;
   typedef typename RowVec<NT>::type VT;
-  if constexpr (kTileInPage) {
-    // The 16 tokens of the tile share one page; slot0 is its first slot.
-    int32_t pid = idx[t0 / p.page_size];
-    if (pid < 0 || (int64_t)pid >= p.num_pages) pid = 0;
-    const int slot0 = t0 % p.page_size;
-    const int64_t page_base = (int64_t)pid * p.page_size;
-    int tk = t0 + r;
-    tk = tk > t_last ? t_last : tk;
-    const uint16_t* krow = p.k_pool + (page_base + slot0 + (tk - t0)) * row_elems + head_off;
+  int tk = t0 + r;
+  tk = tk > t_last ? t_last : tk;
+  const uint16_t* krow = token_row(p.k_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tk);
 #pragma unroll
-    for (int s = 0; s < Tile<D>::kSteps; ++s)
-      t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
+  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int tv = t0 + 4 * gq + j;
-      tv = tv > t_last ? t_last : tv;
-      const uint16_t* vrow = p.v_pool + (page_base + slot0 + (tv - t0)) * row_elems + head_off;
-      t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
-    }
-  } else {
-    int tk = t0 + r;
-    tk = tk > t_last ? t_last : tk;
-    const uint16_t* krow = token_row(p.k_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tk);
-#pragma unroll
-    for (int s = 0; s < Tile<D>::kSteps; ++s)
-      t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int tv = t0 + 4 * gq + j;
-      tv = tv > t_last ? t_last : tv;
-      const uint16_t* vrow = token_row(p.v_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tv);
-      t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
-    }
+  for (int j = 0; j < 4; ++j) {
+    int tv = t0 + 4 * gq + j;
+    tv = tv > t_last ? t_last : tv;
+    const uint16_t* vrow = token_row(p.v_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tv);
+    t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
   }
 }
 
-template <typename T, int D, bool kTileInPage>
+// Running-max rescale threshold (log2 units): the accumulators are rescaled only
+// when a tile's max exceeds the running max by more than this, so probabilities
+// stay <= 2^8 and most tiles never touch the accumulators. Exact: O and l are
+// always relative to the same m.
+constexpr float kRescaleSlack = 8.0f;
+
+template <typename T, int D, bool kTileInPage, int kDepth>
 __global__ void __launch_bounds__(64 * kMaxWaves)
 paged_decode_kernel(DecodeParams p) {
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;  // P = hi + lo for bf16's 8-bit mantissa
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = blockIdx.y * (blockDim.x >> 6) + wave;
   if (h >= p.num_kv_heads) return;
 
@@ -182,10 +191,12 @@ paged_decode_kernel(DecodeParams p) {
   if (!locate_chunk(p.indptr, p.last_len, p.batch, p.page_size, p.chunk_tokens, blockIdx.x, b,
                     cstart, nchunks))
     return;
+  b = __builtin_amdgcn_readfirstlane(b);
+  cstart = __builtin_amdgcn_readfirstlane(cstart);
+  nchunks = __builtin_amdgcn_readfirstlane(nchunks);
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
   const int t_begin = (blockIdx.x - cstart) * p.chunk_tokens;
-  int t_end = t_begin + p.chunk_tokens;
-  t_end = t_end > len ? len : t_end;
+  const int t_end = min(t_begin + p.chunk_tokens, len);
   const int t_last = t_end - 1;
   const int32_t* idx = p.indices + p.indptr[b];
 
@@ -205,39 +216,34 @@ paged_decode_kernel(DecodeParams p) {
     for (int s = 0; s < kSteps; ++s) qb[s] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  const int head_off = h * D;
   float m_run = -INFINITY;
   float l_run = 0.f;
   f32x4 o[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Tile<D> cur, nxt;
-  load_tile<D, kTileInPage>(p, idx, head_off, t_begin, t_last, cur);
-  for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-    const bool has_next = t0 + 16 < t_end;
-    if (has_next) load_tile<D, kTileInPage>(p, idx, head_off, t0 + 16, t_last, nxt);
-
+  auto process = [&](const Tile<D>& cur, int t0) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(cur.k[ks], qb[ks], s);
-
     float sv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sv[j] = (t0 + 4 * gq + j < t_end) ? s[j] * p.scale_log2 : -INFINITY;
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = wave_xor_max(mx, 16);
     mx = wave_xor_max(mx, 32);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
+    if (__ballot(mx > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) o[n] *= alpha;
+      m_run = m_new;
+    }
     float pj[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pj[j] = fast_exp2(sv[j] - m_new);
-    l_run = l_run * alpha + ((pj[0] + pj[1]) + (pj[2] + pj[3]));
-    m_run = m_new;
-#pragma unroll
-    for (int n = 0; n < NT; ++n) o[n] *= alpha;
-
+    for (int j = 0; j < 4; ++j) pj[j] = fast_exp2(sv[j] - m_run);
+    l_run += (pj[0] + pj[1]) + (pj[2] + pj[3]);
     u16x4 pb;
 #pragma unroll
     for (int j = 0; j < 4; ++j) pb[j] = T::from_f32(pj[j]);
@@ -252,7 +258,76 @@ paged_decode_kernel(DecodeParams p) {
       o[n] = T::mma_k16(a, pb, o[n]);
       if constexpr (kSplitP) o[n] = T::mma_k16(a, pb_lo, o[n]);
     }
-    if (has_next) cur = nxt;
+  };
+
+  // Software pipeline over the chunk's 16-token tiles: tile i+kDepth-1 is loaded
+  // while tile i is computed. Loads are issued unconditionally (past the end the
+  // last tile is issued again, an L2 hit) so the compiler's wait counts stay exact
+  // and no wait drains the prefetched tiles.
+  const int n_tiles = (t_end - t_begin + 15) >> 4;
+  Tile<D> buf[kDepth];
+  if constexpr (kTileInPage) {
+    // Every tile lies inside one page. The chunk touches at most 64 pages (the host
+    // caps chunk_tokens), whose ids sit one per lane; each tile's id is broadcast
+    // to a scalar register, so page lookups never wait on the K/V loads in flight.
+    const int ps = p.page_size;
+    const int row_bytes = p.num_kv_heads * D * 2;
+    const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
+    const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
+    const int first_page = t_begin / ps;
+    const int np_seq = p.indptr[b + 1] - p.indptr[b];
+    int pid_vec = 0;
+    if (first_page + lane < np_seq) {
+      pid_vec = idx[first_page + lane];
+      if (pid_vec < 0 || (int64_t)pid_vec >= p.num_pages) pid_vec = 0;
+    }
+    int ld_tile = 0;
+    int page_ld = 0;
+    int slot_ld = t_begin - first_page * ps;
+    const char* kb = kpool;
+    const char* vb = vpool;
+    int last = 0;
+    auto issue = [&](Tile<D>& dst) {
+      if (ld_tile < n_tiles) {
+        const int pid = __builtin_amdgcn_readlane(pid_vec, page_ld);
+        const int64_t row0 = (int64_t)pid * ps + slot_ld;
+        kb = kpool + row0 * row_bytes;
+        vb = vpool + row0 * row_bytes;
+        last = min(15, t_last - (t_begin + 16 * ld_tile));
+        slot_ld += 16;
+        if (slot_ld == ps) {
+          slot_ld = 0;
+          ++page_ld;
+        }
+        ++ld_tile;
+      }
+      load_tile_rows<D>(kb, vb, row_bytes, last, dst);
+    };
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j) issue(buf[j]);
+    for (int i = 0; i < n_tiles; i += kDepth) {
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j) {
+        if (i + j >= n_tiles) break;
+        issue(buf[(j + kDepth - 1) % kDepth]);
+        process(buf[j], t_begin + 16 * (i + j));
+      }
+    }
+  } else {
+    const int head_off = h * D;
+    auto issue_any = [&](int tile, Tile<D>& dst) {
+      load_tile_any<D>(p, idx, head_off, t_begin + 16 * min(tile, n_tiles - 1), t_last, dst);
+    };
+#pragma unroll
+    for (int j = 0; j < kDepth - 1; ++j) issue_any(j, buf[j]);
+    for (int i = 0; i < n_tiles; i += kDepth) {
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j) {
+        if (i + j >= n_tiles) break;
+        issue_any(i + j + kDepth - 1, buf[(j + kDepth - 1) % kDepth]);
+        process(buf[j], t_begin + 16 * (i + j));
+      }
+    }
   }
 
   float l_tot = wave_xor_sum(l_run, 16);
@@ -302,22 +377,26 @@ struct MergeParams {
   int64_t out_stride;
 };
 
-// One workgroup per sequence; sequences with several chunks are merged, empty
-// sequences get zero rows, single-chunk ones were finished by the decode kernel.
-// Thread -> (head, 4 consecutive d).
+// Merge of the split-K partials: one wave per (sequence, query head), lane ->
+// D/64 consecutive d. Sequences with several chunks are merged; empty sequences
+// get zero rows; single-chunk sequences were finished by the decode kernel.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
+  constexpr int PER = D / 64;
+  typedef typename RowVec<PER>::type OutVec;
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63;
+  const int hq = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (hq >= p.num_qo_heads) return;
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
   int nchunks = (len + p.chunk_tokens - 1) / p.chunk_tokens;
-  constexpr int DV = D / 4;
-  const int total = p.num_qo_heads * DV;
+  uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + lane * PER;
   if (nchunks == 0) {
     // A sequence with no tokens attends to nothing: its output rows are zero.
-    for (int it = threadIdx.x; it < total; it += blockDim.x)
-      *reinterpret_cast<u16x4*>(p.out + (int64_t)b * p.out_stride + (int64_t)(it / DV) * D +
-                                4 * (it % DV)) = u16x4{0, 0, 0, 0};
+    OutVec z;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) z[j] = 0;
+    *reinterpret_cast<OutVec*>(orow) = z;
     return;
   }
   if (nchunks == 1) return;
@@ -332,36 +411,43 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
   if (cstart >= p.max_chunks) return;
   if (cstart + nchunks > p.max_chunks) nchunks = p.max_chunks - cstart;
 
-  for (int it = threadIdx.x; it < total; it += blockDim.x) {
-    const int hq = it / DV;
-    const int d4 = it % DV;
-    float mmax = -INFINITY;
-    for (int c = 0; c < nchunks; ++c)
-      mmax = fmaxf(mmax, p.part_ml[((int64_t)(cstart + c) * p.num_qo_heads + hq) * 2]);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
-      const int64_t slot = (int64_t)(cstart + c) * p.num_qo_heads + hq;
-      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + slot * 2);
-      const float w = fast_exp2(ml.x - mmax);
-      const f32x4 oc = *reinterpret_cast<const f32x4*>(p.part_o + slot * D + 4 * d4);
-      acc += w * oc;
-      lsum += w * ml.y;
-    }
-    const float inv = 1.f / lsum;
-    u16x4 w16;
+  const float* ml = p.part_ml + ((int64_t)cstart * p.num_qo_heads + hq) * 2;
+  const int64_t ml_stride = (int64_t)p.num_qo_heads * 2;
+  float mmax = -INFINITY;
+  for (int c = lane; c < nchunks; c += 64) mmax = fmaxf(mmax, ml[c * ml_stride]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(acc[j] * inv);
-    *reinterpret_cast<u16x4*>(p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + 4 * d4) = w16;
+  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off, 64));
+  float lsum = 0.f;
+  for (int c = lane; c < nchunks; c += 64) lsum += fast_exp2(ml[c * ml_stride] - mmax) * ml[c * ml_stride + 1];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
+
+  const float* po = p.part_o + ((int64_t)cstart * p.num_qo_heads + hq) * D + lane * PER;
+  const int64_t po_stride = (int64_t)p.num_qo_heads * D;
+  float acc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+#pragma unroll 4
+  for (int c = 0; c < nchunks; ++c) {
+    const float w = fast_exp2(ml[c * ml_stride] - mmax);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) acc[j] += w * po[c * po_stride + j];
   }
+  const float inv = 1.f / lsum;
+  OutVec w16;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) w16[j] = T::from_f32(acc[j] * inv);
+  *reinterpret_cast<OutVec*>(orow) = w16;
 }
 
 // Tokens per split: about 1024 splits over the whole batch, at least 64 tokens,
-// a multiple of 16.
-inline int choose_chunk_tokens(int64_t total_tokens) {
+// a multiple of 16, and (page sizes that are multiples of 16) at most 63 pages.
+inline int choose_chunk_tokens(int64_t total_tokens, int page_size) {
   int64_t c = (total_tokens + 1023) / 1024;
   c = ((c + 15) / 16) * 16;
   if (c < 64) c = 64;
+  // page-aligned tiles: a chunk may touch at most 64 pages (one page id per lane)
+  if (page_size % 16 == 0 && c > 63LL * page_size) c = 63LL * page_size;
   if (c > (1 << 20)) c = 1 << 20;
   return (int)c;
 }
@@ -375,12 +461,12 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, hipStream_t s) {
   const int waves = p.num_kv_heads < kMaxWaves ? p.num_kv_heads : kMaxWaves;
   dim3 grid(p.max_chunks, (p.num_kv_heads + waves - 1) / waves);
   if (p.page_size % 16 == 0)
-    paged_decode_kernel<T, D, true><<<grid, 64 * waves, 0, s>>>(p);
+    paged_decode_kernel<T, D, true, 2><<<grid, 64 * waves, 0, s>>>(p);
   else
-    paged_decode_kernel<T, D, false><<<grid, 64 * waves, 0, s>>>(p);
+    paged_decode_kernel<T, D, false, 2><<<grid, 64 * waves, 0, s>>>(p);
   int rc = check_launch("paged_decode");
   if (rc) return rc;
-  decode_merge_kernel<T, D><<<p.batch, 256, 0, s>>>(mp);
+  decode_merge_kernel<T, D><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp);
   return check_launch("paged_decode_merge");
 }
 
@@ -394,7 +480,7 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
                                                    int32_t page_size) {
   if (batch <= 0 || num_qo_heads <= 0 || head_dim <= 0 || total_pages < 0 || page_size <= 0) return 0;
   const int64_t total_tokens = total_pages * page_size;
-  const int ct = choose_chunk_tokens(total_tokens);
+  const int ct = choose_chunk_tokens(total_tokens, page_size);
   const int64_t mc = max_chunks_for(batch, total_tokens, ct);
   return (size_t)(mc * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
 }
@@ -428,7 +514,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
     return fail(NSLG_EINVAL, "paged_decode: q/pool/out must be 16-byte aligned");
   const int64_t total_tokens = total_pages * page_size;
   if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
-  const int ct = choose_chunk_tokens(total_tokens);
+  const int ct = choose_chunk_tokens(total_tokens, page_size);
   const int64_t mc = max_chunks_for(batch, total_tokens, ct);
   const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, head_dim, total_pages, page_size);
   if (!workspace || workspace_bytes < need)

@@ -215,25 +215,37 @@ def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Ten
     return out
 
 
-def _positions(start_positions, new_token_counts, input_offsets, iw) -> np.ndarray:
-    """[B, iw] positions: pos[b, off+t] = start_b + t, zeros elsewhere (kv_cache.py:267-278)."""
+def _ragged_layout(start_positions, new_token_counts, input_offsets, iw):
+    """Vectorised input-grid layout of one forward.
+
+    Returns (positions [B*iw] int32, rows [T] int64, qo_indptr [B+1] int64): positions
+    pos[b, off_b+t] = start_b + t and zero elsewhere (kv_cache.py:267-278); rows are the
+    flat [B*iw] indices of the new tokens in ragged (sequence-major) order."""
     B = len(start_positions)
-    pos = np.zeros((B, iw), np.int32)
-    for b in range(B):
-        o, n = input_offsets[b], new_token_counts[b]
-        if n > 0:
-            pos[b, o:o + n] = np.arange(start_positions[b], start_positions[b] + n, dtype=np.int32)
-    return pos
+    n = np.asarray(new_token_counts, np.int64).reshape(B)
+    start = np.asarray(start_positions, np.int64).reshape(B)
+    offs = np.asarray(input_offsets, np.int64).reshape(B)
+    qo = np.zeros(B + 1, np.int64)
+    np.cumsum(n, out=qo[1:])
+    T = int(qo[-1])
+    b_idx = np.repeat(np.arange(B, dtype=np.int64), n)
+    t_in = np.arange(T, dtype=np.int64) - np.repeat(qo[:-1], n)
+    rows = b_idx * iw + offs[b_idx] + t_in
+    pos = np.zeros(B * iw, np.int32)
+    pos[rows] = start[b_idx] + t_in
+    return pos, rows, qo
 
 
 class _ForwardPlan:
     """Device-side metadata of one forward, shared by every layer's attend()."""
 
     def __init__(self, device, batch, iw, slot_grid, positions, indptr, indices, lpl, qo_indptr,
-                 q_rows, cow_src, cow_dst):
+                 q_rows, cow_src, cow_dst, zero_ids=None):
+        zero_ids = np.zeros(0, np.int32) if zero_ids is None else np.asarray(zero_ids, np.int32)
         (self.slot, self.pos_i32, self.indptr, self.indices, self.lpl, self.qo_indptr, self.q_rows,
-         self.cow_src, self.cow_dst) = _upload_i32(
-            [slot_grid, positions, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst], device)
+         self.cow_src, self.cow_dst, self.zero_ids) = _upload_i32(
+            [slot_grid, positions, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst, zero_ids],
+            device)
         self.batch, self.iw = batch, iw
         self.total_pages = int(indptr[-1]) if len(indptr) else 0
         self.total_q = int(qo_indptr[-1]) if len(qo_indptr) else 0
@@ -562,32 +574,57 @@ class PagedCacheContext(CacheContext):
 
         # write plan + copy-on-write, in batch order (kv_cache.py:575-594): a shared page
         # is copied by every writer but the last remaining sharer, which writes in place.
-        slot = np.full((B, iw), -1, np.int32)
         cow_src: List[int] = []
         cow_dst: List[int] = []
-        for b, st in enumerate(states):
-            n = self.new_token_counts[b]
-            if n <= 0:
-                continue
-            ap = np.arange(st.num_tokens, st.num_tokens + n, dtype=np.int64)
-            pi = ap // ps
-            for p in range(int(pi[0]), min(int(pi[-1]) + 1, st.n_pages)):
-                pid = int(st.bt[p])
-                if pool.is_shared(pid):
-                    new = pool.cow_alloc(pid)
-                    if new is None:
-                        raise RuntimeError("KV OOM during CoW")
-                    cow_src.append(pid)
-                    cow_dst.append(new)
-                    st.bt[p] = new
-                    pool.release(pid)
-            ok = pi < st.n_pages
-            pids = np.where(ok, st.bt[np.minimum(pi, max(st.n_pages - 1, 0))] if st.n_pages else 0, 0)
-            sls = np.where(ok, ap % ps, 0)
-            o = self.input_offsets[b]
-            slot[b, o:o + n] = (pids * ps + sls).astype(np.int32)
+
+        def _cow(st, p):
+            pid = int(st.bt[p])
+            new = pool.cow_alloc(pid)
+            if new is None:
+                raise RuntimeError("KV OOM during CoW")
+            cow_src.append(pid)
+            cow_dst.append(new)
+            st.bt[p] = new
+            pool.release(pid)
+
+        if self._is_decode and iw == 1:
+            # one token per sequence: vectorised over the batch. Only a page that is
+            # shared before any copy can need one, so the candidates are re-checked in
+            # batch order, which reproduces the sequential rule exactly.
+            start = np.fromiter(self.start_positions, np.int64, B)
+            pi = start // ps
+            sl = start % ps
+            have = np.fromiter((st.n_pages for st in states), np.int64, B)
+            ok = pi < have
+            pids = np.fromiter((int(st.bt[p]) if p < st.n_pages else 0
+                                for st, p in zip(states, pi.tolist())), np.int64, B)
+            cand = np.nonzero(ok & (pool.ref_count[pids] > 1))[0]
+            for b in cand.tolist():
+                st = states[b]
+                if pool.is_shared(int(st.bt[pi[b]])):
+                    _cow(st, int(pi[b]))
+                    pids[b] = st.bt[pi[b]]
+            slot = np.where(ok, pids * ps + sl, 0).astype(np.int32).reshape(B, 1)
             if ok.any():
-                np.maximum.at(pool.tokens_used, pids[ok], sls[ok] + 1)
+                np.maximum.at(pool.tokens_used, pids[ok], sl[ok] + 1)
+        else:
+            slot = np.full((B, iw), -1, np.int32)
+            for b, st in enumerate(states):
+                n = self.new_token_counts[b]
+                if n <= 0:
+                    continue
+                ap = np.arange(st.num_tokens, st.num_tokens + n, dtype=np.int64)
+                pi = ap // ps
+                for p in range(int(pi[0]), min(int(pi[-1]) + 1, st.n_pages)):
+                    if pool.is_shared(int(st.bt[p])):
+                        _cow(st, p)
+                ok = pi < st.n_pages
+                pids = np.where(ok, st.bt[np.minimum(pi, max(st.n_pages - 1, 0))] if st.n_pages else 0, 0)
+                sls = np.where(ok, ap % ps, 0)
+                o = self.input_offsets[b]
+                slot[b, o:o + n] = (pids * ps + sls).astype(np.int32)
+                if ok.any():
+                    np.maximum.at(pool.tokens_used, pids[ok], sls[ok] + 1)
         self.cow_pairs = list(zip(cow_src, cow_dst))
 
         # CSR block table (kv_cache.py:598-615)
@@ -596,12 +633,12 @@ class PagedCacheContext(CacheContext):
         indptr = np.zeros(B + 1, np.int64)
         np.cumsum(npg, out=indptr[1:])
         parts = []
-        for b, st in enumerate(states):
-            k = int(npg[b])
-            have = min(k, st.n_pages)
-            parts.append(st.bt[:have])
-            if k > have:
-                parts.append(np.zeros(k - have, np.int32))
+        for k, st in zip(npg.tolist(), states):
+            if k <= st.n_pages:
+                parts.append(st.bt[:k])
+            else:  # pages missing from the table read the null page (kv_cache.py:606-607)
+                parts.append(st.bt[:st.n_pages])
+                parts.append(np.zeros(k - st.n_pages, np.int32))
         indices = np.concatenate(parts) if parts else np.zeros(0, np.int32)
         if indices.size == 0:
             indices = np.zeros(1, np.int32)
@@ -609,21 +646,15 @@ class PagedCacheContext(CacheContext):
         if B == 0:
             lpl = np.zeros(1, np.int64)
 
-        qn = np.asarray(self.new_token_counts, np.int64)
-        qo = np.zeros(B + 1, np.int64)
-        np.cumsum(qn, out=qo[1:])
-        self._max_q = int(qn.max()) if B else 0
-        # rows of the [B*S] input grid that carry new tokens, in ragged order
-        self._uniform_rows = all(o == 0 for o in self.input_offsets) and all(n == iw for n in self.new_token_counts)
-        rows = [np.arange(b * iw + self.input_offsets[b], b * iw + self.input_offsets[b] + self.new_token_counts[b])
-                for b in range(B)]
-        q_rows = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+        pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
+        self._max_q = max(self.new_token_counts) if B else 0
+        self._uniform_rows = int(qo[-1]) == B * iw  # every grid row carries a new token
 
-        if zero_pages:
-            pool.zero(zero_pages)
-        self._plan = _ForwardPlan(pool.device, B, iw, slot.reshape(-1), _positions(
-            self.start_positions, self.new_token_counts, self.input_offsets, iw).reshape(-1),
-            indptr, indices, lpl, qo, q_rows, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32))
+        self._plan = _ForwardPlan(pool.device, B, iw, slot.reshape(-1), pos, indptr, indices, lpl, qo,
+                                  q_rows, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32),
+                                  zero_pages)
+        if zero_pages:  # zero-on-alloc of the pages this forward's extensions took
+            cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
             cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
 
@@ -794,9 +825,9 @@ class ContiguousCacheContext(CacheContext):
         iw = self._iw
         slot = np.full((B, iw), -1, np.int32)
         for b in range(B):
-            o, n, s = self.input_offsets[b], self.new_token_counts[b], self.start_positions[b]
+            o, n, s0 = self.input_offsets[b], self.new_token_counts[b], self.start_positions[b]
             if n > 0:
-                slot[b, o:o + n] = self.slots[b] * Smax + np.arange(s, s + n)
+                slot[b, o:o + n] = self.slots[b] * Smax + np.arange(s0, s0 + n)
         indptr = np.arange(B + 1, dtype=np.int64)
         indices = np.asarray(self.slots or [0], np.int32)
         lpl = np.asarray(self.seq_lens or [0], np.int64)
@@ -806,17 +837,11 @@ class ContiguousCacheContext(CacheContext):
             indptr = np.zeros(B + 1, np.int64)
             np.cumsum(npg, out=indptr[1:])
             indices = np.asarray([s for s, L in zip(self.slots, self.seq_lens) if L > 0] or [0], np.int32)
-        qn = np.asarray(self.new_token_counts, np.int64)
-        qo = np.zeros(B + 1, np.int64)
-        np.cumsum(qn, out=qo[1:])
-        self._max_q = int(qn.max()) if B else 0
-        self._uniform_rows = all(o == 0 for o in self.input_offsets) and all(n == iw for n in self.new_token_counts)
-        rows = [np.arange(b * iw + self.input_offsets[b], b * iw + self.input_offsets[b] + self.new_token_counts[b])
-                for b in range(B)]
-        q_rows = np.concatenate(rows) if rows else np.zeros(0, np.int64)
-        self._plan = _ForwardPlan(cache.device, B, iw, slot.reshape(-1), _positions(
-            self.start_positions, self.new_token_counts, self.input_offsets, iw).reshape(-1),
-            indptr, indices, lpl, qo, q_rows, np.zeros(0, np.int32), np.zeros(0, np.int32))
+        pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
+        self._max_q = max(self.new_token_counts) if B else 0
+        self._uniform_rows = int(qo[-1]) == B * iw
+        self._plan = _ForwardPlan(cache.device, B, iw, slot.reshape(-1), pos, indptr, indices, lpl, qo,
+                                  q_rows, np.zeros(0, np.int32), np.zeros(0, np.int32))
 
     def get_position_ids(self, S: int) -> torch.Tensor:
         return _get_positions(self._plan, self.batch_size, self._iw, S)

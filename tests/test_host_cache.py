@@ -1,0 +1,348 @@
+"""Host layer (nanoslg_amd.kv_cache) against the CPU oracle on identical call
+sequences. The HIP kernels are replaced by tests/fake_kernels.py so the
+bookkeeping (allocation, block tables, copy-on-write order, radix sharing,
+eviction, plans, positions) is checked on the CPU; the GPU tests run the same
+host layer on the real kernels."""
+import math
+import random
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import fake_kernels as FK
+from nanoslg_amd import kv_cache as KC
+from oracle import kv_oracle as O
+
+L, HQ, HKV, D = 2, 4, 2, 8
+
+
+def make(ps=4, pages=64, prefix=True, dtype=torch.float32):
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
+                           max_pages=pages, dtype=dtype, device=None, enable_prefix_caching=prefix,
+                           backend="paged")
+    mgr = KC.PagedKVCache(cfg, kernels=FK)
+    ref = O.PagedRef(L, pages, ps, HKV, D, dtype, enable_prefix_caching=prefix)
+    return mgr, ref
+
+
+def logical(mgr, sid, layer):
+    st = mgr.seqs[sid]
+    ps = mgr.cfg.page_size
+    n = st.num_tokens
+    bt = st.block_table
+    k = torch.stack([mgr.pool.k[layer, bt[t // ps], t % ps] for t in range(n)]) if n else None
+    v = torch.stack([mgr.pool.v[layer, bt[t // ps], t % ps] for t in range(n)]) if n else None
+    return k, v
+
+
+def forward_both(mgr, ref, ids, ntok, offs, g):
+    S = max(o + n for o, n in zip(offs, ntok))
+    B = len(ids)
+    q = torch.randn(B, S, HQ, D, generator=g)
+    k = torch.randn(B, S, HKV, D, generator=g)
+    v = torch.randn(B, S, HKV, D, generator=g)
+    c1 = mgr.begin_forward(ids, ntok, offs)
+    c2 = ref.begin_forward(ids, ntok, offs)
+    assert c1.start_positions == c2.start_positions and c1.seq_lens == c2.seq_lens
+    assert torch.equal(c1.get_position_ids(S), c2.get_position_ids(S))
+    assert len(c1.cow_pairs) == len(c2.cow_events)
+    for layer in range(L):
+        o1 = c1.attend(layer, q, k, v, HQ, HKV)
+        o2 = c2.attend(layer, q, k, v, HQ, HKV)
+        assert o1.shape == (B, S, HQ * D)
+        for b in range(B):
+            rows = slice(offs[b], offs[b] + ntok[b])
+            torch.testing.assert_close(o1[b, rows].float(), o2[b, rows], atol=1e-5, rtol=1e-5)
+            # rows without a new token are zero
+            pad = torch.ones(S, dtype=torch.bool)
+            pad[rows] = False
+            assert not o1[b, pad].any()
+    mgr.end_forward(c1)
+    ref.end_forward(c2)
+    return c1, c2
+
+
+def check_state(mgr, ref, ids):
+    assert mgr.pool.num_free == ref.pool.num_free
+    for sid in ids:
+        assert mgr.seqs[sid].num_tokens == ref.seqs[sid].num_tokens
+        for layer in range(L):
+            k1, v1 = logical(mgr, sid, layer)
+            k2, v2 = ref.logical_kv(sid, layer)
+            if k1 is None:
+                assert k2.shape[0] == 0
+                continue
+            assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+def test_prefill_then_decode_matches_oracle():
+    g = torch.Generator().manual_seed(0)
+    mgr, ref = make()
+    ids = ["a", "b", "c"]
+    lens = [5, 9, 3]
+    for s, n in zip(ids, lens):
+        assert mgr.allocate_sequence(s, num_tokens=n) == ref.allocate_sequence(s, num_tokens=n) == 0
+    forward_both(mgr, ref, ids, lens, [max(lens) - n for n in lens], g)  # left-padded prefill
+    check_state(mgr, ref, ids)
+    for _ in range(9):
+        forward_both(mgr, ref, ids, [1, 1, 1], [0, 0, 0], g)
+    check_state(mgr, ref, ids)
+    # chunked prefill step of uneven sizes, including a sequence with no new tokens
+    forward_both(mgr, ref, ids, [3, 0, 6], [3, 6, 0], g)
+    check_state(mgr, ref, ids)
+
+
+def test_positions_shapes():
+    mgr, _ = make()
+    mgr.allocate_sequence("a", num_tokens=3)
+    mgr.allocate_sequence("b", num_tokens=2)
+    ctx = mgr.begin_forward(["a", "b"], [3, 2], [0, 1])
+    assert ctx.get_position_ids(3).tolist() == [[0, 1, 2], [0, 0, 1]]
+    assert ctx.get_position_ids(2).tolist() == [[0, 1], [0, 0]]
+    assert ctx.get_position_ids(5).tolist() == [[0, 1, 2, 0, 0], [0, 0, 1, 0, 0]]
+    assert ctx.get_position_ids(3).dtype == torch.long
+    assert ctx.get_start_pos(1) == 0 and ctx.get_position(3).shape == (2, 3)
+
+
+def test_csr_plan_closed_form():
+    mgr, _ = make(ps=4)
+    mgr.allocate_sequence("a", num_tokens=9)
+    mgr.allocate_sequence("b", num_tokens=4)
+    mgr.seqs["a"].num_tokens = 9
+    mgr.seqs["b"].num_tokens = 4
+    ctx = mgr.begin_forward(["a", "b"], [1, 1])
+    plan = ctx.plan
+    bt_a, bt_b = mgr.seqs["a"].block_table, mgr.seqs["b"].block_table
+    assert plan.indptr.tolist() == [0, 3, 5]
+    assert plan.indices.tolist() == bt_a[:3] + bt_b[:2]
+    assert plan.lpl.tolist() == [2, 1]
+    assert plan.slot.tolist() == [bt_a[2] * 4 + 1, bt_b[1] * 4 + 0]
+    assert plan.total_pages == 5
+
+
+def _share_page(mgr_or_ref, ids, page, tokens):
+    """Make `ids` share one page holding `tokens` tokens (refcount = len(ids))."""
+    for s in ids:
+        st = mgr_or_ref.seqs[s]
+        if isinstance(st, KC._PagedSeqState):
+            st.bt[0] = page
+            st.n_pages = 1
+        else:
+            st.block_table = [page]
+        st.num_tokens = tokens
+
+
+def test_copy_on_write_order_rule():
+    """Refcount R held by R sharers: the first R-1 writers copy, the last writes in place."""
+    g = torch.Generator().manual_seed(1)
+    for mgr_ref in [make(prefix=False)]:
+        mgr, ref = mgr_ref
+        ids = ["x", "y", "z"]
+        for s in ids:
+            mgr.allocate_sequence(s, num_tokens=1)
+            ref.allocate_sequence(s, num_tokens=1)
+        # both: seq x's page becomes the shared one, the others' pages are released
+        for impl in (mgr, ref):
+            shared = impl.seqs["x"].block_table[0]
+            for s in ["y", "z"]:
+                impl.pool.release(impl.seqs[s].block_table[0])
+                impl.pool.add_ref(shared)
+            impl.pool.k[:, shared] = 3.0
+            impl.pool.v[:, shared] = -1.0
+            _share_page(impl, ids, shared, 2)
+        assert mgr.pool.ref_count[mgr.seqs["x"].block_table[0]] == 3
+        c1, c2 = forward_both(mgr, ref, ids, [1, 1, 1], [0, 0, 0], g)
+        assert len(c1.cow_pairs) == 2
+        src = c1.cow_pairs[0][0]
+        assert [p[0] for p in c1.cow_pairs] == [src, src]
+        assert mgr.seqs["z"].block_table[0] == src        # last sharer writes in place
+        assert mgr.pool.ref_count[src] == 1
+        check_state(mgr, ref, ids)
+        # copied pages carry the source's tokens_used and the source's bytes beyond slot 2
+        for s in ["x", "y"]:
+            p = mgr.seqs[s].block_table[0]
+            assert mgr.pool.tokens_used[p] == 3
+            assert torch.equal(mgr.pool.k[:, p, 3], mgr.pool.k[:, src, 3])
+
+
+def test_cow_oom_raises():
+    mgr, _ = make(prefix=False, pages=4)
+    mgr.allocate_sequence("x", num_tokens=1)
+    mgr.allocate_sequence("y", num_tokens=1)
+    mgr.allocate_sequence("z", num_tokens=1)
+    shared = mgr.seqs["x"].block_table[0]
+    for s in ["y", "z"]:
+        mgr.pool.release(mgr.seqs[s].block_table[0])
+        mgr.pool.add_ref(shared)
+    _share_page(mgr, ["x", "y", "z"], shared, 2)
+    mgr.allocate_sequence("w", num_tokens=8)  # takes the two free pages
+    with pytest.raises(RuntimeError, match="KV OOM during CoW"):
+        mgr.begin_forward(["x"], [1])
+
+
+def test_kv_oom_message_and_eviction():
+    mgr, ref = make(pages=6, prefix=True)
+    with pytest.raises(RuntimeError, match=r"KV OOM: need 6, free 5"):
+        mgr.allocate_sequence("big", num_tokens=24)
+    with pytest.raises(RuntimeError, match=r"KV OOM: need 6, free 5"):
+        ref.allocate_sequence("big", num_tokens=24)
+    # fill the tree with cached pages, then allocation must evict them
+    g = torch.Generator().manual_seed(2)
+    toks = list(range(100, 116))
+    for impl in (mgr, ref):
+        impl.allocate_sequence("a", token_ids=toks)
+    forward_both(mgr, ref, ["a"], [16], [0], g)
+    mgr.release_sequence("a")
+    ref.release_sequence("a")
+    assert mgr.tree.cached_pages == ref.tree.cached_pages == 4
+    assert mgr.pool.num_free == ref.pool.num_free == 1
+    assert mgr.allocate_sequence("b", num_tokens=12) == 0
+    ref.allocate_sequence("b", num_tokens=12)
+    assert mgr.pool.num_free == ref.pool.num_free
+    assert mgr.tree.cached_pages == ref.tree.cached_pages
+
+
+def test_radix_prefix_sharing_matches_oracle():
+    g = torch.Generator().manual_seed(3)
+    mgr, ref = make(ps=4, pages=64, prefix=True)
+    prompt = [7, 1, 3, 3, 9, 9, 2, 5, 4, 4, 6, 8, 1, 2]  # 3 full pages + 2 tokens
+    for impl in (mgr, ref):
+        assert impl.allocate_sequence("p", token_ids=prompt) == 0
+    forward_both(mgr, ref, ["p"], [len(prompt)], [0], g)
+    for _ in range(3):
+        forward_both(mgr, ref, ["p"], [1], [0], g)
+        for impl in (mgr, ref):
+            impl.append_token_ids("p", [11])
+    mgr.release_sequence("p")
+    ref.release_sequence("p")
+    assert mgr.tree.cached_pages == ref.tree.cached_pages == 4
+    # a new request sharing the first 2 pages, then diverging
+    q = prompt[:8] + [0, 0, 0, 0, 0]
+    p1 = mgr.allocate_sequence("q", token_ids=q)
+    p2 = ref.allocate_sequence("q", token_ids=q)
+    assert p1 == p2 == 8
+    # the cache's first two logical pages hold the same K/V as the prompt had
+    check_state(mgr, ref, ["q"])
+    forward_both(mgr, ref, ["q"], [len(q) - 8], [0], g)
+    check_state(mgr, ref, ["q"])
+    forward_both(mgr, ref, ["q"], [1], [0], g)
+    check_state(mgr, ref, ["q"])
+    mgr.release_sequence("q")
+    ref.release_sequence("q")
+    assert mgr.pool.num_free == ref.pool.num_free
+
+
+def test_radix_random_workload_matches_oracle():
+    """Random admissions over a small vocabulary: prefix hits, inserts and evictions."""
+    rnd = random.Random(5)
+    g = torch.Generator().manual_seed(5)
+    mgr, ref = make(ps=2, pages=40, prefix=True)
+    live = {}
+    for it in range(60):
+        if live and (rnd.random() < 0.4 or len(live) >= 3):
+            sid = rnd.choice(sorted(live))
+            mgr.release_sequence(sid)
+            ref.release_sequence(sid)
+            del live[sid]
+        else:
+            sid = f"r{it}"
+            toks = [rnd.randint(0, 2) for _ in range(rnd.randint(2, 9))]
+            try:
+                p1 = mgr.allocate_sequence(sid, token_ids=toks)
+            except RuntimeError:
+                with pytest.raises(RuntimeError):
+                    ref.allocate_sequence(sid, token_ids=toks)
+                continue
+            p2 = ref.allocate_sequence(sid, token_ids=toks)
+            assert p1 == p2
+            n = len(toks) - p1
+            if n > 0:
+                forward_both(mgr, ref, [sid], [n], [0], g)
+            live[sid] = toks
+        assert mgr.pool.num_free == ref.pool.num_free
+        assert mgr.tree.cached_pages == ref.tree.cached_pages
+        check_state(mgr, ref, sorted(live))
+
+
+def test_decode_batch_with_new_pages_zeroed():
+    g = torch.Generator().manual_seed(6)
+    mgr, ref = make(ps=4)
+    ids = ["a", "b"]
+    for impl in (mgr, ref):
+        impl.allocate_sequence("a", num_tokens=4)
+        impl.allocate_sequence("b", num_tokens=3)
+    forward_both(mgr, ref, ids, [4, 3], [0, 1], g)
+    FK.CALLS.clear()
+    forward_both(mgr, ref, ids, [1, 1], [0, 0], g)  # "a" crosses into a new page
+    assert [c for c in FK.CALLS if c[0] == "zero_pages"] == [("zero_pages", 1)]
+    p = mgr.seqs["a"].block_table[1]
+    assert not mgr.pool.k[:, p, 1:].any()
+    check_state(mgr, ref, ids)
+
+
+def test_contiguous_backend_matches_oracle():
+    g = torch.Generator().manual_seed(7)
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, max_batch_size=3,
+                           max_seq_len=32, dtype=torch.float32, device=None, backend="contiguous")
+    mgr = KC.ContiguousKVCache(cfg, kernels=FK)
+    ref = O.ContiguousRef(L, 3, 32, HKV, D)
+    ids = ["a", "b", "c"]
+    for s in ids:
+        mgr.allocate_sequence(s)
+        ref.allocate_sequence(s)
+    steps = [([5, 9, 3], [4, 0, 6])] + [([1, 1, 1], [0, 0, 0])] * 5
+    for ntok, offs in steps:
+        S = max(o + n for o, n in zip(offs, ntok))
+        q = torch.randn(3, S, HQ, D, generator=g)
+        k = torch.randn(3, S, HKV, D, generator=g)
+        v = torch.randn(3, S, HKV, D, generator=g)
+        c1 = mgr.begin_forward(ids, ntok, offs)
+        c2 = ref.begin_forward(ids, ntok, offs)
+        assert torch.equal(c1.get_position_ids(S), c2.get_position_ids(S))
+        for layer in range(L):
+            o1 = c1.attend(layer, q, k, v, HQ, HKV)
+            o2 = c2.attend(layer, q, k, v, HQ, HKV)
+            for b in range(3):
+                rows = slice(offs[b], offs[b] + ntok[b])
+                torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=1e-5, rtol=1e-5)
+        mgr.end_forward(c1)
+        ref.end_forward(c2)
+    assert torch.equal(mgr.k, ref.k) and torch.equal(mgr.v, ref.v)
+    assert mgr.stats["slots"] == "3/3"
+    with pytest.raises(AssertionError):
+        mgr.allocate_sequence("d")
+    mgr.reset()
+    assert mgr.stats["active_seqs"] == 0 and mgr.stats["slots"] == "0/3"
+
+
+def test_config_and_factory():
+    hf = types.SimpleNamespace(num_hidden_layers=32, num_key_value_heads=8, num_attention_heads=32,
+                               hidden_size=4096)
+    par = types.SimpleNamespace(tp_size=2, pp_size=1, pp_layer_splits=None)
+    cfg = KC.KVCacheConfig.from_hf_config(hf, par, device=None, dtype=torch.float16)
+    assert (cfg.num_layers, cfg.num_kv_heads, cfg.num_qo_heads, cfg.head_dim) == (32, 4, 16, 128)
+    assert cfg.backend == "paged" and cfg.max_pages == 256  # no device -> the reference's default
+    assert KC.KVCacheConfig(1, 8, 32, 128, backend="flashinfer", device=None).backend == "paged"
+    with pytest.raises(ValueError):
+        KC.KVCacheConfig(1, 8, 32, 128, backend="bogus")
+    hf1 = types.SimpleNamespace(num_hidden_layers=2, num_key_value_heads=2, num_attention_heads=4,
+                                hidden_size=32)
+    m = types.SimpleNamespace(kv_backend="contiguous", max_seq_len=64)
+    mgr = KC.create_cache_manager(hf1, None, "cpu", torch.float16, m, max_batch_size=2)
+    assert isinstance(mgr, KC.ContiguousKVCache) and mgr.stats["max_seq"] == 64
+    assert mgr.k.shape == (2, 2, 64, 2, 8)
+    m = types.SimpleNamespace(page_size=8)  # kv_backend defaults to auto -> paged
+    mgr = KC.create_cache_manager(hf1, None, "cpu", torch.float16, m)
+    assert isinstance(mgr, KC.PagedKVCache) and mgr.pool.k.shape == (2, 256, 8, 2, 8)
+
+
+def test_stats_and_reset():
+    mgr, _ = make(ps=4, pages=16, prefix=True)
+    mgr.allocate_sequence("a", token_ids=list(range(9)))
+    st = mgr.stats
+    assert st["backend"] == "paged" and st["active_seqs"] == 1 and st["pages_used"] == 3
+    mgr.seqs["a"].num_tokens = 9
+    mgr.reset()
+    assert mgr.stats["active_seqs"] == 0 and mgr.stats["radix"] == 2 and mgr.pool.num_free == 13
