@@ -1,19 +1,419 @@
-// Paged causal prefill attention (placeholder until the MFMA kernel lands).
+// Paged causal (chunked) prefill attention for gfx950 (CDNA4), MFMA fp16/bf16
+// with fp32 accumulation.
+//
+// Query rows are packed GQA-style: for KV head h of sequence b the row space is
+// the b's n_b new tokens x the G query heads of h, row = token*G + g. A
+// workgroup (4 waves) owns 128 consecutive rows of one (sequence, KV head);
+// each wave owns 32 rows as two 16-row column blocks of the MFMA.
+//
+// Per 64-key tile (staged in LDS, double buffered, shared by the 4 waves):
+//   S^T[16 key x 16 row] = K[16 key x D] * Q^T[D x 16 row]   v_mfma 16x16x32, D/32 steps
+//   online softmax per row (column) in fp32, running max rescaled lazily
+//   O^T[D x 16 row] += V^T[D x 16 key] * P^T[16 key x 16 row]  v_mfma 16x16x16
+// which is the decode kernel's formulation with all 16 MFMA columns live.
+//
+// Causality is bottom-right aligned: sequence b holds L_b tokens of which the
+// last n_b are the new ones, so row token t sees keys j <= L_b - n_b + t.
+// The sequence's page ids for the workgroup's key range sit in LDS (windows of
+// 2048 pages), so tile loads never wait on index loads.
 #include "nslg_common.h"
+
+#include <math.h>
+
+namespace nslg {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerWG = kWaves * kRowsPerWave;  // 128
+constexpr int kKeys = 64;                          // keys per LDS tile
+constexpr int kPageWin = 2048;                     // page ids per LDS window
+constexpr float kRescaleSlack = 8.0f;
+
+struct PrefillParams {
+  const uint16_t* q;
+  int64_t q_stride;
+  const int32_t* qo_indptr;
+  const uint16_t* k_pool;
+  const uint16_t* v_pool;
+  int64_t num_pages;
+  int32_t page_size;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* last_len;
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t group;
+  float scale_log2;
+  uint16_t* out;
+  int64_t out_stride;
+};
+
+template <int N>
+struct Vec {
+  typedef unsigned short type __attribute__((ext_vector_type(N)));
+};
+
+__device__ inline int kv_len_of(const PrefillParams& p, int s) {
+  const int np = p.indptr[s + 1] - p.indptr[s];
+  if (np <= 0) return 0;
+  int lpl = p.last_len[s];
+  lpl = lpl < 1 ? 1 : (lpl > p.page_size ? p.page_size : lpl);
+  return (np - 1) * p.page_size + lpl;
+}
+
+// Wave-wide search for the (sequence, row tile) of workgroup x.
+__device__ inline bool locate_tile(const PrefillParams& p, int g, int& b, int& tile) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  for (int s0 = 0; s0 < p.batch; s0 += 64) {
+    const int s = s0 + lane;
+    int nt = 0;
+    if (s < p.batch) {
+      const int n = p.qo_indptr[s + 1] - p.qo_indptr[s];
+      nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+    }
+    int incl = nt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int excl = incl - nt;
+    const unsigned long long m = __ballot(nt > 0 && g >= base + excl && g < base + incl);
+    if (m) {
+      const int src = __ffsll((long long)m) - 1;
+      b = s0 + src;
+      tile = g - base - __shfl(excl, src, 64);
+      return true;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  return false;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
+  constexpr int kSteps = D / 32;
+  constexpr int NT = D / 16;
+  constexpr int kPitch = D + 8;  // LDS row pitch in elements (16 B pad vs bank conflicts)
+  constexpr bool kSplitP = T::kDtype == NSLG_BF16;
+  typedef typename Vec<NT>::type VT;
+
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKeys * kPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kPitch];
+  __shared__ int32_t page_lds[kPageWin];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = blockIdx.y;
+  int b = 0, tile = 0;
+  if (!locate_tile(p, blockIdx.x, b, tile)) return;  // uniform across the workgroup
+  b = __builtin_amdgcn_readfirstlane(b);
+  tile = __builtin_amdgcn_readfirstlane(tile);
+
+  const int q0 = p.qo_indptr[b];
+  const int n_new = p.qo_indptr[b + 1] - q0;
+  const int L = kv_len_of(p, b);
+  const int start = L - n_new > 0 ? L - n_new : 0;  // position of the first new token
+  const int G = p.group;
+  const int nrows = n_new * G;
+  const int row0_wg = tile * kRowsPerWG;
+  // keys this workgroup needs: up to the last row's position (inclusive)
+  const int last_row = min(row0_wg + kRowsPerWG, nrows) - 1;
+  const int kv_end = min(L, start + last_row / G + 1);
+  const int n_kt = (kv_end + kKeys - 1) / kKeys;
+  const int32_t* idx = p.indices + p.indptr[b];
+  const int np_seq = p.indptr[b + 1] - p.indptr[b];
+  const int ps = p.page_size;
+  const int row_bytes = p.num_kv_heads * D * 2;
+  const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
+  const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
+
+  const int r = lane & 15;
+  const int gq = lane >> 4;
+
+  // ---- per-wave rows: two 16-row column blocks --------------------------------------
+  u16x8 qb[2][kSteps];
+  int row_tok[2];
+  bool row_ok[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
+    row_ok[cb] = row < nrows;
+    const int t = row_ok[cb] ? row / G : 0;
+    row_tok[cb] = start + t;  // absolute position of this row's token
+    if (row_ok[cb]) {
+      const uint16_t* qrow = p.q + (int64_t)(q0 + t) * p.q_stride + (int64_t)(h * G + row % G) * D;
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) qb[cb][s] = *reinterpret_cast<const u16x8*>(qrow + 32 * s + 8 * gq);
+    } else {
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) qb[cb][s] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  // highest key any row of this wave may see (rows are token-major, so the wave's last row)
+  const int wave_last_row = min(row0_wg + wave * kRowsPerWave + kRowsPerWave, nrows) - 1;
+  const int wave_kv_end = wave_last_row >= row0_wg + wave * kRowsPerWave ? start + wave_last_row / G + 1 : 0;
+  // lowest position among the wave's rows: keys below start + first_tok + 1 are visible to all
+  const int wave_first_tok = start + (row0_wg + wave * kRowsPerWave) / G;
+
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.f, 0.f};
+  f32x4 o[2][NT];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[cb][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // ---- cooperative tile loads: 64 keys x D for K and V, 16 B per thread-chunk ------
+  constexpr int kChunks = D / 8;                       // 16 B chunks per row
+  constexpr int kPerThread = kKeys * kChunks / 256;    // 4 (D=128) or 2 (D=64)
+  u32x4 kreg[kPerThread], vreg[kPerThread];
+  int win_base = -1;
+
+  auto load_pages = [&](int first_key) {
+    // page ids for keys [first_key, first_key + kPageWin*ps), one window
+    const int pg0 = first_key / ps;
+    for (int i = tid; i < kPageWin; i += 256) {
+      int v = 0;
+      if (pg0 + i < np_seq) {
+        v = idx[pg0 + i];
+        if (v < 0 || (int64_t)v >= p.num_pages) v = 0;
+      }
+      page_lds[i] = v;
+    }
+    win_base = pg0;
+  };
+  auto fetch = [&](int kt) {
+    const int key0 = kt * kKeys;
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / kChunks;
+      const int ch = c % kChunks;
+      int kabs = key0 + key;
+      kabs = kabs < kv_end ? kabs : kv_end - 1;
+      const int pid = page_lds[kabs / ps - win_base];
+      const int64_t rowi = (int64_t)pid * ps + kabs % ps;
+      kreg[i] = *reinterpret_cast<const u32x4*>(kpool + rowi * row_bytes + ch * 16);
+      vreg[i] = *reinterpret_cast<const u32x4*>(vpool + rowi * row_bytes + ch * 16);
+    }
+  };
+  auto stash = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / kChunks;
+      const int ch = c % kChunks;
+      *reinterpret_cast<u32x4*>(&k_lds[stage][key * kPitch + ch * 8]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&v_lds[stage][key * kPitch + ch * 8]) = vreg[i];
+    }
+  };
+  // first key of the window holding tile kt must cover the whole tile
+  auto window_ok = [&](int kt) {
+    const int k_first = kt * kKeys;
+    const int k_last = min(k_first + kKeys, kv_end) - 1;
+    return win_base >= 0 && k_first / ps >= win_base && k_last / ps < win_base + kPageWin;
+  };
+
+  if (n_kt > 0) {
+    load_pages(0);
+    __syncthreads();
+    fetch(0);
+    stash(0);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int stage = kt & 1;
+    const bool more = kt + 1 < n_kt;
+    bool need_win = false;
+    if (more) {
+      need_win = !window_ok(kt + 1);
+      if (!need_win) fetch(kt + 1);
+    }
+    const int key0 = kt * kKeys;
+    if (key0 < wave_kv_end) {
+      const bool full = key0 + kKeys <= wave_first_tok + 1 && key0 + kKeys <= kv_end;
+#pragma unroll
+      for (int kb = 0; kb < kKeys / 16; ++kb) {
+        const int kbase = key0 + 16 * kb;
+        if (kbase >= wave_kv_end) break;
+        // K operand rows of this 16-key block, V operand rows 4*gq + j
+        u16x8 ka[kSteps];
+        const uint16_t* krow = &k_lds[stage][(16 * kb + r) * kPitch + 8 * gq];
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) ka[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
+        VT va[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          va[j] = *reinterpret_cast<const VT*>(&v_lds[stage][(16 * kb + 4 * gq + j) * kPitch + NT * r]);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < kSteps; ++s) sacc = T::mma_k32(ka[s], qb[cb][s], sacc);
+          float sv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key = kbase + 4 * gq + j;
+            const bool vis = full || (key < kv_end && key <= row_tok[cb]);
+            sv[j] = vis ? sacc[j] * p.scale_log2 : -INFINITY;
+          }
+          float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+          mx = wave_xor_max(mx, 16);
+          mx = wave_xor_max(mx, 32);
+          if (__ballot(mx > m_run[cb] + kRescaleSlack)) {
+            const float m_new = fmaxf(m_run[cb], mx);
+            const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[cb] - m_new);
+            l_run[cb] *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) o[cb][n] *= alpha;
+            m_run[cb] = m_new;
+          }
+          float pj[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pj[j] = sv[j] == -INFINITY ? 0.f : fast_exp2(sv[j] - m_run[cb]);
+          l_run[cb] += (pj[0] + pj[1]) + (pj[2] + pj[3]);
+          u16x4 pb, pb_lo;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pb[j] = T::from_f32(pj[j]);
+          if constexpr (kSplitP) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pb_lo[j] = T::from_f32(pj[j] - T::to_f32(pb[j]));
+          }
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            u16x4 a = {va[0][n], va[1][n], va[2][n], va[3][n]};
+            o[cb][n] = T::mma_k16(a, pb, o[cb][n]);
+            if constexpr (kSplitP) o[cb][n] = T::mma_k16(a, pb_lo, o[cb][n]);
+          }
+        }
+      }
+    }
+    if (more) {
+      if (need_win) {
+        // the next tile crosses the page-id window: reload it (all threads finished
+        // reading the current stage's page ids in the fetch above, so only the new
+        // window must be visible before fetching)
+        __syncthreads();
+        load_pages((kt + 1) * kKeys);
+        __syncthreads();
+        fetch(kt + 1);
+      }
+      stash(stage ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalise and store rows ----------------------------------------
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    float l_tot = wave_xor_sum(l_run[cb], 16);
+    l_tot = wave_xor_sum(l_tot, 32);
+    if (!row_ok[cb]) continue;
+    const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
+    const int t = row / G;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint16_t* orow = p.out + (int64_t)(q0 + t) * p.out_stride + (int64_t)(h * G + row % G) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      VT w;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) w[n] = T::from_f32(o[cb][n][i] * inv);
+      *reinterpret_cast<VT*>(orow + NT * (4 * gq + i)) = w;
+    }
+  }
+}
+
+// Rows of every sequence with no key to attend (n_new > 0 but L = 0 cannot occur
+// with a consistent plan; sequences with n_new = 0 have no rows) need no pass.
+
+inline int64_t grid_tiles(int64_t total_q, int32_t batch, int group) {
+  return (total_q * group + kRowsPerWG - 1) / kRowsPerWG + batch;
+}
+
+template <typename T, int D>
+int launch_prefill(const PrefillParams& p, int64_t tiles, hipStream_t s) {
+  dim3 grid((unsigned)tiles, p.num_kv_heads);
+  paged_prefill_kernel<T, D><<<grid, 256, 0, s>>>(p);
+  return check_launch("paged_prefill");
+}
+
+}  // namespace
+}  // namespace nslg
 
 using namespace nslg;
 
 extern "C" size_t nslg_paged_prefill_workspace_size(int32_t batch, int32_t num_qo_heads,
                                                     int32_t head_dim, int64_t total_q,
                                                     int32_t max_q) {
-  (void)batch; (void)num_qo_heads; (void)head_dim; (void)total_q; (void)max_q;
-  return 256;
+  (void)batch;
+  (void)num_qo_heads;
+  (void)head_dim;
+  (void)total_q;
+  (void)max_q;
+  return 256;  // the prefill kernel keeps all state on chip
 }
 
-extern "C" int nslg_paged_prefill(const void*, int64_t, const int32_t*, int64_t, int32_t,
-                                  const void*, const void*, int64_t, int32_t, const int32_t*,
-                                  const int32_t*, const int32_t*, int32_t, int32_t, int32_t,
-                                  int32_t, float, int32_t, void*, int64_t, void*, size_t,
-                                  nslg_stream_t) {
-  return fail(NSLG_EUNSUPPORTED, "paged_prefill: not built yet");
+extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                                  int64_t total_q, int32_t max_q, const void* k_pool,
+                                  const void* v_pool, int64_t num_pages, int32_t page_size,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices,
+                                  const int32_t* kv_last_page_len, int32_t batch,
+                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  float sm_scale, int32_t dtype, void* out, int64_t out_stride,
+                                  void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
+  (void)max_q;
+  (void)workspace;
+  (void)workspace_bytes;
+  if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
+      num_pages <= 0 || total_q < 0)
+    return fail(NSLG_EINVAL, "paged_prefill: bad sizes");
+  if (batch == 0 || total_q == 0) return NSLG_OK;
+  if (!q || !qo_indptr || !k_pool || !v_pool || !kv_indptr || !kv_indices || !kv_last_page_len || !out)
+    return fail(NSLG_EINVAL, "paged_prefill: null pointer");
+  if (num_qo_heads % num_kv_heads != 0)
+    return fail(NSLG_EINVAL, "paged_prefill: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
+  const int group = num_qo_heads / num_kv_heads;
+  if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_prefill: GQA group %d > 16", group);
+  if (dtype != NSLG_F16 && dtype != NSLG_BF16)
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: dtype %d (f16/bf16 only)", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: head_dim %d (64 or 128)", head_dim);
+  if (num_kv_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many KV heads");
+  if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
+    return fail(NSLG_EINVAL, "paged_prefill: row stride smaller than Hq*D");
+  if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) & 15 ||
+      (q_stride * 2) % 16 || (out_stride * 2) % 16)
+    return fail(NSLG_EINVAL, "paged_prefill: q/pool/out must be 16-byte aligned");
+  if (num_pages * (int64_t)page_size >= ((int64_t)1 << 31))
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: pool has >= 2^31 token slots");
+  const int64_t tiles = grid_tiles(total_q, batch, group);
+  if (tiles > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
+
+  PrefillParams p;
+  p.q = (const uint16_t*)q;
+  p.q_stride = q_stride;
+  p.qo_indptr = qo_indptr;
+  p.k_pool = (const uint16_t*)k_pool;
+  p.v_pool = (const uint16_t*)v_pool;
+  p.num_pages = num_pages;
+  p.page_size = page_size;
+  p.indptr = kv_indptr;
+  p.indices = kv_indices;
+  p.last_len = kv_last_page_len;
+  p.batch = batch;
+  p.num_qo_heads = num_qo_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = group;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.out = (uint16_t*)out;
+  p.out_stride = out_stride;
+  hipStream_t s = as_stream(stream);
+  if (dtype == NSLG_F16) return head_dim == 64 ? launch_prefill<F16, 64>(p, tiles, s) : launch_prefill<F16, 128>(p, tiles, s);
+  return head_dim == 64 ? launch_prefill<BF16, 64>(p, tiles, s) : launch_prefill<BF16, 128>(p, tiles, s);
 }

@@ -1,0 +1,201 @@
+"""The drop-in cache API on the GPU (real HIP kernels) against the CPU oracle on
+identical call sequences: ragged prefill, decode, copy-on-write, radix prefix
+sharing, the contiguous backend and the factory. Page contents are compared
+bit-exactly through each sequence's block table; attention outputs within
+2e-3 abs + 1e-2 rel of fp32 SDPA."""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+DEV = torch.device("cuda:0")
+L, HQ, HKV, D = 2, 32, 8, 128
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make(ps=16, pages=256, prefix=True, dtype=torch.float16):
+    from nanoslg_amd import kv_cache as KC
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
+                           max_pages=pages, dtype=dtype, device=DEV, enable_prefix_caching=prefix,
+                           backend="paged")
+    return KC.PagedKVCache(cfg), O.PagedRef(L, pages, ps, HKV, D, torch.float32, enable_prefix_caching=prefix)
+
+
+def forward_both(mgr, ref, ids, ntok, offs, g, dtype=torch.float16):
+    S = max(o + n for o, n in zip(offs, ntok))
+    B = len(ids)
+    q = torch.randn(B, S, HQ, D, generator=g).to(dtype)
+    k = torch.randn(B, S, HKV, D, generator=g).to(dtype)
+    v = torch.randn(B, S, HKV, D, generator=g).to(dtype)
+    c1 = mgr.begin_forward(ids, ntok, offs)
+    c2 = ref.begin_forward(ids, ntok, offs)
+    assert torch.equal(c1.get_position_ids(S).cpu(), c2.get_position_ids(S))
+    assert len(c1.cow_pairs) == len(c2.cow_events)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    for layer in range(L):
+        o1 = c1.attend(layer, qd, kd, vd, HQ, HKV).float().cpu()
+        o2 = c2.attend(layer, q.float(), k.float(), v.float(), HQ, HKV)
+        assert o1.shape == (B, S, HQ * D)
+        for b in range(B):
+            rows = slice(offs[b], offs[b] + ntok[b])
+            torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=ATOL, rtol=RTOL)
+            pad = torch.ones(S, dtype=torch.bool)
+            pad[rows] = False
+            assert not o1[b, pad].any()
+    mgr.end_forward(c1)
+    ref.end_forward(c2)
+    return c1, c2
+
+
+def check_state(mgr, ref, ids):
+    torch.cuda.synchronize()
+    assert mgr.pool.num_free == ref.pool.num_free
+    ps = mgr.cfg.page_size
+    kpool, vpool = mgr.pool.k.cpu(), mgr.pool.v.cpu()
+    for sid in ids:
+        st = mgr.seqs[sid]
+        assert st.num_tokens == ref.seqs[sid].num_tokens
+        bt = st.block_table
+        n = st.num_tokens
+        for layer in range(L):
+            k1 = torch.stack([kpool[layer, bt[t // ps], t % ps] for t in range(n)])
+            v1 = torch.stack([vpool[layer, bt[t // ps], t % ps] for t in range(n)])
+            k2, v2 = ref.logical_kv(sid, layer)
+            assert torch.equal(k1.float(), k2) and torch.equal(v1.float(), v2)
+
+
+def test_paged_prefill_then_decode():
+    _log("cache: prefill + decode")
+    g = torch.Generator().manual_seed(0)
+    mgr, ref = make()
+    ids = ["a", "b", "c"]
+    lens = [50, 90, 17]
+    for s, n in zip(ids, lens):
+        assert mgr.allocate_sequence(s, num_tokens=n) == ref.allocate_sequence(s, num_tokens=n) == 0
+    forward_both(mgr, ref, ids, lens, [max(lens) - n for n in lens], g)
+    for _ in range(20):
+        forward_both(mgr, ref, ids, [1, 1, 1], [0, 0, 0], g)
+    forward_both(mgr, ref, ids, [33, 0, 5], [0, 33, 28], g)  # chunked prefill, one idle sequence
+    check_state(mgr, ref, ids)
+    for s in ids:
+        mgr.release_sequence(s)
+        ref.release_sequence(s)
+    assert mgr.pool.num_free == ref.pool.num_free
+
+
+def test_copy_on_write_shared_partial_page():
+    """16 sequences share a 2040-token prefix (127 full pages + a page with 8 slots);
+    the first append of each hits slot 8 of the shared page: 15 copies, the last
+    sharer writes in place."""
+    _log("cache: copy-on-write")
+    g = torch.Generator().manual_seed(1)
+    mgr, ref = make(pages=512, prefix=False)
+    R = 16
+    ids = [f"r{i}" for i in range(R)]
+    prefix = 2040
+    for impl in (mgr, ref):
+        impl.allocate_sequence("p", num_tokens=prefix)
+    forward_both(mgr, ref, ["p"], [prefix], [0], g)
+    for impl in (mgr, ref):
+        pages = impl.seqs["p"].block_table
+        for sid in ids:
+            impl.allocate_sequence(sid)
+            for p in pages:
+                impl.pool.add_ref(p)
+            st = impl.seqs[sid]
+            if hasattr(st, "bt"):
+                st.extend(pages)
+            else:
+                st.block_table = list(pages)
+            st.num_tokens = prefix
+        # the prefix owner steps away: the sequences hold the only references
+        st = impl.seqs.pop("p")
+        for p in pages:
+            impl.pool.release(p)
+    shared_last = mgr.seqs[ids[0]].block_table[-1]
+    assert mgr.pool.ref_count[shared_last] == R
+    c1, c2 = forward_both(mgr, ref, ids, [1] * R, [0] * R, g)
+    assert len(c1.cow_pairs) == R - 1 == len(c2.cow_events)
+    assert mgr.seqs[ids[-1]].block_table[-1] == shared_last
+    for _ in range(10):
+        forward_both(mgr, ref, ids, [1] * R, [0] * R, g)
+    check_state(mgr, ref, ids)
+
+
+def test_radix_prefix_reuse():
+    _log("cache: radix prefix reuse")
+    g = torch.Generator().manual_seed(2)
+    mgr, ref = make(pages=128, prefix=True)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, 128256, size=70).tolist()
+    for impl in (mgr, ref):
+        impl.allocate_sequence("a", token_ids=prompt)
+    forward_both(mgr, ref, ["a"], [70], [0], g)
+    mgr.release_sequence("a")
+    ref.release_sequence("a")
+    q2 = prompt[:64] + rng.integers(0, 128256, size=9).tolist()
+    p1 = mgr.allocate_sequence("b", token_ids=q2)
+    p2 = ref.allocate_sequence("b", token_ids=q2)
+    assert p1 == p2 == 64
+    check_state(mgr, ref, ["b"])
+    forward_both(mgr, ref, ["b"], [9], [0], g)
+    forward_both(mgr, ref, ["b"], [1], [0], g)
+    check_state(mgr, ref, ["b"])
+
+
+def test_contiguous_backend_on_gpu():
+    _log("cache: contiguous backend")
+    from nanoslg_amd import kv_cache as KC
+    g = torch.Generator().manual_seed(3)
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, max_batch_size=3,
+                           max_seq_len=256, dtype=torch.float16, device=DEV, backend="contiguous")
+    mgr = KC.ContiguousKVCache(cfg)
+    ref = O.ContiguousRef(L, 3, 256, HKV, D)
+    ids = ["a", "b", "c"]
+    for s in ids:
+        mgr.allocate_sequence(s)
+        ref.allocate_sequence(s)
+    steps = [([40, 100, 7], [60, 0, 93])] + [([1, 1, 1], [0, 0, 0])] * 6 + [([20, 3, 1], [0, 17, 19])]
+    for ntok, offs in steps:
+        S = max(o + n for o, n in zip(offs, ntok))
+        q = torch.randn(3, S, HQ, D, generator=g).half()
+        k = torch.randn(3, S, HKV, D, generator=g).half()
+        v = torch.randn(3, S, HKV, D, generator=g).half()
+        c1 = mgr.begin_forward(ids, ntok, offs)
+        c2 = ref.begin_forward(ids, ntok, offs)
+        assert torch.equal(c1.get_position_ids(S).cpu(), c2.get_position_ids(S))
+        for layer in range(L):
+            o1 = c1.attend(layer, q.to(DEV), k.to(DEV), v.to(DEV), HQ, HKV).float().cpu()
+            o2 = c2.attend(layer, q.float(), k.float(), v.float(), HQ, HKV)
+            for b in range(3):
+                rows = slice(offs[b], offs[b] + ntok[b])
+                torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=ATOL, rtol=RTOL)
+        mgr.end_forward(c1)
+        ref.end_forward(c2)
+    torch.cuda.synchronize()
+    assert torch.equal(mgr.k.cpu().float(), ref.k) and torch.equal(mgr.v.cpu().float(), ref.v)
+
+
+def test_factory_on_gpu():
+    _log("cache: factory")
+    import types
+    from nanoslg_amd import kv_cache as KC
+    hf = types.SimpleNamespace(num_hidden_layers=2, num_key_value_heads=8, num_attention_heads=32,
+                               hidden_size=4096)
+    m = types.SimpleNamespace(kv_backend="auto", page_size=16, max_kv_pages=64)
+    mgr = KC.create_cache_manager(hf, None, "cuda:0", torch.float16, m)
+    assert isinstance(mgr, KC.PagedKVCache) and mgr.pool.k.is_cuda and mgr.cfg.max_pages == 64
+    m = types.SimpleNamespace(kv_backend="auto", page_size=16)  # pages sized from free memory
+    mgr = KC.create_cache_manager(hf, None, "cuda:0", torch.float16, m)
+    assert 64 <= mgr.cfg.max_pages <= 65536

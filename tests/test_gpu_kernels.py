@@ -223,3 +223,65 @@ def test_decode_rejects_bad_arguments():
     ip = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
     with pytest.raises(KernelLibraryError):
         kern.paged_decode(q, kv, kv, ip, ip[:2].contiguous(), ip[:2].contiguous(), 2)
+
+
+# ------------------------------------------------------------------ prefill attention
+
+
+def _prefill_case(lens, news, Hq, Hkv, D, ps, dtype, seed, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    npg = sum(math.ceil(L / ps) for L in lens)
+    P = npg + 4
+    k = torch.randn(P, ps, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(P, ps, Hkv, D, generator=g).to(dtype)
+    T = sum(news)
+    q = torch.randn(T, Hq, D, generator=g).to(dtype)
+    tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, seed)
+    qo = np.zeros(len(lens) + 1, np.int32)
+    qo[1:] = np.cumsum(news)
+    out = _k().paged_prefill(q.to(DEV), torch.from_numpy(qo).to(DEV), T, max(news), k.to(DEV), v.to(DEV),
+                             torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV),
+                             torch.from_numpy(lpl).to(DEV), sm_scale=scale)
+    torch.cuda.synchronize()
+    qs = [q[qo[b]:qo[b + 1]] for b in range(len(lens))]
+    ref = O.paged_attention_ref(qs, k.view(-1, Hkv, D), v.view(-1, Hkv, D), ps, indptr, indices, lpl, news, scale)
+    return out.cpu().float(), torch.cat(ref, 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_from_zero(dtype, D):
+    _log(f"prefill from zero dtype={dtype} D={D}")
+    out, ref = _prefill_case([37, 100, 1], [37, 100, 1], 32, 8, D, 16, dtype, seed=31 + D)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (8, 8), (16, 1), (48, 3), (16, 8)])
+def test_prefill_chunk_over_cached_context(Hq, Hkv):
+    _log(f"prefill chunked Hq={Hq} Hkv={Hkv}")
+    out, ref = _prefill_case([300, 1000, 64, 17], [64, 200, 64, 3], Hq, Hkv, 128, 16, torch.float16,
+                             seed=Hq * 7 + Hkv)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("ps", [1, 8, 32, 48])
+def test_prefill_page_sizes(ps):
+    _log(f"prefill ps={ps}")
+    out, ref = _prefill_case([130, 77, 400], [130, 20, 129], 32, 8, 128, ps, torch.float16, seed=40 + ps)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_long_chunk_and_page_window():
+    """A 512-token chunk over 3584 cached tokens, and a sequence whose page ids span
+    more than one 2048-entry window (page size 1)."""
+    _log("prefill long + window")
+    out, ref = _prefill_case([4096, 2500], [512, 300], 32, 8, 128, 16, torch.float16, seed=50)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    out, ref = _prefill_case([4500], [70], 32, 8, 128, 1, torch.float16, seed=51)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_sequence_without_new_tokens():
+    _log("prefill n=0 rows")
+    out, ref = _prefill_case([50, 20, 33], [5, 0, 33], 32, 8, 128, 16, torch.float16, seed=52, scale=0.1)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
