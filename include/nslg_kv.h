@@ -110,11 +110,14 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
                    nslg_stream_t stream);
 
 /*
- * Paged GQA decode attention, one query token per sequence, split-K over the
- * sequence's pages with an fp32 log-sum-exp merge.
+ * Paged GQA decode attention, one query token per sequence.
  * Replaces FlashInfer BatchDecodeWithPagedKVCacheWrapper.plan/run
  * (nanoslg/kv_cache.py:617-621, 650) and, with an identity block table, the
  * contiguous decode SDPA (kv_cache.py:312-321).
+ *
+ * The sequences' tokens are cut into equal chunks (about 1024 over the batch);
+ * one wave per (chunk, KV head) streams its pages through MFMA tiles and a
+ * second launch merges the chunks of each sequence in fp32 (log-sum-exp).
  *
  *   q        [batch] rows of Hq*D elements at element stride q_stride
  *   out      [batch] rows of Hq*D elements at element stride out_stride (q's dtype)
@@ -123,13 +126,15 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
  *   total_pages       host copy of kv_indptr[batch] (sizes the launch)
  *   sm_scale          softmax scale (1/sqrt(D) for the reference)
  *   workspace         caller-owned device scratch of at least
- *                     nslg_paged_decode_workspace_size(...) bytes
+ *                     nslg_paged_decode_workspace_size(...) bytes, 256-byte aligned;
+ *                     one call at a time per workspace
  * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16;
- * D in {64, 128, 256}; 1 <= Hq/Hkv <= 16.
+ * D in {64, 128, 256}; 1 <= Hq/Hkv <= 16. A sequence with no tokens gets zeros.
  */
 size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
-                                        int32_t head_dim, int64_t total_pages,
-                                        int32_t page_size);
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int64_t total_pages, int32_t page_size,
+                                        int32_t dtype);
 
 int nslg_paged_decode(const void* q, int64_t q_stride,
                       const void* k_pool, const void* v_pool, int64_t num_pages,

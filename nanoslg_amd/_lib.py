@@ -32,7 +32,8 @@ SIGNATURES = {
     "nslg_gather_kv": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p,
                                  c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                  c_void_p]),
-    "nslg_paged_decode_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int64, c_int32]),
+    "nslg_paged_decode_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
+                                                    c_int32]),
     "nslg_paged_decode": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                     c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,

@@ -227,8 +227,13 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(cur.k[ks], qb[ks], s);
     float sv[4];
+    if (t0 + 16 <= t_end) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sv[j] = (t0 + 4 * gq + j < t_end) ? s[j] * p.scale_log2 : -INFINITY;
+      for (int j = 0; j < 4; ++j) sv[j] = s[j] * p.scale_log2;
+    } else {  // the chunk's partial last tile
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sv[j] = (t0 + 4 * gq + j < t_end) ? s[j] * p.scale_log2 : -INFINITY;
+    }
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = wave_xor_max(mx, 16);
     mx = wave_xor_max(mx, 32);
@@ -310,6 +315,9 @@ paged_decode_kernel(DecodeParams p) {
       for (int j = 0; j < kDepth; ++j) {
         if (i + j >= n_tiles) break;
         issue(buf[(j + kDepth - 1) % kDepth]);
+        // keep the prefetch ahead of this tile's math (the scheduler would otherwise
+        // sink the loads below the first MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
         process(buf[j], t_begin + 16 * (i + j));
       }
     }
@@ -325,6 +333,7 @@ paged_decode_kernel(DecodeParams p) {
       for (int j = 0; j < kDepth; ++j) {
         if (i + j >= n_tiles) break;
         issue_any(i + j + kDepth - 1, buf[(j + kDepth - 1) % kDepth]);
+        __builtin_amdgcn_sched_barrier(0);
         process(buf[j], t_begin + 16 * (i + j));
       }
     }
@@ -413,25 +422,46 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
 
   const float* ml = p.part_ml + ((int64_t)cstart * p.num_qo_heads + hq) * 2;
   const int64_t ml_stride = (int64_t)p.num_qo_heads * 2;
-  float mmax = -INFINITY;
-  for (int c = lane; c < nchunks; c += 64) mmax = fmaxf(mmax, ml[c * ml_stride]);
+  // pass 1, lanes over chunks: the running max M and the denominator sum_c 2^(m_c - M) l_c
+  float mmax = -INFINITY, lsum = 0.f;
+  for (int c = lane; c < nchunks; c += 64) {
+    const float2 v = *reinterpret_cast<const float2*>(ml + c * ml_stride);
+    const float m_new = fmaxf(mmax, v.x);
+    lsum = lsum * fast_exp2(mmax - m_new) + v.y * fast_exp2(v.x - m_new);
+    mmax = m_new;
+  }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off, 64));
-  float lsum = 0.f;
-  for (int c = lane; c < nchunks; c += 64) lsum += fast_exp2(ml[c * ml_stride] - mmax) * ml[c * ml_stride + 1];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off, 64);
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float om = __shfl_xor(mmax, off, 64);
+    const float ol = __shfl_xor(lsum, off, 64);
+    const float m_new = fmaxf(mmax, om);
+    lsum = (mmax == -INFINITY ? 0.f : lsum * fast_exp2(mmax - m_new)) +
+           (om == -INFINITY ? 0.f : ol * fast_exp2(om - m_new));
+    mmax = m_new;
+  }
 
+  // pass 2: sum_c 2^(m_c - M) O_c, eight chunks' loads in flight at a time
   const float* po = p.part_o + ((int64_t)cstart * p.num_qo_heads + hq) * D + lane * PER;
   const int64_t po_stride = (int64_t)p.num_qo_heads * D;
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
-#pragma unroll 4
-  for (int c = 0; c < nchunks; ++c) {
-    const float w = fast_exp2(ml[c * ml_stride] - mmax);
+  for (int c0 = 0; c0 < nchunks; c0 += 8) {
+    float mc[8];
+    float oc[8][PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) acc[j] += w * po[c * po_stride + j];
+    for (int k = 0; k < 8; ++k) {
+      const int c = min(c0 + k, nchunks - 1);
+      mc[k] = ml[c * ml_stride];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) oc[k][j] = po[c * po_stride + j];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float w = c0 + k < nchunks ? fast_exp2(mc[k] - mmax) : 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] += w * oc[k][j];
+    }
   }
   const float inv = 1.f / lsum;
   OutVec w16;
@@ -476,9 +506,15 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, hipStream_t s) {
 using namespace nslg;
 
 extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
-                                                   int32_t head_dim, int64_t total_pages,
-                                                   int32_t page_size) {
-  if (batch <= 0 || num_qo_heads <= 0 || head_dim <= 0 || total_pages < 0 || page_size <= 0) return 0;
+                                                   int32_t num_kv_heads, int32_t head_dim,
+                                                   int64_t total_pages, int32_t page_size,
+                                                   int32_t dtype) {
+  (void)dtype;
+  if (batch <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || total_pages < 0 ||
+      page_size <= 0)
+    return 0;
+  if (num_qo_heads % num_kv_heads) return 0;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
   const int64_t total_tokens = total_pages * page_size;
   const int ct = choose_chunk_tokens(total_tokens, page_size);
   const int64_t mc = max_chunks_for(batch, total_tokens, ct);
@@ -516,7 +552,8 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
   const int ct = choose_chunk_tokens(total_tokens, page_size);
   const int64_t mc = max_chunks_for(batch, total_tokens, ct);
-  const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, head_dim, total_pages, page_size);
+  const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, total_pages,
+                                                       page_size, dtype);
   if (!workspace || workspace_bytes < need)
     return fail(NSLG_EWORKSPACE, "paged_decode: workspace %zu < %zu bytes", workspace_bytes, need);
   if (((uintptr_t)workspace) & 255) return fail(NSLG_EINVAL, "paged_decode: workspace must be 256-byte aligned");

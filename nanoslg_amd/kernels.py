@@ -150,22 +150,23 @@ def gather_kv(k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Ten
 
 
 class Workspace:
-    """Caller-owned device scratch for the attention kernels; grows on demand."""
+    """Caller-owned device scratch for the attention kernels; grows on demand.
+    One call at a time may use a workspace (zero-filled when allocated)."""
 
     def __init__(self, device: torch.device, nbytes: int = 0):
         self.device = torch.device(device)
-        self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf.numel() < nbytes:
-            self.buf = torch.empty(int(nbytes * 1.25) + 256, dtype=torch.uint8, device=self.device)
+            self.buf = torch.zeros(int(nbytes * 1.25) + 256, dtype=torch.uint8, device=self.device)
         return self.buf
 
 
-def paged_decode_workspace_size(batch: int, num_qo_heads: int, head_dim: int, total_pages: int,
-                                page_size: int) -> int:
-    return int(_lib.load().nslg_paged_decode_workspace_size(batch, num_qo_heads, head_dim, total_pages,
-                                                            page_size))
+def paged_decode_workspace_size(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                                total_pages: int, page_size: int, dtype: torch.dtype) -> int:
+    return int(_lib.load().nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim,
+                                                            total_pages, page_size, dtype_code(dtype)))
 
 
 def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
@@ -192,7 +193,7 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     if out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D or out.dtype != q.dtype:
         raise ValueError("paged_decode: bad out tensor")
     lib = _lib.load()
-    need = int(lib.nslg_paged_decode_workspace_size(B, Hq, D, int(total_pages), ps))
+    need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(total_pages), ps, dtype_code(q.dtype)))
     ws = (workspace or Workspace(q.device)).get(need)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,

@@ -198,14 +198,38 @@ class KVCacheManager(ABC):
 # --------------------------------------------------------------------------------------
 
 
+_COPY_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
+
+
+def _copy_stream(device: torch.device) -> "torch.cuda.Stream":
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _COPY_STREAMS.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=idx)  # default priority
+        _COPY_STREAMS[idx] = st
+    return st
+
+
 def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Tensor]:
-    """Concatenate int32 arrays, copy once host->device (pinned, async), return views."""
+    """Concatenate int32 arrays, copy once host->device, return views.
+
+    On a GPU the copy runs from pinned memory on a side stream, so it overlaps the
+    kernels still queued on the compute stream; the compute stream waits for it
+    only where the plan is first used."""
     sizes = [int(p.size) for p in parts]
     flat = np.concatenate([np.asarray(p, dtype=np.int32).reshape(-1) for p in parts]) if parts else \
         np.zeros(0, np.int32)
     host = torch.from_numpy(flat)
     if device.type == "cuda":
-        dev = host.pin_memory().to(device, non_blocking=True)
+        main = torch.cuda.current_stream(device)
+        side = _copy_stream(device)
+        pinned = host.pin_memory()
+        # the destination comes from the side stream's pool and is recorded on the
+        # compute stream, so the allocator never hands it out while still in use
+        with torch.cuda.stream(side):
+            dev = pinned.to(device, non_blocking=True)
+        main.wait_stream(side)
+        dev.record_stream(main)
     else:
         dev = host.clone()
     out, off = [], 0

@@ -56,9 +56,10 @@ def test_host_side_argument_checks():
 def test_decode_workspace_size_monotone():
     from nanoslg_amd import _lib
     lib = _lib.load()
-    a = lib.nslg_paged_decode_workspace_size(4, 32, 128, 640, 16)
-    b = lib.nslg_paged_decode_workspace_size(64, 32, 128, 44000, 16)
+    a = lib.nslg_paged_decode_workspace_size(4, 32, 8, 128, 640, 16, 0)
+    b = lib.nslg_paged_decode_workspace_size(64, 64, 8, 128, 44000, 16, 0)  # group 8 vs 4
     assert 0 < a < b < (64 << 20)
+    assert lib.nslg_paged_decode_workspace_size(4, 32, 8, 100, 640, 16, 0) == 0  # unsupported D
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):

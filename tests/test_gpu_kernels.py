@@ -285,3 +285,28 @@ def test_prefill_sequence_without_new_tokens():
     _log("prefill n=0 rows")
     out, ref = _prefill_case([50, 20, 33], [5, 0, 33], 32, 8, 128, 16, torch.float16, seed=52, scale=0.1)
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_decode_workspace_reuse_across_calls():
+    """One workspace serves a sequence of different batches (split-K partials of a
+    call never leak into the next)."""
+    _log("decode workspace reuse")
+    from nanoslg_amd.kernels import Workspace
+    ws = Workspace(torch.device(DEV))
+    cases = [([32768, 2048, 9000, 16], 60), ([5, 64, 129, 700], 61), ([20000] * 8, 62), ([1, 3000], 63),
+             ([32768, 2048, 9000, 16], 60)]
+    for lens, seed in cases:
+        g = torch.Generator().manual_seed(seed)
+        ps, Hq, Hkv, D = 16, 32, 8, 128
+        npg = sum(math.ceil(L / ps) for L in lens)
+        P = npg + 8
+        k = torch.randn(P, ps, Hkv, D, generator=g).half()
+        v = torch.randn(P, ps, Hkv, D, generator=g).half()
+        q = torch.randn(len(lens), Hq, D, generator=g).half()
+        tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, seed)
+        out = _k().paged_decode(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(indptr).to(DEV),
+                                torch.from_numpy(indices).to(DEV), torch.from_numpy(lpl).to(DEV),
+                                int(indptr[-1]), workspace=ws)
+        ref = O.paged_attention_ref([q[b:b + 1] for b in range(len(lens))], k.view(-1, Hkv, D),
+                                    v.view(-1, Hkv, D), ps, indptr, indices, lpl, [1] * len(lens))
+        torch.testing.assert_close(out.cpu().float(), torch.stack([r[0] for r in ref]), atol=ATOL, rtol=RTOL)
