@@ -9,11 +9,13 @@ step of that layer through the drop-in API (begin_forward -> attend -> end_forwa
 plan upload, K/V append kernel, split-K decode kernel and merge.
 
 Prints ONE JSON line. `value` = algorithmic HBM bytes per step / wall time per
-step (GB/s). `roofline` = the decode kernel alone, timed with HIP events on its
-stream. `cpu_baseline` = the CPU restatement of the reference's contiguous SDPA
-path on a bounded sample of the same workload, on this host's cores.
+step (GB/s). `roofline` = the nslg_paged_decode call (split-K decode kernel + merge
+kernel), timed with HIP events on its stream around every call of the timed steps.
+`cpu_baseline` = the CPU restatement of the reference's contiguous SDPA path on a
+bounded sample of the same workload, on this host's cores.
 
-  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch|radix|prefill]
+  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch]
+  python bench.py --workload copy_calibration   (a plain 1 GiB copy, for counter scaling)
 """
 from __future__ import annotations
 
@@ -28,6 +30,11 @@ import numpy as np
 
 HQ, HKV, D, PS = 32, 8, 128, 16
 HBM_PEAK_GBS = 8000.0
+
+# HBM bytes per nslg_paged_decode call (split-K kernel + merge) from the FETCH_SIZE and
+# WRITE_SIZE counters, each scaled by what the counter reads for a plain copy of known
+# size; profiles/paged_decode_hbm_traffic_kv_pressure_b64.md holds the runs.
+MEASURED_TRAFFIC = {}
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -37,10 +44,9 @@ def _parse():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--workload", default="kv_pressure",
-                    choices=["kv_pressure", "small_batch", "radix", "prefill"])
+                    choices=["kv_pressure", "small_batch", "radix", "prefill", "copy_calibration"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-reps", type=int, default=50)
     return ap.parse_args()
 
 
@@ -147,6 +153,15 @@ def step_bytes(lens_after, B, total_pages):
     return kv, append, qo, csr
 
 
+def decode_call_bytes(lens_after, B, total_pages):
+    """Algorithmic HBM bytes of one nslg_paged_decode call: K and V of every cached
+    token once, q read and out written once, the CSR block table once."""
+    kv = sum(lens_after) * HKV * D * 2 * 2
+    qo = B * HQ * D * 2 * 2
+    csr = 4 * (total_pages + 2 * B + 1)
+    return kv + qo + csr
+
+
 def kv_pressure_lens(seed, B=64):
     rng = np.random.default_rng(seed)
     return [int(round(math.exp(x))) for x in rng.uniform(math.log(2048), math.log(32768), size=B)]
@@ -155,51 +170,55 @@ def kv_pressure_lens(seed, B=64):
 # --------------------------------------------------------------------------- measurement
 
 
-def time_decode_kernel(w: DecodeWorkload, reps: int):
-    """Average duration of one paged_decode call (split-K kernel + merge) on the last
-    step's plan, with HIP events recorded on the launch stream."""
-    torch = w.torch
-    from nanoslg_amd import kernels
-    ctx = w.last_ctx
-    plan = ctx.plan
-    pool = w.mgr.pool
-    q = w.q[0][:, 0]
-    out = torch.empty(w.B, HQ, D, dtype=torch.float16, device="cuda:0")
-    stream = torch.cuda.current_stream()
-    for _ in range(3):
-        kernels.paged_decode(q, pool.k[0], pool.v[0], plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                             out=out, workspace=w.mgr.workspace)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
+class EventTimedKernels:
+    """The kernel module with nslg_paged_decode bracketed by HIP events on the stream it
+    is launched on, so the decode call is timed live inside the timed steps."""
+
+    def __init__(self, kernels):
+        import torch
+        self._k = kernels
+        self._torch = torch
+        self.events = []
+        self.recording = False
+
+    def __getattr__(self, name):
+        return getattr(self._k, name)
+
+    def paged_decode(self, *args, **kw):
+        if not self.recording:
+            return self._k.paged_decode(*args, **kw)
+        torch = self._torch
+        stream = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        kernels.paged_decode(q, pool.k[0], pool.v[0], plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                             out=out, workspace=w.mgr.workspace)
+        out = self._k.paged_decode(*args, **kw)
         b.record(stream)
-    torch.cuda.synchronize()
-    ms = [a.elapsed_time(b) for a, b in evs]
-    lens = [int(x) for x in ctx.seq_lens]
-    kv = sum(lens) * HKV * D * 2 * 2
-    qo = w.B * HQ * D * 2 * 2
-    csr = 4 * (plan.total_pages + 2 * w.B + 1)
-    return float(np.median(ms)), float(np.mean(ms)), kv + qo + csr
+        self.events.append((a, b))
+        return out
+
+    def mean_ms(self):
+        return float(np.mean([a.elapsed_time(b) for a, b in self.events]))
 
 
-def stream_read_ceiling():
-    """Measured HBM read rate of a plain reduction over 4 GiB (context for the roofline)."""
+def copy_calibration():
+    """A plain 1 GiB device-to-device copy (torch's copy kernel), for scaling the
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
     import torch
-    x = torch.empty(2 << 30, dtype=torch.float16, device="cuda:0").fill_(1.0)
+    n = 1 << 30
+    x = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(4):
+        y.copy_(x)
     torch.cuda.synchronize()
-    x.sum()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(5):
-        x.sum()
+    for _ in range(8):
+        y.copy_(x)
     e.record()
     torch.cuda.synchronize()
-    gbs = 5 * x.numel() * 2 / (s.elapsed_time(e) * 1e-3) / 1e9
-    del x
-    torch.cuda.empty_cache()
-    return gbs
+    ms = s.elapsed_time(e) / 8
+    return {"workload": "copy_calibration", "bytes_read": n, "bytes_written": n,
+            "ms_per_copy": round(ms, 4), "GB_s": round(2 * n / (ms * 1e-3) / 1e9, 1)}
 
 
 def cpu_baseline_sample(lens, seed, budget_s=12.0, max_steps=32):
@@ -279,12 +298,17 @@ def run_decode(args):
                "pool_pages": 65536, "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D,
                "layers": 1, "seed": args.seed}
     _log(f"workload {w.name}: B={w.B} pages={w.mgr.cfg.max_pages} sum(L)={sum(lens)}")
+    from nanoslg_amd import kernels
+    timed = EventTimedKernels(kernels)
+    w.mgr.kernels = timed
     for _ in range(args.warmup):
         w.step()
     torch.cuda.synchronize()
+    timed.recording = True
     lens_before = w.seq_lens()
     churn_at = args.steps // 2 if w.churn_frac > 0 else -1
     nbytes = [0, 0, 0, 0]
+    kbytes = 0
     churn_s = 0.0
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -299,17 +323,21 @@ def run_decode(args):
         tp = sum(math.ceil(L / PS) for L in lens_i)
         for j, x in enumerate(step_bytes(lens_i, w.B, tp)):
             nbytes[j] += x
+        kbytes += decode_call_bytes(lens_i, w.B, tp)
         w.step()
     torch.cuda.synchronize()
+    timed.recording = False
     wall = time.perf_counter() - t0 - churn_s
     ms_step = wall / args.steps * 1e3
     total_bytes = sum(nbytes)
     value = total_bytes / wall / 1e9
     _log(f"{args.steps} steps in {wall*1e3:.1f} ms -> {ms_step:.3f} ms/step, {value:.1f} GB/s")
 
-    med_ms, mean_ms, kbytes = time_decode_kernel(w, args.kernel_reps)
+    mean_ms = timed.mean_ms()
+    kbytes /= args.steps
     achieved = kbytes / (mean_ms * 1e-3) / 1e9
-    _log(f"decode kernel: mean {mean_ms*1e3:.1f} us, median {med_ms*1e3:.1f} us, {achieved:.1f} GB/s")
+    _log(f"decode call: mean {mean_ms*1e3:.1f} us over {len(timed.events)} launches, {achieved:.1f} GB/s")
+    traffic = MEASURED_TRAFFIC.get(w.name)
     res = {
         "metric": "paged decode attn+append: achieved HBM GB/s (% of peak) and decode tok/s/layer",
         "value": round(value, 2),
@@ -334,7 +362,7 @@ def run_decode(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "avg_launch_us": round(mean_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": int(kbytes),
         },
@@ -353,6 +381,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
+    if args.workload == "copy_calibration":
+        print(json.dumps(copy_calibration()), flush=True)
+        return
     if args.workload in ("kv_pressure", "small_batch"):
         res, lens = run_decode(args)
     else:

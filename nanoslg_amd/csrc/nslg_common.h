@@ -87,6 +87,23 @@ __device__ inline float wave_xor_sum(float x, int mask) {
   return x + __shfl_xor(x, mask, 64);
 }
 
+// Reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48) with
+// gfx950's row-swap permutes: v_permlane16_swap(x, x) leaves rows {0,0,2,2} in one
+// result and {1,1,3,3} in the other, v_permlane32_swap(x, x) rows {0,1,0,1} and
+// {2,3,2,3}. VALU only: no LDS instruction, no wait on the LDS counter.
+__device__ inline float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace nslg

@@ -2,14 +2,15 @@
 // log-sum-exp merge of the splits.
 //
 // Work decomposition
-//   The sequences' tokens are cut into chunks of `chunk_tokens` (a multiple of
-//   16). Workgroup x = global chunk id, workgroup y = group of KV heads; each
-//   wave owns one (chunk, kv head) and works alone: no LDS, no barriers. A
-//   sequence of L tokens gets ceil(L / chunk_tokens) chunks, so a 32k-token
-//   sequence gets 64x the waves of a 512-token one and the grid stays balanced
-//   under log-uniform lengths. Each wave finds its sequence by a wave-wide
-//   prefix sum over the per-sequence chunk counts (kv_indptr is a few hundred
-//   bytes and L2-resident), so no separate planning launch is needed.
+//   Each sequence's tokens are cut into ceil(L / chunk_tokens) chunks of equal
+//   length (boundaries on 16-token tiles). Workgroup x of the 1-D grid is
+//   (chunk, group of KV heads); each wave owns one (chunk, KV head) and works
+//   alone: no LDS, no barriers. chunk_tokens is chosen on the host so that the
+//   whole grid fits the device's resident workgroup slots at once: every wave
+//   starts at launch and streams one long chunk, and no second, partly filled
+//   round of workgroups trails the first. A wave finds its sequence by a
+//   wave-wide prefix sum over the per-sequence chunk counts (kv_indptr is a few
+//   hundred bytes and L2-resident), so no separate planning launch is needed.
 //
 // Per 16-token tile (one page at page_size 16), for the G query heads of the
 // wave's KV head (G = Hq/Hkv <= 16):
@@ -23,12 +24,15 @@
 //     A = V^T: lane l loads tokens 4(l/16)+j (j=0..3), 16 B at d = (D/16)*(l%16), so each
 //     load instruction reads 4 whole 256 B rows; output tile n then holds
 //     d = (D/16)*row + n, a permutation undone when the result is stored.
-// K and V of the next tile are loaded before the current tile is computed.
+// K and V of the next tile are loaded before the current tile is computed; page
+// ids arrive through the scalar cache one page ahead of their use.
 //
 // HBM traffic per (token, kv head): 2*D*2 bytes (K and V, read once).
 #include "nslg_common.h"
 
 #include <math.h>
+
+#include <atomic>
 
 namespace nslg {
 namespace {
@@ -52,6 +56,7 @@ struct DecodeParams {
   float scale_log2;
   int32_t chunk_tokens;
   int32_t max_chunks;
+  int32_t head_groups;  // workgroups per chunk
   uint16_t* out;
   int64_t out_stride;
   float* part_o;   // [max_chunks, Hq, D]
@@ -184,19 +189,23 @@ paged_decode_kernel(DecodeParams p) {
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;  // P = hi + lo for bf16's 8-bit mantissa
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int chunk = blockIdx.x / p.head_groups;
+  const int h = (blockIdx.x - chunk * p.head_groups) * (blockDim.x >> 6) + wave;
   if (h >= p.num_kv_heads) return;
 
   int b = 0, cstart = 0, nchunks = 0;
-  if (!locate_chunk(p.indptr, p.last_len, p.batch, p.page_size, p.chunk_tokens, blockIdx.x, b,
-                    cstart, nchunks))
+  if (!locate_chunk(p.indptr, p.last_len, p.batch, p.page_size, p.chunk_tokens, chunk, b, cstart,
+                    nchunks))
     return;
   b = __builtin_amdgcn_readfirstlane(b);
   cstart = __builtin_amdgcn_readfirstlane(cstart);
   nchunks = __builtin_amdgcn_readfirstlane(nchunks);
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
-  const int t_begin = (blockIdx.x - cstart) * p.chunk_tokens;
-  const int t_end = min(t_begin + p.chunk_tokens, len);
+  // chunk c of the sequence's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
+  const int ntiles_seq = (len + 15) >> 4;
+  const int c_local = chunk - cstart;
+  const int t_begin = 16 * (int)((int64_t)c_local * ntiles_seq / nchunks);
+  const int t_end = min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
   const int t_last = t_end - 1;
   const int32_t* idx = p.indices + p.indptr[b];
 
@@ -235,8 +244,7 @@ paged_decode_kernel(DecodeParams p) {
       for (int j = 0; j < 4; ++j) sv[j] = (t0 + 4 * gq + j < t_end) ? s[j] * p.scale_log2 : -INFINITY;
     }
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = wave_xor_max(mx, 16);
-    mx = wave_xor_max(mx, 32);
+    mx = rows_max(mx);
     if (__ballot(mx > m_run + kRescaleSlack)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
@@ -272,41 +280,47 @@ paged_decode_kernel(DecodeParams p) {
   const int n_tiles = (t_end - t_begin + 15) >> 4;
   Tile<D> buf[kDepth];
   if constexpr (kTileInPage) {
-    // Every tile lies inside one page. The chunk touches at most 64 pages (the host
-    // caps chunk_tokens), whose ids sit one per lane; each tile's id is broadcast
-    // to a scalar register, so page lookups never wait on the K/V loads in flight.
+    // Every tile lies inside one page. Page ids are wave-uniform and come through the
+    // scalar cache: the id of the page after the current one is loaded while the
+    // current page's tiles stream, so a page lookup never waits on K/V loads.
     const int ps = p.page_size;
     const int row_bytes = p.num_kv_heads * D * 2;
     const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
     const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
     const int first_page = t_begin / ps;
-    const int np_seq = p.indptr[b + 1] - p.indptr[b];
-    int pid_vec = 0;
-    if (first_page + lane < np_seq) {
-      pid_vec = idx[first_page + lane];
-      if (pid_vec < 0 || (int64_t)pid_vec >= p.num_pages) pid_vec = 0;
-    }
+    const int32_t* pidx = idx + first_page;
+    const int np_chunk = (p.indptr[b + 1] - p.indptr[b]) - first_page;
+    auto page_id = [&](int i) -> int { return pidx[i < np_chunk ? i : np_chunk - 1]; };
     int ld_tile = 0;
     int page_ld = 0;
     int slot_ld = t_begin - first_page * ps;
+    int pid_cur = page_id(0);
+    int pid_next = page_id(1);
     const char* kb = kpool;
     const char* vb = vpool;
     int last = 0;
+    // Address from pid_cur, the tile's loads, and only then the bookkeeping and the
+    // next scalar load: scalar loads complete out of order, so a use of an older id
+    // issued after a newer load would wait for the newer one too.
     auto issue = [&](Tile<D>& dst) {
       if (ld_tile < n_tiles) {
-        const int pid = __builtin_amdgcn_readlane(pid_vec, page_ld);
+        const int pid = (pid_cur < 0 || (int64_t)pid_cur >= p.num_pages) ? 0 : pid_cur;
         const int64_t row0 = (int64_t)pid * ps + slot_ld;
         kb = kpool + row0 * row_bytes;
         vb = vpool + row0 * row_bytes;
         last = min(15, t_last - (t_begin + 16 * ld_tile));
-        slot_ld += 16;
-        if (slot_ld == ps) {
-          slot_ld = 0;
-          ++page_ld;
-        }
-        ++ld_tile;
       }
       load_tile_rows<D>(kb, vb, row_bytes, last, dst);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ld_tile < n_tiles) {
+        slot_ld += 16;
+        const bool cross = slot_ld == ps;
+        slot_ld = cross ? 0 : slot_ld;
+        page_ld += cross ? 1 : 0;
+        pid_cur = cross ? pid_next : pid_cur;
+        ++ld_tile;
+      }
+      pid_next = page_id(page_ld + 1);
     };
 #pragma unroll
     for (int j = 0; j < kDepth - 1; ++j) issue(buf[j]);
@@ -339,8 +353,7 @@ paged_decode_kernel(DecodeParams p) {
     }
   }
 
-  float l_tot = wave_xor_sum(l_run, 16);
-  l_tot = wave_xor_sum(l_tot, 32);
+  const float l_tot = rows_sum(l_run);
   if (!head_ok) return;
 
   // Lane l holds O[head r][d = NT*(4*gq + i) + n] in o[n][i].
@@ -355,7 +368,7 @@ paged_decode_kernel(DecodeParams p) {
       *reinterpret_cast<typename RowVec<NT>::type*>(orow + NT * (4 * gq + i)) = w;
     }
   } else {
-    const int64_t slot = (int64_t)blockIdx.x * p.num_qo_heads + hq;
+    const int64_t slot = (int64_t)chunk * p.num_qo_heads + hq;
     float* prow = p.part_o + slot * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -470,26 +483,71 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
   *reinterpret_cast<OutVec*>(orow) = w16;
 }
 
-// Tokens per split: about 1024 splits over the whole batch, at least 64 tokens,
-// a multiple of 16, and (page sizes that are multiples of 16) at most 63 pages.
-inline int choose_chunk_tokens(int64_t total_tokens, int page_size) {
-  int64_t c = (total_tokens + 1023) / 1024;
-  c = ((c + 15) / 16) * 16;
-  if (c < 64) c = 64;
-  // page-aligned tiles: a chunk may touch at most 64 pages (one page id per lane)
-  if (page_size % 16 == 0 && c > 63LL * page_size) c = 63LL * page_size;
-  if (c > (1 << 20)) c = 1 << 20;
-  return (int)c;
+// Resident workgroup slots of the decode kernel on the current device (CUs x
+// workgroups per CU at its register footprint), cached per device and variant.
+// Without a device (a host-only process sizing a workspace) the MI355X figure
+// is used: 256 CUs x 3 workgroups of 4 waves.
+constexpr int kMaxDevices = 64;
+constexpr int kDefaultSlots = 768;
+
+template <typename T, int D, bool kTileInPage>
+int decode_wg_slots(int waves) {
+  static std::atomic<int> cache[kMaxDevices][kMaxWaves + 1];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return kDefaultSlots;
+  }
+  int v = cache[dev][waves].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, kTileInPage, 2>,
+                                                   64 * waves, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0) {
+    (void)hipGetLastError();
+    return kDefaultSlots;
+  }
+  v = cus * per_cu;
+  cache[dev][waves].store(v, std::memory_order_relaxed);
+  return v;
 }
 
-inline int64_t max_chunks_for(int32_t batch, int64_t total_tokens, int chunk_tokens) {
-  return (total_tokens + chunk_tokens - 1) / chunk_tokens + batch;
+struct DecodeShape {
+  int waves;        // waves (KV heads) per workgroup
+  int head_groups;  // workgroups per chunk
+  int chunk_tokens;
+  int64_t max_chunks;
+};
+
+// Chunk length for `total_tokens` (an upper bound of the batch's tokens) over
+// `batch` sequences: sequence b gets ceil(L_b / chunk_tokens) chunks, at most
+// total/chunk_tokens + batch in all, so chunk_tokens = total / (capacity - batch)
+// keeps every chunk of the grid resident at once. A batch too large for that
+// (capacity <= 2 * batch) gets about `capacity` chunks per round instead. At least
+// 64 tokens and a multiple of 16 (tiles never straddle a chunk boundary).
+template <typename T, int D>
+DecodeShape decode_shape(int32_t batch, int32_t num_kv_heads, int64_t total_tokens, int page_size) {
+  DecodeShape sh;
+  sh.waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
+  sh.head_groups = (num_kv_heads + sh.waves - 1) / sh.waves;
+  const int slots = page_size % 16 == 0 ? decode_wg_slots<T, D, true>(sh.waves)
+                                        : decode_wg_slots<T, D, false>(sh.waves);
+  int64_t capacity = slots / sh.head_groups;
+  if (capacity < 1) capacity = 1;
+  int64_t usable = capacity > 2 * (int64_t)batch ? capacity - batch : capacity;
+  int64_t c = (total_tokens + usable - 1) / usable;
+  c = ((c + 15) / 16) * 16;
+  if (c < 64) c = 64;
+  if (c > ((int64_t)1 << 30)) c = (int64_t)1 << 30;
+  sh.chunk_tokens = (int)c;
+  sh.max_chunks = (total_tokens + c - 1) / c + batch;
+  return sh;
 }
 
 template <typename T, int D>
-int launch_decode(const DecodeParams& p, const MergeParams& mp, hipStream_t s) {
-  const int waves = p.num_kv_heads < kMaxWaves ? p.num_kv_heads : kMaxWaves;
-  dim3 grid(p.max_chunks, (p.num_kv_heads + waves - 1) / waves);
+int launch_decode(const DecodeParams& p, const MergeParams& mp, int waves, hipStream_t s) {
+  const dim3 grid((unsigned)(p.max_chunks * (int64_t)p.head_groups));
   if (p.page_size % 16 == 0)
     paged_decode_kernel<T, D, true, 2><<<grid, 64 * waves, 0, s>>>(p);
   else
@@ -498,6 +556,16 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, hipStream_t s) {
   if (rc) return rc;
   decode_merge_kernel<T, D><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp);
   return check_launch("paged_decode_merge");
+}
+
+template <typename T>
+DecodeShape decode_shape_for(int32_t head_dim, int32_t batch, int32_t num_kv_heads, int64_t total_tokens,
+                             int page_size) {
+  switch (head_dim) {
+    case 64: return decode_shape<T, 64>(batch, num_kv_heads, total_tokens, page_size);
+    case 128: return decode_shape<T, 128>(batch, num_kv_heads, total_tokens, page_size);
+    default: return decode_shape<T, 256>(batch, num_kv_heads, total_tokens, page_size);
+  }
 }
 
 }  // namespace
@@ -509,16 +577,16 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
                                                    int32_t num_kv_heads, int32_t head_dim,
                                                    int64_t total_pages, int32_t page_size,
                                                    int32_t dtype) {
-  (void)dtype;
   if (batch <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || total_pages < 0 ||
       page_size <= 0)
     return 0;
   if (num_qo_heads % num_kv_heads) return 0;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
   const int64_t total_tokens = total_pages * page_size;
-  const int ct = choose_chunk_tokens(total_tokens, page_size);
-  const int64_t mc = max_chunks_for(batch, total_tokens, ct);
-  return (size_t)(mc * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
+  const DecodeShape sh = dtype == NSLG_BF16
+                             ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
+                             : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
+  return (size_t)(sh.max_chunks * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
 }
 
 extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_pool,
@@ -550,8 +618,11 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
     return fail(NSLG_EINVAL, "paged_decode: q/pool/out must be 16-byte aligned");
   const int64_t total_tokens = total_pages * page_size;
   if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
-  const int ct = choose_chunk_tokens(total_tokens, page_size);
-  const int64_t mc = max_chunks_for(batch, total_tokens, ct);
+  const DecodeShape sh = dtype == NSLG_BF16
+                             ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
+                             : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
+  const int ct = sh.chunk_tokens;
+  const int64_t mc = sh.max_chunks;
   const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, total_pages,
                                                        page_size, dtype);
   if (!workspace || workspace_bytes < need)
@@ -575,6 +646,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.chunk_tokens = ct;
   p.max_chunks = (int32_t)mc;
+  p.head_groups = sh.head_groups;
   p.out = (uint16_t*)out;
   p.out_stride = out_stride;
   float* ws = (float*)workspace;
@@ -597,14 +669,14 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) {
     switch (head_dim) {
-      case 64: return launch_decode<F16, 64>(p, mp, s);
-      case 128: return launch_decode<F16, 128>(p, mp, s);
-      default: return launch_decode<F16, 256>(p, mp, s);
+      case 64: return launch_decode<F16, 64>(p, mp, sh.waves, s);
+      case 128: return launch_decode<F16, 128>(p, mp, sh.waves, s);
+      default: return launch_decode<F16, 256>(p, mp, sh.waves, s);
     }
   }
   switch (head_dim) {
-    case 64: return launch_decode<BF16, 64>(p, mp, s);
-    case 128: return launch_decode<BF16, 128>(p, mp, s);
-    default: return launch_decode<BF16, 256>(p, mp, s);
+    case 64: return launch_decode<BF16, 64>(p, mp, sh.waves, s);
+    case 128: return launch_decode<BF16, 128>(p, mp, sh.waves, s);
+    default: return launch_decode<BF16, 256>(p, mp, sh.waves, s);
   }
 }

@@ -264,8 +264,7 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
             sv[j] = vis ? sacc[j] * p.scale_log2 : -INFINITY;
           }
           float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-          mx = wave_xor_max(mx, 16);
-          mx = wave_xor_max(mx, 32);
+          mx = rows_max(mx);
           if (__ballot(mx > m_run[cb] + kRescaleSlack)) {
             const float m_new = fmaxf(m_run[cb], mx);
             const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[cb] - m_new);
@@ -312,8 +311,7 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
   // ---- epilogue: normalise and store rows ----------------------------------------
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    float l_tot = wave_xor_sum(l_run[cb], 16);
-    l_tot = wave_xor_sum(l_tot, 32);
+    const float l_tot = rows_sum(l_run[cb]);
     if (!row_ok[cb]) continue;
     const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
     const int t = row / G;

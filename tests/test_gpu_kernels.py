@@ -310,3 +310,44 @@ def test_decode_workspace_reuse_across_calls():
         ref = O.paged_attention_ref([q[b:b + 1] for b in range(len(lens))], k.view(-1, Hkv, D),
                                     v.view(-1, Hkv, D), ps, indptr, indices, lpl, [1] * len(lens))
         torch.testing.assert_close(out.cpu().float(), torch.stack([r[0] for r in ref]), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("lens,Hq,Hkv,D,ps", [
+    ([91, 51, 18], 32, 8, 128, 16),
+    ([32768, 2048, 9000, 16, 300], 32, 8, 128, 16),
+    ([5000, 17, 2048], 8, 2, 64, 32),
+    ([4000, 129], 16, 1, 256, 8),
+    ([20000] * 8, 28, 4, 128, 16),
+])
+def test_decode_writes_stay_inside_workspace_and_out(lens, Hq, Hkv, D, ps):
+    """Every byte the decode call writes lies inside `out` and the sized workspace:
+    guard regions after both keep their fill pattern, and the result is correct."""
+    _log(f"decode guards {lens} Hq={Hq} Hkv={Hkv} D={D} ps={ps}")
+    import ctypes
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(70)
+    npg = sum(math.ceil(L / ps) for L in lens)
+    P = npg + 8
+    k = torch.randn(P, ps, Hkv, D, generator=g).half()
+    v = torch.randn(P, ps, Hkv, D, generator=g).half()
+    B = len(lens)
+    q = torch.randn(B, Hq, D, generator=g).half()
+    tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, 70)
+    need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(indptr[-1]), ps, 0))
+    guard = 1 << 20
+    ws = torch.full((need + guard,), 0xA5, dtype=torch.uint8, device=DEV)
+    out = torch.full((B + 4, Hq, D), -7.0, dtype=torch.float16, device=DEV)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    ip, ix, lp = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl))
+    rc = lib.nslg_paged_decode(qd.data_ptr(), Hq * D, kd.data_ptr(), vd.data_ptr(), P, ps, ip.data_ptr(),
+                               ix.data_ptr(), lp.data_ptr(), int(indptr[-1]), B, Hq, Hkv, D,
+                               1.0 / math.sqrt(D), 0, out.data_ptr(), Hq * D, ws.data_ptr(), need,
+                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert bool((ws[need:] == 0xA5).all()), "decode wrote past its workspace"
+    assert bool((out[B:] == -7.0).all()), "decode wrote past its output rows"
+    ref = O.paged_attention_ref([q[b:b + 1] for b in range(B)], k.view(-1, Hkv, D), v.view(-1, Hkv, D), ps,
+                                indptr, indices, lpl, [1] * B)
+    torch.testing.assert_close(out[:B].cpu().float(), torch.stack([r[0] for r in ref]), atol=ATOL, rtol=RTOL)
