@@ -3,14 +3,16 @@
 //
 // Work decomposition
 //   Each sequence's tokens are cut into ceil(L / chunk_tokens) chunks of equal
-//   length (boundaries on 16-token tiles). Workgroup x of the 1-D grid is
+//   length (boundaries on 16-token tiles). Workgroup (x, y) of the grid is
 //   (chunk, group of KV heads); each wave owns one (chunk, KV head) and works
-//   alone: no LDS, no barriers. chunk_tokens is chosen on the host so that the
-//   whole grid fits the device's resident workgroup slots at once: every wave
-//   starts at launch and streams one long chunk, and no second, partly filled
-//   round of workgroups trails the first. A wave finds its sequence by a
-//   wave-wide prefix sum over the per-sequence chunk counts (kv_indptr is a few
-//   hundred bytes and L2-resident), so no separate planning launch is needed.
+//   alone: no LDS, no barriers. The chunk length is the smallest one whose chunk
+//   count fits the device's resident workgroup slots (the host passes that
+//   budget; every wave finds the same length by a binary search over the
+//   sequence lengths), so every wave starts at launch and streams one long chunk
+//   and no second, partly filled round of workgroups trails the first. A wave
+//   finds its sequence by a wave-wide prefix sum over the per-sequence chunk
+//   counts (kv_indptr is a few hundred bytes and L2-resident), so no separate
+//   planning launch is needed.
 //
 // Per 16-token tile (one page at page_size 16), for the G query heads of the
 // wave's KV head (G = Hq/Hkv <= 16):
@@ -24,8 +26,7 @@
 //     A = V^T: lane l loads tokens 4(l/16)+j (j=0..3), 16 B at d = (D/16)*(l%16), so each
 //     load instruction reads 4 whole 256 B rows; output tile n then holds
 //     d = (D/16)*row + n, a permutation undone when the result is stored.
-// K and V of the next tile are loaded before the current tile is computed; page
-// ids arrive through the scalar cache one page ahead of their use.
+// K and V of the next tile are loaded before the current tile is computed.
 //
 // HBM traffic per (token, kv head): 2*D*2 bytes (K and V, read once).
 #include "nslg_common.h"
@@ -54,9 +55,11 @@ struct DecodeParams {
   int32_t num_kv_heads;
   int32_t group;  // Hq / Hkv
   float scale_log2;
-  int32_t chunk_tokens;
+  int32_t chunk_tokens;  // an upper bound that fits chunk_budget, or the length to use
+  int32_t chunk_budget;  // > 0: search the smallest length with <= this many chunks
   int32_t max_chunks;
-  int32_t head_groups;  // workgroups per chunk
+  int32_t head_groups;   // workgroups per chunk (grid y)
+  int32_t* chunk_out;    // the length used, for the merge launch
   uint16_t* out;
   int64_t out_stride;
   float* part_o;   // [max_chunks, Hq, D]
@@ -72,19 +75,80 @@ __device__ inline int seq_len_of(const int32_t* indptr, const int32_t* last_len,
   return (np - 1) * page_size + lpl;
 }
 
+__device__ inline int wave_sum_i32(int x) {
+  x += __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);  // row_ror:8
+  x += __builtin_amdgcn_mov_dpp(x, 0x124, 0xf, 0xf, false);  // row_ror:4
+  x += __builtin_amdgcn_mov_dpp(x, 0x122, 0xf, 0xf, false);  // row_ror:2
+  x += __builtin_amdgcn_mov_dpp(x, 0x121, 0xf, 0xf, false);  // row_ror:1
+  const auto a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  x = (int)(a[0] + a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return (int)(c[0] + c[1]);
+}
+
+// Sequence lengths as the lanes see them: lane l holds sequence 64 i + l of
+// the batch in v[i] for the first 256 sequences (loaded once, so the searches
+// below do not go back to memory); later ones are read on demand.
+struct LaneLens {
+  static constexpr int kRegs = 4;
+  int v[kRegs];
+  const int32_t* indptr;
+  const int32_t* last_len;
+  int batch;
+  int page_size;
+
+  __device__ LaneLens(const int32_t* ip, const int32_t* ll, int b, int ps)
+      : indptr(ip), last_len(ll), batch(b), page_size(ps) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < kRegs; ++i) {
+      const int s = 64 * i + lane;
+      v[i] = s < batch ? seq_len_of(indptr, last_len, s, page_size) : 0;
+    }
+  }
+  // length of sequence 64 i + lane (0 past the batch)
+  __device__ int at(int i) const {
+    if (i < kRegs) {
+      int r = v[0];
+#pragma unroll
+      for (int j = 1; j < kRegs; ++j) r = i == j ? v[j] : r;
+      return r;
+    }
+    const int s = 64 * i + (threadIdx.x & 63);
+    return s < batch ? seq_len_of(indptr, last_len, s, page_size) : 0;
+  }
+};
+
+// Smallest chunk length in [lo, hi] (multiples of 16) for which the batch's chunk
+// count sum_b ceil(L_b / len) is at most `budget`; `hi` is known to fit. The
+// count does not grow with the length, so a binary search finds it; all waves
+// compute the same value from the same lengths.
+__device__ inline int fit_chunk_tokens(const LaneLens& lens, int lo, int hi, int budget) {
+  int a = lo >> 4, z = hi >> 4;
+  const int groups = (lens.batch + 63) >> 6;
+  while (a < z) {
+    const int mid = (a + z) >> 1;
+    const int ct = mid << 4;
+    int cnt = 0;
+    for (int i = 0; i < groups; ++i) cnt += (lens.at(i) + ct - 1) / ct;
+    cnt = __builtin_amdgcn_readfirstlane(wave_sum_i32(cnt));
+    if (cnt <= budget)
+      z = mid;
+    else
+      a = mid + 1;
+  }
+  return a << 4;
+}
+
 // Wave-wide search for the sequence owning global chunk `g`.
-__device__ inline bool locate_chunk(const int32_t* indptr, const int32_t* last_len, int batch,
-                                    int page_size, int chunk_tokens, int g, int& b, int& cstart,
+__device__ inline bool locate_chunk(const LaneLens& lens, int chunk_tokens, int g, int& b, int& cstart,
                                     int& nchunks) {
   const int lane = threadIdx.x & 63;
   int base = 0;
-  for (int s0 = 0; s0 < batch; s0 += 64) {
-    const int s = s0 + lane;
-    int nc = 0;
-    if (s < batch) {
-      const int len = seq_len_of(indptr, last_len, s, page_size);
-      nc = (len + chunk_tokens - 1) / chunk_tokens;
-    }
+  const int groups = (lens.batch + 63) >> 6;
+  for (int i = 0; i < groups; ++i) {
+    const int len = lens.at(i);
+    const int nc = (len + chunk_tokens - 1) / chunk_tokens;
     int incl = nc;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -96,7 +160,7 @@ __device__ inline bool locate_chunk(const int32_t* indptr, const int32_t* last_l
     const unsigned long long m = __ballot(hit);
     if (m) {
       const int src = __ffsll((long long)m) - 1;
-      b = s0 + src;
+      b = 64 * i + src;
       cstart = base + __shfl(excl, src, 64);
       nchunks = __shfl(nc, src, 64);
       return true;
@@ -189,14 +253,16 @@ paged_decode_kernel(DecodeParams p) {
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;  // P = hi + lo for bf16's 8-bit mantissa
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int chunk = blockIdx.x / p.head_groups;
-  const int h = (blockIdx.x - chunk * p.head_groups) * (blockDim.x >> 6) + wave;
+  const int chunk = blockIdx.x;
+  const int h = blockIdx.y * (blockDim.x >> 6) + wave;
   if (h >= p.num_kv_heads) return;
 
+  const LaneLens lens(p.indptr, p.last_len, p.batch, p.page_size);
+  int ct = p.chunk_tokens;
+  if (p.chunk_budget > 0) ct = fit_chunk_tokens(lens, 64, ct, p.chunk_budget);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *p.chunk_out = ct;
   int b = 0, cstart = 0, nchunks = 0;
-  if (!locate_chunk(p.indptr, p.last_len, p.batch, p.page_size, p.chunk_tokens, chunk, b, cstart,
-                    nchunks))
-    return;
+  if (!locate_chunk(lens, ct, chunk, b, cstart, nchunks)) return;
   b = __builtin_amdgcn_readfirstlane(b);
   cstart = __builtin_amdgcn_readfirstlane(cstart);
   nchunks = __builtin_amdgcn_readfirstlane(nchunks);
@@ -280,47 +346,52 @@ paged_decode_kernel(DecodeParams p) {
   const int n_tiles = (t_end - t_begin + 15) >> 4;
   Tile<D> buf[kDepth];
   if constexpr (kTileInPage) {
-    // Every tile lies inside one page. Page ids are wave-uniform and come through the
-    // scalar cache: the id of the page after the current one is loaded while the
-    // current page's tiles stream, so a page lookup never waits on K/V loads.
+    // Every tile lies inside one page. The ids of a window of 128 pages sit one per
+    // lane in two registers and each tile's id is broadcast to a scalar register
+    // (readlane), so page lookups never wait behind the K/V loads in flight; a chunk
+    // longer than the window refills it once per 128 pages.
     const int ps = p.page_size;
     const int row_bytes = p.num_kv_heads * D * 2;
     const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
     const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
     const int first_page = t_begin / ps;
-    const int32_t* pidx = idx + first_page;
-    const int np_chunk = (p.indptr[b + 1] - p.indptr[b]) - first_page;
-    auto page_id = [&](int i) -> int { return pidx[i < np_chunk ? i : np_chunk - 1]; };
+    const int np_seq = p.indptr[b + 1] - p.indptr[b];
+    int win_lo = 0, win_hi = 0;  // window = pages [first_page + win_base, +128)
+    int win_base = 0;
+    auto load_window = [&]() {
+      const int pg0 = first_page + win_base + lane;
+      int a = pg0 < np_seq ? idx[pg0] : 0;
+      int c = pg0 + 64 < np_seq ? idx[pg0 + 64] : 0;
+      win_lo = (a < 0 || (int64_t)a >= p.num_pages) ? 0 : a;
+      win_hi = (c < 0 || (int64_t)c >= p.num_pages) ? 0 : c;
+    };
+    load_window();
     int ld_tile = 0;
-    int page_ld = 0;
+    int page_ld = 0;  // page of the next tile, relative to first_page
     int slot_ld = t_begin - first_page * ps;
-    int pid_cur = page_id(0);
-    int pid_next = page_id(1);
     const char* kb = kpool;
     const char* vb = vpool;
     int last = 0;
-    // Address from pid_cur, the tile's loads, and only then the bookkeeping and the
-    // next scalar load: scalar loads complete out of order, so a use of an older id
-    // issued after a newer load would wait for the newer one too.
     auto issue = [&](Tile<D>& dst) {
       if (ld_tile < n_tiles) {
-        const int pid = (pid_cur < 0 || (int64_t)pid_cur >= p.num_pages) ? 0 : pid_cur;
+        if (page_ld - win_base == 128) {
+          win_base += 128;
+          load_window();
+        }
+        const int j = page_ld - win_base;
+        const int pid = j < 64 ? __builtin_amdgcn_readlane(win_lo, j) : __builtin_amdgcn_readlane(win_hi, j - 64);
         const int64_t row0 = (int64_t)pid * ps + slot_ld;
         kb = kpool + row0 * row_bytes;
         vb = vpool + row0 * row_bytes;
         last = min(15, t_last - (t_begin + 16 * ld_tile));
-      }
-      load_tile_rows<D>(kb, vb, row_bytes, last, dst);
-      __builtin_amdgcn_sched_barrier(0);
-      if (ld_tile < n_tiles) {
         slot_ld += 16;
-        const bool cross = slot_ld == ps;
-        slot_ld = cross ? 0 : slot_ld;
-        page_ld += cross ? 1 : 0;
-        pid_cur = cross ? pid_next : pid_cur;
+        if (slot_ld == ps) {
+          slot_ld = 0;
+          ++page_ld;
+        }
         ++ld_tile;
       }
-      pid_next = page_id(page_ld + 1);
+      load_tile_rows<D>(kb, vb, row_bytes, last, dst);
     };
 #pragma unroll
     for (int j = 0; j < kDepth - 1; ++j) issue(buf[j]);
@@ -391,7 +462,7 @@ struct MergeParams {
   int32_t batch;
   int32_t page_size;
   int32_t num_qo_heads;
-  int32_t chunk_tokens;
+  const int32_t* chunk_in;  // the chunk length the decode launch used
   int32_t max_chunks;
   const float* part_o;
   const float* part_ml;
@@ -411,7 +482,8 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
   const int hq = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (hq >= p.num_qo_heads) return;
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
-  int nchunks = (len + p.chunk_tokens - 1) / p.chunk_tokens;
+  const int ct = max(16, *p.chunk_in);
+  int nchunks = (len + ct - 1) / ct;
   uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + lane * PER;
   if (nchunks == 0) {
     // A sequence with no tokens attends to nothing: its output rows are zero.
@@ -425,7 +497,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
   int before = 0;
   for (int s = lane; s < b; s += 64) {
     const int ls = seq_len_of(p.indptr, p.last_len, s, p.page_size);
-    before += (ls + p.chunk_tokens - 1) / p.chunk_tokens;
+    before += (ls + ct - 1) / ct;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off, 64);
@@ -514,18 +586,21 @@ int decode_wg_slots(int waves) {
 }
 
 struct DecodeShape {
-  int waves;        // waves (KV heads) per workgroup
-  int head_groups;  // workgroups per chunk
-  int chunk_tokens;
+  int waves;         // waves (KV heads) per workgroup
+  int head_groups;   // workgroups per chunk
+  int chunk_tokens;  // upper bound passed to the kernel
+  int chunk_budget;  // 0: no device-side search
   int64_t max_chunks;
 };
 
 // Chunk length for `total_tokens` (an upper bound of the batch's tokens) over
-// `batch` sequences: sequence b gets ceil(L_b / chunk_tokens) chunks, at most
-// total/chunk_tokens + batch in all, so chunk_tokens = total / (capacity - batch)
-// keeps every chunk of the grid resident at once. A batch too large for that
-// (capacity <= 2 * batch) gets about `capacity` chunks per round instead. At least
-// 64 tokens and a multiple of 16 (tiles never straddle a chunk boundary).
+// `batch` sequences. Sequence b gets ceil(L_b / len) chunks, at most
+// total / len + batch in all, so len = total / (capacity - batch) keeps every
+// chunk of the grid resident at once; the kernel then lowers it to the smallest
+// length that still fits `capacity` chunks for the actual lengths. A batch too
+// large for that (capacity <= 2 * batch) gets about `capacity` chunks per round
+// at the host's length. Lengths are multiples of 16 (tiles never straddle a
+// chunk) and at least 64.
 template <typename T, int D>
 DecodeShape decode_shape(int32_t batch, int32_t num_kv_heads, int64_t total_tokens, int page_size) {
   DecodeShape sh;
@@ -535,19 +610,21 @@ DecodeShape decode_shape(int32_t batch, int32_t num_kv_heads, int64_t total_toke
                                         : decode_wg_slots<T, D, false>(sh.waves);
   int64_t capacity = slots / sh.head_groups;
   if (capacity < 1) capacity = 1;
-  int64_t usable = capacity > 2 * (int64_t)batch ? capacity - batch : capacity;
+  const bool fit = capacity > 2 * (int64_t)batch;
+  const int64_t usable = fit ? capacity - batch : capacity;
   int64_t c = (total_tokens + usable - 1) / usable;
   c = ((c + 15) / 16) * 16;
   if (c < 64) c = 64;
   if (c > ((int64_t)1 << 30)) c = (int64_t)1 << 30;
   sh.chunk_tokens = (int)c;
-  sh.max_chunks = (total_tokens + c - 1) / c + batch;
+  sh.chunk_budget = fit ? (int)capacity : 0;
+  sh.max_chunks = fit ? capacity : (total_tokens + c - 1) / c + batch;
   return sh;
 }
 
 template <typename T, int D>
 int launch_decode(const DecodeParams& p, const MergeParams& mp, int waves, hipStream_t s) {
-  const dim3 grid((unsigned)(p.max_chunks * (int64_t)p.head_groups));
+  const dim3 grid((unsigned)p.max_chunks, (unsigned)p.head_groups);
   if (p.page_size % 16 == 0)
     paged_decode_kernel<T, D, true, 2><<<grid, 64 * waves, 0, s>>>(p);
   else
@@ -586,6 +663,8 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
   const DecodeShape sh = dtype == NSLG_BF16
                              ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
                              : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
+  // partials [max_chunks, Hq, D] and [max_chunks, Hq, 2] fp32, then 256 bytes holding
+  // the chunk length the decode launch chose
   return (size_t)(sh.max_chunks * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
 }
 
@@ -645,6 +724,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   p.group = group;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.chunk_tokens = ct;
+  p.chunk_budget = sh.chunk_budget;
   p.max_chunks = (int32_t)mc;
   p.head_groups = sh.head_groups;
   p.out = (uint16_t*)out;
@@ -652,6 +732,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   float* ws = (float*)workspace;
   p.part_o = ws;
   p.part_ml = ws + mc * num_qo_heads * head_dim;
+  p.chunk_out = reinterpret_cast<int32_t*>(ws + mc * num_qo_heads * (head_dim + 2));
 
   MergeParams mp;
   mp.indptr = kv_indptr;
@@ -659,7 +740,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   mp.batch = batch;
   mp.page_size = page_size;
   mp.num_qo_heads = num_qo_heads;
-  mp.chunk_tokens = ct;
+  mp.chunk_in = p.chunk_out;
   mp.max_chunks = (int32_t)mc;
   mp.part_o = p.part_o;
   mp.part_ml = p.part_ml;

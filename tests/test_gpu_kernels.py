@@ -351,3 +351,37 @@ def test_decode_writes_stay_inside_workspace_and_out(lens, Hq, Hkv, D, ps):
     ref = O.paged_attention_ref([q[b:b + 1] for b in range(B)], k.view(-1, Hkv, D), v.view(-1, Hkv, D), ps,
                                 indptr, indices, lpl, [1] * B)
     torch.testing.assert_close(out[:B].cpu().float(), torch.stack([r[0] for r in ref]), atol=ATOL, rtol=RTOL)
+
+
+def test_decode_chunks_longer_than_the_page_window():
+    """Two 400k-token sequences whose block tables draw (with repeats) from a
+    64-page pool: the chunks run past 128 pages, so the per-lane page-id window is
+    refilled mid-chunk. Reference: attention over the distinct rows weighted by
+    how often each appears, in float64."""
+    _log("decode long chunks / page-id window refill")
+    ps, Hq, Hkv, D, P = 16, 32, 8, 128, 64
+    lens = [400_000, 399_993]
+    g = torch.Generator().manual_seed(71)
+    rng = np.random.default_rng(71)
+    k = torch.randn(P, ps, Hkv, D, generator=g).half()
+    v = torch.randn(P, ps, Hkv, D, generator=g).half()
+    q = torch.randn(len(lens), Hq, D, generator=g).half()
+    tables = [rng.integers(1, P, size=math.ceil(L / ps)).tolist() for L in lens]
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    out = _k().paged_decode(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(indptr).to(DEV),
+                            torch.from_numpy(indices).to(DEV), torch.from_numpy(lpl).to(DEV), int(indptr[-1]))
+    torch.cuda.synchronize()
+    kf = k.double().reshape(P * ps, Hkv, D)
+    vf = v.double().reshape(P * ps, Hkv, D)
+    G = Hq // Hkv
+    for b, L in enumerate(lens):
+        rows = (np.asarray(tables[b])[:, None] * ps + np.arange(ps)[None, :]).reshape(-1)[:L]
+        mult = torch.from_numpy(np.bincount(rows, minlength=P * ps)).double()
+        used = mult > 0
+        ks, vs, w = kf[used], vf[used], mult[used]
+        qb = q[b].double().reshape(Hkv, G, D)
+        s = torch.einsum("hgd,nhd->hgn", qb, ks) / math.sqrt(D)
+        s = s - s.amax(-1, keepdim=True)
+        p = torch.exp(s) * w
+        ref = torch.einsum("hgn,nhd->hgd", p, vs) / p.sum(-1, keepdim=True)
+        torch.testing.assert_close(out[b].cpu().float(), ref.reshape(Hq, D).float(), atol=ATOL, rtol=RTOL)
