@@ -295,7 +295,8 @@ class _ContigCtxRef:
         return self.start_positions[idx]
 
     def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
-        """kv_cache.py:297-322, batch-row indexing (Q7) kept."""
+        """kv_cache.py:297-322; like the reference, the pool is indexed by batch row b,
+        not by the sequence's slot (:302, :309)."""
         B, S, _, D = q.shape
         pool = self.cache
         if self._is_decode:
@@ -395,7 +396,8 @@ class _RNodeRef:
 
 
 class RadixTreeRef:
-    """Per-token trie of kv_cache.py:453-531 (quirks Q3/Q4 kept as the reference has them)."""
+    """Per-token trie of kv_cache.py:453-531, with the reference's behaviour kept: match does not
+    stop at an evicted interior page (:467), and LRU ties keep DFS pre-order (:507)."""
 
     def __init__(self, ps, pool):
         self.root = _RNodeRef()

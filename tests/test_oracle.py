@@ -266,7 +266,7 @@ def test_contiguous_and_paged_oracles_agree():
     cont, paged, outs = _run_both(0)
     for o1, o2, ntok, offs in outs:
         for b in range(3):
-            rows = slice(offs[b], offs[b] + ntok[b])  # pad rows differ by design (Q6)
+            rows = slice(offs[b], offs[b] + ntok[b])  # pad rows: zeros here, masked averages in the reference
             torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=1e-5, rtol=1e-5)
     for b, s in enumerate(["a", "b", "c"]):
         n = paged.seqs[s].num_tokens
