@@ -428,9 +428,11 @@ class RadixTree:
     returns whole pages only, kv_cache.py:459-472).
 
     Differences from the reference's per-token trie, on purpose:
-      * match stops at the first page node without a page (after an interior
-        eviction), so the returned pages always cover tokens [0, 16*len(pages)) with no
-        gap (the reference can skip a page there);
+      * match returns pages only up to the first page node whose page was evicted
+        (an interior eviction), so the pages always cover tokens [0, ps*len(pages));
+        the reference returns the deeper pages too, leaving a gap (kv_cache.py:467).
+        The walk itself, its access stamps and its invalidation of pages whose
+        refcount dropped to zero are the reference's, so eviction order stays the same;
       * access times come from a counter, so ties only arise within one call, as
         with the reference's monotonic clock (LRU ties keep DFS pre-order)."""
 
@@ -453,6 +455,7 @@ class RadixTree:
     def match(self, tokens) -> Tuple[int, List[int]]:
         with self._lock:
             node, pages, now = self.root, [], self._now()
+            contiguous = True
             for key in self._keys(tokens):
                 ch = node.children.get(key)
                 if ch is None:
@@ -460,9 +463,11 @@ class RadixTree:
                 node = ch
                 node.last_access = now
                 if node.page_id < 0:
-                    break
+                    contiguous = False  # evicted inside the path: no page past here
+                    continue
                 if self.pool.ref_count[node.page_id] > 0:
-                    pages.append(node.page_id)
+                    if contiguous:
+                        pages.append(node.page_id)
                 else:
                     node.page_id = -1
                     break

@@ -32,8 +32,12 @@ tests live in tests/test_oracle.py):
                                                 reserved, no double allocation,
                                                 conservation, zero on alloc)
   RadixTreeRef           kv_cache.py:445-531    pinned by brute-force longest
-                                                common full-page prefix and
-                                                invariants
+                                                common full-page prefix,
+                                                invariants, and operation
+                                                sequences recorded from the
+                                                reference's own RadixTree and
+                                                PagePool (tests/golden/
+                                                radix_vectors.json)
   PagedRef               kv_cache.py:534-777    write plan + CoW order rule,
                                                 CSR, attend = SDPA over the
                                                 gathered pages; pinned against
