@@ -16,7 +16,7 @@ step, so the pass that gives `value` runs without them).
 `cpu_baseline` = the CPU restatement of the reference's contiguous SDPA path on a
 bounded sample of the same workload, on this host's cores.
 
-  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch]
+  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch|radix|prefill]
   python bench.py --workload copy_calibration   (a plain 1 GiB copy, for counter scaling)
 """
 from __future__ import annotations
@@ -186,6 +186,22 @@ class EventTimedKernels:
     def __getattr__(self, name):
         return getattr(self._k, name)
 
+    def DecodeLaunch(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                     num_qo_heads, workspace=None, sm_scale=None):
+        """The per-forward launcher; while recording, each layer runs as append_kv and
+        then an event-timed paged_decode (the same launches, the same results)."""
+        real = self._k.DecodeLaunch(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len,
+                                    total_pages, num_qo_heads, workspace=workspace, sm_scale=sm_scale)
+        timed = self
+
+        def launch(layer, q, k_new, v_new):
+            if not timed.recording:
+                return real(layer, q, k_new, v_new)
+            timed._k.append_kv(k_new, v_new, slot_mapping, k_pool[layer], v_pool[layer])
+            return timed.paged_decode(q, k_pool[layer], v_pool[layer], kv_indptr, kv_indices, kv_last_page_len,
+                                      total_pages, sm_scale=sm_scale, workspace=workspace)
+        return launch
+
     def paged_decode(self, *args, **kw):
         if not self.recording:
             return self._k.paged_decode(*args, **kw)
@@ -198,8 +214,23 @@ class EventTimedKernels:
         self.events.append((a, b))
         return out
 
+    def paged_prefill(self, *args, **kw):
+        if not self.recording:
+            return self._k.paged_prefill(*args, **kw)
+        torch = self._torch
+        stream = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        out = self._k.paged_prefill(*args, **kw)
+        b.record(stream)
+        self.events.append((a, b))
+        return out
+
     def mean_ms(self):
         return float(np.mean([a.elapsed_time(b) for a, b in self.events]))
+
+    def total_ms(self):
+        return float(np.sum([a.elapsed_time(b) for a, b in self.events]))
 
 
 def copy_calibration():
@@ -382,6 +413,257 @@ def run_decode(args):
     return res, lens
 
 
+RADIX_B, RADIX_PREFIX = 16, 2040
+
+
+def run_radix(args):
+    """Radix prefix sharing + copy-on-write: a 2040-token prompt (127 full pages and a
+    page holding 8 tokens) is prefilled once; 16 requests whose prompts start with it
+    are admitted through the radix tree (the 127 full pages are matched by token ids)
+    and also take a reference on the shared partial page, as a caller that shares
+    partial pages does with add_ref (kv_cache.py:713). Their suffixes (128..1024
+    tokens) are then prefilled in one ragged forward: the first write lands in slot 8
+    of the shared page, so 15 requests copy it and the last writes in place
+    (kv_cache.py:586-591). Then `--steps` decode steps of all 16.
+    Decode bytes count the 127 shared pages once (distinct pages); the kernel reads
+    them once per request, and how many of those reads reach HBM is the caches'
+    business, so the per-request total is reported beside it as effective GB/s."""
+    import torch
+    from nanoslg_amd import kernels
+    from nanoslg_amd.kv_cache import KVCacheConfig, PagedKVCache
+    B, PRE = RADIX_B, RADIX_PREFIX
+    full = PRE // PS
+    rng = np.random.default_rng(args.seed)
+    suffix = [int(x) for x in rng.integers(128, 1025, size=B)]
+    steps = args.steps
+    # prompt pages, then per request: its suffix and 2 * steps + warmup decode tokens
+    # (timed pass + roofline pass) after the 8 shared tokens, plus its copy of the page
+    pages = full + 1 + sum(math.ceil((PRE % PS + s + 2 * steps + args.warmup) / PS) + 1 for s in suffix) + 64
+    dev = torch.device("cuda:0")
+    cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
+                        max_pages=pages, dtype=torch.float16, device=dev, enable_prefix_caching=True,
+                        backend="paged")
+    mgr = PagedKVCache(cfg)
+    timed = EventTimedKernels(kernels)
+    mgr.kernels = timed
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    randn = lambda *shape: torch.randn(*shape, generator=g, device=dev, dtype=torch.float16)  # noqa: E731
+    prompt = rng.integers(0, 128256, size=PRE).tolist()
+    mgr.allocate_sequence("owner", token_ids=prompt)
+    ctx = mgr.begin_forward(["owner"], [PRE])
+    ctx.attend(0, randn(1, PRE, HQ, D), randn(1, PRE, HKV, D), randn(1, PRE, HKV, D), HQ, HKV)
+    mgr.end_forward(ctx)
+    owner_pages = mgr.seqs["owner"].bt[:full + 1].tolist()
+    mgr.tree.insert(prompt[:full * PS], owner_pages[:full])  # the full pages, as release inserts them
+    ids = [f"r{b}" for b in range(B)]
+    for sid, n in zip(ids, suffix):
+        tids = prompt + rng.integers(0, 128256, size=n).tolist()
+        plen = mgr.allocate_sequence(sid, token_ids=tids)
+        assert plen == full * PS, plen
+        st = mgr.seqs[sid]
+        own = int(st.bt[full])
+        st.bt[full] = owner_pages[full]  # share the partial page
+        mgr.pool.add_ref(owner_pages[full])
+        mgr.pool.release(own)
+        st.num_tokens = PRE
+    mgr.release_sequence("owner")
+    assert mgr.pool.ref_count[owner_pages[full]] == B
+    # suffix prefill with copy-on-write of the shared page
+    S = max(suffix)
+    q, k, v = randn(B, S, HQ, D), randn(B, S, HKV, D), randn(B, S, HKV, D)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ctx = mgr.begin_forward(ids, suffix)
+    ctx.attend(0, q, k, v, HQ, HKV)
+    mgr.end_forward(ctx)
+    torch.cuda.synchronize()
+    suffix_ms = (time.perf_counter() - t0) * 1e3
+    cow = len(ctx.cow_pairs)
+    assert cow == B - 1 and mgr.seqs[ids[-1]].bt[full] == owner_pages[full]
+    # decode
+    ring = 8
+    qd, kd, vd = randn(ring, B, 1, HQ, D), randn(ring, B, 1, HKV, D), randn(ring, B, 1, HKV, D)
+
+    def step(i):
+        c = mgr.begin_forward(ids, [1] * B)
+        c.attend(0, qd[i % ring], kd[i % ring], vd[i % ring], HQ, HKV)
+        mgr.end_forward(c)
+
+    def lens():
+        return [mgr.seqs[s].num_tokens + 1 for s in ids]
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    shared_bytes = full * PS * HKV * D * 2 * 2
+    nbytes = eff = kbytes = 0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        L = lens()
+        tp = sum(math.ceil(x / PS) for x in L)
+        kv, app, qo, csr = step_bytes(L, B, tp)
+        nbytes += kv - (B - 1) * shared_bytes + app + qo + csr
+        eff += kv + app + qo + csr
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    timed.recording = True
+    for i in range(steps):
+        L = lens()
+        kbytes += decode_call_bytes(L, B, sum(math.ceil(x / PS) for x in L)) - (B - 1) * shared_bytes
+        step(i)
+    torch.cuda.synchronize()
+    timed.recording = False
+    mean_ms = timed.mean_ms()
+    kbytes /= steps
+    value = nbytes / wall / 1e9
+    _log(f"suffix prefill + {cow} copy-on-writes: {suffix_ms:.2f} ms; decode {wall / steps * 1e3:.3f} ms/step, "
+         f"{value:.1f} GB/s distinct, {eff / wall / 1e9:.1f} GB/s effective; decode call {mean_ms * 1e3:.1f} us")
+    return {
+        "metric": "paged decode attn+append with a shared radix prefix: HBM GB/s (distinct pages) and tok/s/layer",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic: Q/K/V ~ N(0,1), token ids ~ U[0,128256), seeded",
+        "config": {"workload": "radix_prefix_cow", "batch": B, "shared_prefix": PRE, "suffix": "U[128,1024]",
+                   "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "layers": 1, "seed": args.seed},
+        "effective_GB_s": round(eff / wall / 1e9, 2),
+        "decode_tok_s_layer": round(B * steps / wall, 1),
+        "suffix_prefill_ms": round(suffix_ms, 3),
+        "copy_on_write_pages": cow,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "nslg_paged_decode (split-K decode kernel + LSE merge kernel)",
+            "timing": f"HIP events around each of {steps} decode calls in a second pass",
+            "achieved": round(kbytes / (mean_ms * 1e-3) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(mean_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": int(kbytes),
+        },
+    }
+
+
+PREFILL_B, PREFILL_LEN, PREFILL_CHUNK = 8, 4096, 512
+
+
+def prefill_flops(B, L, Hq, D, start=0, n=None):
+    """Algorithmic flops of causal attention for rows [start, start+n) of B sequences:
+    4*Hq*D per (row, visible key); row p sees keys 0..p."""
+    n = L - start if n is None else n
+    keys = (start + 1 + start + n) * n // 2
+    return 4 * Hq * D * B * keys
+
+
+def run_prefill(args):
+    """Chunked prefill: 8 sequences x 4096 tokens, each fed as 8 chunks of 512 through
+    the drop-in API (begin_forward -> attend -> end_forward): every chunk appends its
+    K/V to fresh pages, then attends causally (bottom-right) to all earlier pages and
+    itself. One step = the whole batch prefilled (8 chunked forwards); sequences are
+    released and re-admitted between steps, outside the timed region."""
+    import torch
+    from nanoslg_amd import kernels
+    from nanoslg_amd.kv_cache import KVCacheConfig, PagedKVCache
+    B, L, CH = PREFILL_B, PREFILL_LEN, PREFILL_CHUNK
+    nchunks = L // CH
+    dev = torch.device("cuda:0")
+    cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
+                        max_pages=B * L // PS + 64, dtype=torch.float16, device=dev,
+                        enable_prefix_caching=False, backend="paged")
+    mgr = PagedKVCache(cfg)
+    timed = EventTimedKernels(kernels)
+    mgr.kernels = timed
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn(nchunks, B, CH, HQ, D, generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    ids = [f"p{b}" for b in range(B)]
+
+    def admit():
+        for sid in ids:
+            mgr.allocate_sequence(sid)
+
+    def prefill():
+        for c in range(nchunks):
+            ctx = mgr.begin_forward(ids, [CH] * B)
+            ctx.attend(0, q[c], k[c], v[c], HQ, HKV)
+            mgr.end_forward(ctx)
+
+    def release():
+        for sid in ids:
+            mgr.release_sequence(sid)
+
+    for _ in range(max(1, args.warmup // 8)):
+        admit()
+        prefill()
+        release()
+    torch.cuda.synchronize()
+    steps = args.steps
+    wall = 0.0
+    for _ in range(steps):
+        admit()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prefill()
+        torch.cuda.synchronize()
+        wall += time.perf_counter() - t0
+        release()
+    ms_step = wall / steps * 1e3
+    flops = prefill_flops(B, L, HQ, D)
+    tflops = flops / (wall / steps) / 1e12
+    _log(f"{steps} prefills in {wall*1e3:.1f} ms -> {ms_step:.3f} ms each, {tflops:.1f} TFLOP/s")
+    # roofline pass: events around each prefill kernel call
+    timed.recording = True
+    for _ in range(steps):
+        admit()
+        prefill()
+        release()
+    torch.cuda.synchronize()
+    timed.recording = False
+    kernel_ms = timed.total_ms() / steps
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    _log(f"prefill kernel: {kernel_ms:.3f} ms per 8 chunks ({len(timed.events)} launches), {achieved:.1f} TFLOP/s")
+    res = {
+        "metric": "chunked prefill attention: TFLOP/s (causal, algorithmic) and prefill tok/s/layer",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic: Q/K/V ~ N(0,1), seeded",
+        "config": {"workload": "chunked_prefill", "batch": B, "tokens_per_seq": L, "chunk": CH,
+                   "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "layers": 1},
+        "prefill_tok_s_layer": round(B * L / (wall / steps), 1),
+        "flops_per_step": flops,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "nslg_paged_prefill (8 chunk launches per step)",
+            "timing": f"HIP events around each of {len(timed.events)} prefill calls in a second pass",
+            "achieved": round(achieved, 2),
+            "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(timed.mean_ms() * 1e3, 2),
+        },
+    }
+    return res
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -394,6 +676,12 @@ def main():
         sys.exit(1)
     if args.workload == "copy_calibration":
         print(json.dumps(copy_calibration()), flush=True)
+        return
+    if args.workload == "prefill":
+        print(json.dumps(run_prefill(args)), flush=True)
+        return
+    if args.workload == "radix":
+        print(json.dumps(run_radix(args)), flush=True)
         return
     if args.workload in ("kv_pressure", "small_batch"):
         res, lens = run_decode(args)

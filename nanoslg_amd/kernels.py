@@ -204,6 +204,74 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     return out
 
 
+class DecodeLaunch:
+    """Append + split-K decode for every layer of one decode forward.
+
+    What is the same for all layers of the forward (pools, block table, slot
+    mapping, sizes, the workspace and its size) is checked and computed once, here;
+    each call checks that layer's tensors and issues nslg_append_kv then
+    nslg_paged_decode on the current stream. Same results as append_kv followed by
+    paged_decode on the layer's pool slices."""
+
+    def __init__(self, k_pool: torch.Tensor, v_pool: torch.Tensor, slot_mapping: torch.Tensor,
+                 kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                 total_pages: int, num_qo_heads: int, workspace: Optional[Workspace] = None,
+                 sm_scale: Optional[float] = None):
+        _require_gpu(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
+        for t, n in ((slot_mapping, "slot_mapping"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                     (kv_last_page_len, "kv_last_page_len")):
+            _i32(t, n)
+        L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
+        B = kv_indptr.numel() - 1
+        if slot_mapping.numel() != B or kv_last_page_len.numel() < B:
+            raise ValueError("DecodeLaunch: one slot and one last-page length per sequence")
+        if num_qo_heads % Hkv:
+            raise ValueError(f"DecodeLaunch: Hq={num_qo_heads} is not a multiple of Hkv={Hkv}")
+        self.lib = _lib.load()
+        self.device, self.dtype = k_pool.device, k_pool.dtype
+        self.code = dtype_code(k_pool.dtype)
+        self.L, self.P, self.ps, self.Hkv, self.D, self.B, self.Hq = L, P, ps, Hkv, D, B, num_qo_heads
+        self.layer_bytes = P * ps * Hkv * D * k_pool.element_size()
+        self.kp0, self.vp0 = k_pool.data_ptr(), v_pool.data_ptr()
+        self.keep = (k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
+        self.slots, self.indptr, self.indices, self.lpl = (slot_mapping.data_ptr(), kv_indptr.data_ptr(),
+                                                           kv_indices.data_ptr(), kv_last_page_len.data_ptr())
+        self.total_pages = int(total_pages)
+        need = int(self.lib.nslg_paged_decode_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages, ps,
+                                                             self.code))
+        self.ws = (workspace or Workspace(self.device)).get(need)
+        self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+
+    def __call__(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
+        """q [B, Hq, D] (rows may be strided), k_new/v_new [B, ..., Hkv, D] rows of one
+        token each; returns [B, Hq, D] for pool layer `layer`."""
+        if not 0 <= layer < self.L:
+            raise IndexError(f"layer {layer} out of range [0, {self.L})")
+        for t in (q, k_new, v_new):
+            if t.device != self.device or t.dtype != self.dtype:
+                raise ValueError(f"DecodeLaunch: tensors must be {self.dtype} on {self.device}")
+        B, Hq, D = self.B, self.Hq, self.D
+        if tuple(q.shape) != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
+            raise ValueError(f"DecodeLaunch: q must be [{B}, {Hq}, {D}] with a contiguous [Hq, D] block")
+        nk, ks, hk = _rows(k_new, "k_new")
+        nv, vs, hv = _rows(v_new, "v_new")
+        if nk != B or nv != B or hk != self.Hkv or hv != self.Hkv or k_new.shape[-1] != D or v_new.shape[-1] != D:
+            raise ValueError(f"DecodeLaunch: k_new/v_new must hold {B} rows of [{self.Hkv}, {D}]")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        off = layer * self.layer_bytes
+        kp, vp = self.kp0 + off, self.vp0 + off
+        lib = self.lib
+        rc = lib.nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, self.slots, B, kp, vp,
+                                self.P * self.ps, self.Hkv, D, self.code, stream)
+        _lib.check(rc, "nslg_append_kv")
+        out = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
+        rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), kp, vp, self.P, self.ps, self.indptr, self.indices,
+                                   self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
+                                   out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
+        _lib.check(rc, "nslg_paged_decode")
+        return out
+
+
 def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
                   k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
                   kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,

@@ -198,40 +198,87 @@ class KVCacheManager(ABC):
 # --------------------------------------------------------------------------------------
 
 
-_COPY_STREAMS: Dict[int, "torch.cuda.Stream"] = {}
+class _PlanStaging:
+    """Host-to-device staging of per-forward int32 plans on one device.
+
+    The plan is written straight into a pinned host buffer taken from a small ring
+    (a buffer is refilled only after the copy that last read it has completed, which
+    its event records) and moved with one async copy.
+
+    Large plans (big batches, where the GPU has a long queue of work) are copied on
+    a side stream of default priority into memory allocated on that stream; the
+    compute stream waits for the copy through the same event, so the copy of forward
+    i+1 overlaps the kernels of forward i, and the destination is recorded on the
+    compute stream, so the allocator does not hand it out again while those kernels
+    may still read it. Small plans are copied on the compute stream itself: there
+    the GPU waits on the host anyway, and a cross-stream wait costs the host about
+    20 us per forward."""
+
+    RING = 4
+    SIDE_STREAM_BYTES = 64 << 10
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.side = torch.cuda.Stream(device=device)  # default priority
+        self.host: List[Optional[torch.Tensor]] = [None] * self.RING
+        self.host_np: List[Optional[np.ndarray]] = [None] * self.RING
+        self.copied = [torch.cuda.Event() for _ in range(self.RING)]
+        self.pending = [False] * self.RING
+        self.next = 0
+
+    def upload(self, parts: List[np.ndarray], total: int) -> torch.Tensor:
+        k = self.next
+        self.next = (k + 1) % self.RING
+        if self.pending[k]:
+            self.copied[k].synchronize()
+        buf = self.host[k]
+        if buf is None or buf.numel() < total:
+            buf = torch.empty(max(total, 1 << 12) * 2, dtype=torch.int32, pin_memory=True)
+            self.host[k], self.host_np[k] = buf, buf.numpy()
+        host = self.host_np[k]
+        off = 0
+        for a in parts:
+            n = a.size
+            host[off:off + n] = a.reshape(-1)
+            off += n
+        main = torch.cuda.current_stream(self.device)
+        self.pending[k] = True
+        if 4 * total <= self.SIDE_STREAM_BYTES:
+            dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
+            dev[:total].copy_(buf[:total], non_blocking=True)
+            self.copied[k].record(main)
+            return dev
+        with torch.cuda.stream(self.side):
+            dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
+            dev[:total].copy_(buf[:total], non_blocking=True)
+            self.copied[k].record(self.side)
+        main.wait_event(self.copied[k])
+        dev.record_stream(main)
+        return dev
 
 
-def _copy_stream(device: torch.device) -> "torch.cuda.Stream":
+_STAGING: Dict[int, _PlanStaging] = {}
+
+
+def _staging(device: torch.device) -> _PlanStaging:
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    st = _COPY_STREAMS.get(idx)
+    st = _STAGING.get(idx)
     if st is None:
-        st = torch.cuda.Stream(device=idx)  # default priority
-        _COPY_STREAMS[idx] = st
+        st = _PlanStaging(torch.device("cuda", idx))
+        _STAGING[idx] = st
     return st
 
 
 def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Tensor]:
-    """Concatenate int32 arrays, copy once host->device, return views.
-
-    On a GPU the copy runs from pinned memory on a side stream, so it overlaps the
-    kernels still queued on the compute stream; the compute stream waits for it
-    only where the plan is first used."""
-    sizes = [int(p.size) for p in parts]
-    flat = np.concatenate([np.asarray(p, dtype=np.int32).reshape(-1) for p in parts]) if parts else \
-        np.zeros(0, np.int32)
-    host = torch.from_numpy(flat)
+    """Concatenate int32 arrays, copy them to `device` at once, return the views (one
+    per part). On a GPU this goes through the device's _PlanStaging."""
+    sizes = [int(a.size) for a in parts]
+    total = sum(sizes)
     if device.type == "cuda":
-        main = torch.cuda.current_stream(device)
-        side = _copy_stream(device)
-        pinned = host.pin_memory()
-        # the destination comes from the side stream's pool and is recorded on the
-        # compute stream, so the allocator never hands it out while still in use
-        with torch.cuda.stream(side):
-            dev = pinned.to(device, non_blocking=True)
-        main.wait_stream(side)
-        dev.record_stream(main)
+        dev = _staging(device).upload([np.asarray(a) for a in parts], total)
     else:
-        dev = host.clone()
+        dev = torch.from_numpy(np.concatenate([np.asarray(a, dtype=np.int32).reshape(-1) for a in parts])
+                               if parts else np.zeros(0, np.int32)).clone()
     out, off = [], 0
     for n in sizes:
         out.append(dev[off:off + n])
@@ -617,25 +664,39 @@ class PagedCacheContext(CacheContext):
             pool.release(pid)
 
         if self._is_decode and iw == 1:
-            # one token per sequence: vectorised over the batch. Only a page that is
-            # shared before any copy can need one, so the candidates are re-checked in
-            # batch order, which reproduces the sequential rule exactly.
+            # One token per sequence, vectorised over the batch. The page written by
+            # sequence b is the last page of its CSR segment; only a page that is shared
+            # before any copy can need one, so the candidates are re-checked in batch
+            # order, which reproduces the sequential rule exactly.
             start = np.fromiter(self.start_positions, np.int64, B)
-            pi = start // ps
-            sl = start % ps
             have = np.fromiter((st.n_pages for st in states), np.int64, B)
+            lens = start + 1
+            npg = (lens + ps - 1) // ps
+            indptr = np.zeros(B + 1, np.int64)
+            np.cumsum(npg, out=indptr[1:])
+            if bool((npg <= have).all()):
+                indices = np.concatenate([st.bt[:k] for st, k in zip(states, npg.tolist())])
+            else:
+                indices = self._csr_indices(states, npg)
+            pi = npg - 1
+            sl = start - pi * ps
             ok = pi < have
-            pids = np.fromiter((int(st.bt[p]) if p < st.n_pages else 0
-                                for st, p in zip(states, pi.tolist())), np.int64, B)
+            last = indptr[1:] - 1
+            pids = np.where(ok, indices[last], 0).astype(np.int64)
             cand = np.nonzero(ok & (pool.ref_count[pids] > 1))[0]
             for b in cand.tolist():
                 st = states[b]
                 if pool.is_shared(int(st.bt[pi[b]])):
                     _cow(st, int(pi[b]))
                     pids[b] = st.bt[pi[b]]
-            slot = np.where(ok, pids * ps + sl, 0).astype(np.int32).reshape(B, 1)
+                    indices[last[b]] = pids[b]
+            slot = np.where(ok, pids * ps + sl, 0).astype(np.int32)
             if ok.any():
                 np.maximum.at(pool.tokens_used, pids[ok], sl[ok] + 1)
+            lpl = lens - pi * ps
+            pos = start.astype(np.int32)
+            q_rows = np.arange(B, dtype=np.int64)
+            qo = np.arange(B + 1, dtype=np.int64)
         else:
             slot = np.full((B, iw), -1, np.int32)
             for b, st in enumerate(states):
@@ -654,28 +715,20 @@ class PagedCacheContext(CacheContext):
                 slot[b, o:o + n] = (pids * ps + sls).astype(np.int32)
                 if ok.any():
                     np.maximum.at(pool.tokens_used, pids[ok], sls[ok] + 1)
+            # CSR block table (kv_cache.py:598-615)
+            lens = np.asarray(self.seq_lens, np.int64)
+            npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
+            indptr = np.zeros(B + 1, np.int64)
+            np.cumsum(npg, out=indptr[1:])
+            indices = self._csr_indices(states, npg)
+            lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
+            if B == 0:
+                lpl = np.zeros(1, np.int64)
+            pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
         self.cow_pairs = list(zip(cow_src, cow_dst))
-
-        # CSR block table (kv_cache.py:598-615)
-        lens = np.asarray(self.seq_lens, np.int64)
-        npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
-        indptr = np.zeros(B + 1, np.int64)
-        np.cumsum(npg, out=indptr[1:])
-        parts = []
-        for k, st in zip(npg.tolist(), states):
-            if k <= st.n_pages:
-                parts.append(st.bt[:k])
-            else:  # pages missing from the table read the null page (kv_cache.py:606-607)
-                parts.append(st.bt[:st.n_pages])
-                parts.append(np.zeros(k - st.n_pages, np.int32))
-        indices = np.concatenate(parts) if parts else np.zeros(0, np.int32)
+        self._decode_launch = None
         if indices.size == 0:
             indices = np.zeros(1, np.int32)
-        lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
-        if B == 0:
-            lpl = np.zeros(1, np.int64)
-
-        pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
         self._max_q = max(self.new_token_counts) if B else 0
         self._uniform_rows = int(qo[-1]) == B * iw  # every grid row carries a new token
 
@@ -686,6 +739,19 @@ class PagedCacheContext(CacheContext):
             cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
             cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
+
+    @staticmethod
+    def _csr_indices(states, npg) -> np.ndarray:
+        """Concatenated block tables, npg[b] pages of sequence b; pages missing from a
+        table read the null page (kv_cache.py:606-607)."""
+        parts = []
+        for k, st in zip(npg.tolist(), states):
+            if k <= st.n_pages:
+                parts.append(st.bt[:k])
+            else:
+                parts.append(st.bt[:st.n_pages])
+                parts.append(np.zeros(k - st.n_pages, np.int32))
+        return np.concatenate(parts) if parts else np.zeros(0, np.int32)
 
     # ---- CacheContext -----------------------------------------------------------------
     def get_position_ids(self, S: int) -> torch.Tensor:
@@ -700,12 +766,15 @@ class PagedCacheContext(CacheContext):
         cache, pool, plan = self.cache, self.cache.pool, self._plan
         kern = cache.kernels
         B, S = q.shape[0], q.shape[1]
+        if self._is_decode and S == 1:
+            launch = self._decode_launch
+            if launch is None:
+                launch = self._decode_launch = kern.DecodeLaunch(
+                    pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
+                    q.shape[2], workspace=cache.workspace)
+            return launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
-        if self._is_decode and S == 1:
-            out = kern.paged_decode(q[:, 0], k_layer, v_layer, plan.indptr, plan.indices, plan.lpl,
-                                    plan.total_pages, workspace=cache.workspace)
-            return out.reshape(B, 1, -1)
         Hq, D = q.shape[2], q.shape[3]
         if self._uniform_rows and S == self._iw:
             q_rag = q.reshape(B * S, Hq, D)
@@ -762,8 +831,12 @@ class PagedKVCache(KVCacheManager):
             st.extend(self._alloc(need - st.n_pages, defer_zero=True))
 
     def begin_forward(self, seq_ids, ntoks, offsets=None):
-        for s, n in zip(seq_ids, ntoks):
-            self.extend_sequence(s, n)
+        ps = self.cfg.page_size
+        for s, n in zip(seq_ids, ntoks):  # extend_sequence, inlined
+            st = self.seqs[s]
+            need = -(-(st.num_tokens + n) // ps)
+            if need > st.n_pages:
+                st.extend(self._alloc(need - st.n_pages, defer_zero=True))
         zero, self._pending_zero = self._pending_zero, []
         return PagedCacheContext(self, seq_ids, ntoks, offsets, zero_pages=zero)
 

@@ -93,3 +93,20 @@ def paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_
         out[:res.shape[0]].copy_(res)
         return out
     return res
+
+
+class DecodeLaunch:
+    """Per-forward append + decode, as nanoslg_amd.kernels.DecodeLaunch, from the
+    functions above."""
+
+    def __init__(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                 num_qo_heads, workspace=None, sm_scale=None):
+        self.k_pool, self.v_pool = k_pool, v_pool
+        self.args = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages)
+        self.sm_scale = sm_scale
+
+    def __call__(self, layer, q, k_new, v_new):
+        slots, indptr, indices, lpl, total = self.args
+        k_layer, v_layer = self.k_pool[layer], self.v_pool[layer]
+        append_kv(k_new, v_new, slots, k_layer, v_layer)
+        return paged_decode(q, k_layer, v_layer, indptr, indices, lpl, total, sm_scale=self.sm_scale)

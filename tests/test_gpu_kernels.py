@@ -385,3 +385,35 @@ def test_decode_chunks_longer_than_the_page_window():
         p = torch.exp(s) * w
         ref = torch.einsum("hgn,nhd->hgd", p, vs) / p.sum(-1, keepdim=True)
         torch.testing.assert_close(out[b].cpu().float(), ref.reshape(Hq, D).float(), atol=ATOL, rtol=RTOL)
+
+
+def test_decode_launch_matches_separate_calls():
+    """The per-forward launcher (append + decode per layer) gives the same pool bytes
+    and the same outputs as append_kv followed by paged_decode on each layer."""
+    _log("decode launcher vs separate calls")
+    from nanoslg_amd import kernels as K
+    g = torch.Generator().manual_seed(72)
+    L, P, ps, Hq, Hkv, D = 3, 200, 16, 32, 8, 128
+    lens = [700, 33, 1500, 1]
+    k_pool = torch.randn(L, P, ps, Hkv, D, generator=g).half().to(DEV)
+    v_pool = torch.randn(L, P, ps, Hkv, D, generator=g).half().to(DEV)
+    k2, v2 = k_pool.clone(), v_pool.clone()
+    tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, 72)
+    slots = torch.tensor([tables[b][(n - 1) // ps] * ps + (n - 1) % ps for b, n in enumerate(lens)],
+                         dtype=torch.int32, device=DEV)
+    ip, ix, lp = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl))
+    launch = K.DecodeLaunch(k_pool, v_pool, slots, ip, ix, lp, int(indptr[-1]), Hq)
+    for layer in range(L):
+        q = torch.randn(len(lens), Hq, D, generator=g).half().to(DEV)
+        kn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
+        vn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
+        o1 = launch(layer, q, kn, vn)
+        K.append_kv(kn, vn, slots, k2[layer], v2[layer])
+        o2 = K.paged_decode(q, k2[layer], v2[layer], ip, ix, lp, int(indptr[-1]))
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2)
+    assert torch.equal(k_pool, k2) and torch.equal(v_pool, v2)
+    with pytest.raises(ValueError):
+        launch(0, q[:2], kn, vn)
+    with pytest.raises(IndexError):
+        launch(L, q, kn, vn)
