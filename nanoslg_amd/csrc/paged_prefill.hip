@@ -9,7 +9,10 @@
 // Per 64-key tile (staged in LDS, double buffered, shared by the 4 waves):
 //   S^T[16 key x 16 row] = K[16 key x D] * Q^T[D x 16 row]   v_mfma 16x16x32, D/32 steps
 //   online softmax per row (column) in fp32, running max rescaled lazily
-//   O^T[D x 16 row] += V^T[D x 16 key] * P^T[16 key x 16 row]  v_mfma 16x16x16
+//   O^T[D x 16 row] += V^T[D x 32 key] * P^T[32 key x 16 row]  v_mfma 16x16x32,
+//     V^T operands read from the row-major V tile with transposing LDS reads
+//   (P.V runs over 32-key blocks so it uses the full-rate 16x16x32 instruction; the
+//   16x16x16 one issues at half the rate on gfx950)
 // which is the decode kernel's formulation with all 16 MFMA columns live.
 //
 // Causality is bottom-right aligned: sequence b holds L_b tokens of which the
@@ -99,7 +102,6 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
   constexpr int NT = D / 16;
   constexpr int kPitch = D + 8;  // LDS row pitch in elements (16 B pad vs bank conflicts)
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;
-  typedef typename Vec<NT>::type VT;
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKeys * kPitch];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kPitch];
@@ -187,29 +189,38 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
     }
     win_base = pg0;
   };
+  // thread tid moves 16-byte chunk tid % kChunks of keys tid / kChunks + (256 / kChunks) i
+  const int f_ch16 = (tid % kChunks) * 16;
+  const int f_key = tid / kChunks;
+  const bool ps_pow2 = (ps & (ps - 1)) == 0;
+  const int ps_shift = __builtin_ctz((unsigned)ps);
+  const int64_t page_bytes = (int64_t)ps * row_bytes;
   auto fetch = [&](int kt) {
     const int key0 = kt * kKeys;
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / kChunks;
-      const int ch = c % kChunks;
-      int kabs = key0 + key;
+      int kabs = key0 + f_key + (256 / kChunks) * i;
       kabs = kabs < kv_end ? kabs : kv_end - 1;
-      const int pid = page_lds[kabs / ps - win_base];
-      const int64_t rowi = (int64_t)pid * ps + kabs % ps;
-      kreg[i] = *reinterpret_cast<const u32x4*>(kpool + rowi * row_bytes + ch * 16);
-      vreg[i] = *reinterpret_cast<const u32x4*>(vpool + rowi * row_bytes + ch * 16);
+      int pg, slot;
+      if (ps_pow2) {
+        pg = kabs >> ps_shift;
+        slot = kabs & (ps - 1);
+      } else {
+        pg = kabs / ps;
+        slot = kabs - pg * ps;
+      }
+      const int pid = page_lds[pg - win_base];
+      const int64_t off = (int64_t)pid * page_bytes + (slot * row_bytes + f_ch16);
+      kreg[i] = *reinterpret_cast<const u32x4*>(kpool + off);
+      vreg[i] = *reinterpret_cast<const u32x4*>(vpool + off);
     }
   };
   auto stash = [&](int stage) {
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / kChunks;
-      const int ch = c % kChunks;
-      *reinterpret_cast<u32x4*>(&k_lds[stage][key * kPitch + ch * 8]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[stage][key * kPitch + ch * 8]) = vreg[i];
+      const int e = (f_key + (256 / kChunks) * i) * kPitch + f_ch16 / 2;
+      *reinterpret_cast<u32x4*>(&k_lds[stage][e]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&v_lds[stage][e]) = vreg[i];
     }
   };
   // first key of the window holding tile kt must cover the whole tile
@@ -237,58 +248,91 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
     }
     const int key0 = kt * kKeys;
     if (key0 < wave_kv_end) {
-      const bool full = key0 + kKeys <= wave_first_tok + 1 && key0 + kKeys <= kv_end;
+      // 32-key blocks. S^T comes from two 16-key MFMA tiles (keys kbase + 4gq + j and
+      // kbase + 16 + 4gq + j in a lane); P^T feeds one 16x16x32 MFMA per output tile
+      // whose k index 8gq + j stands for exactly those keys (j < 4: first tile,
+      // j >= 4: second), and the V operand is loaded for the same keys, so the
+      // key order inside the block is consistent and P.V is exact.
 #pragma unroll
-      for (int kb = 0; kb < kKeys / 16; ++kb) {
-        const int kbase = key0 + 16 * kb;
+      for (int kb = 0; kb < kKeys / 32; ++kb) {
+        const int kbase = key0 + 32 * kb;
         if (kbase >= wave_kv_end) break;
-        // K operand rows of this 16-key block, V operand rows 4*gq + j
-        u16x8 ka[kSteps];
-        const uint16_t* krow = &k_lds[stage][(16 * kb + r) * kPitch + 8 * gq];
+        const bool full = kbase + 32 <= wave_first_tok + 1 && kbase + 32 <= kv_end;
+        u16x8 ka[2][kSteps];
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) ka[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
-        VT va[4];
+        for (int t = 0; t < 2; ++t) {
+          const uint16_t* krow = &k_lds[stage][(32 * kb + 16 * t + r) * kPitch + 8 * gq];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          va[j] = *reinterpret_cast<const VT*>(&v_lds[stage][(16 * kb + 4 * gq + j) * kPitch + NT * r]);
+          for (int s = 0; s < kSteps; ++s) ka[t][s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
+        }
+        f32x4 sacc[2][2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            sacc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) sacc[cb][t] = T::mma_k32(ka[t][s], qb[cb][s], sacc[cb][t]);
+          }
+        // A operand of output tile n, V^T[d = 16n + r][keys of k = 8gq + j], read from the
+        // row-major tile with gfx950's transposing LDS read: in each 16-lane group, lane
+        // i = 4a + c receives element c of the 8-byte blocks addressed by lanes a, 4 + a,
+        // 8 + a and 12 + a. Lane r addresses keys kbase + 4gq + r/4 (then + 16), columns
+        // 16n + 4(r%4) .. +3, so it receives keys kbase + 4gq + 0..3 (+ 16) at d = 16n + r.
+        u16x8 va[NT];
+        {
+          const uint16_t* vsrc = &v_lds[stage][(32 * kb + 4 * gq + (r >> 2)) * kPitch + 4 * (r & 3)];
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            typedef short i16x4 __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) i16x4* lds_i16x4;
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n + 16 * kPitch));
+            va[n] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          }
+        }
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-          f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+          // raw scores; the softmax scale is applied inside the exponent's FMA. Only a
+          // block that touches the causal diagonal (or the end of the keys) is masked.
+          float sv[8];
+          if (full) {
 #pragma unroll
-          for (int s = 0; s < kSteps; ++s) sacc = T::mma_k32(ka[s], qb[cb][s], sacc);
-          float sv[4];
+            for (int j = 0; j < 8; ++j) sv[j] = sacc[cb][j >> 2][j & 3];
+          } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int key = kbase + 4 * gq + j;
-            const bool vis = full || (key < kv_end && key <= row_tok[cb]);
-            sv[j] = vis ? sacc[j] * p.scale_log2 : -INFINITY;
+            for (int j = 0; j < 8; ++j) {
+              const int key = kbase + 16 * (j >> 2) + 4 * gq + (j & 3);
+              sv[j] = (key < kv_end && key <= row_tok[cb]) ? sacc[cb][j >> 2][j & 3] : -INFINITY;
+            }
           }
-          float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-          mx = rows_max(mx);
-          if (__ballot(mx > m_run[cb] + kRescaleSlack)) {
-            const float m_new = fmaxf(m_run[cb], mx);
+          // Lazy rescale: the row's running max m is raised only when some score of the
+          // block exceeds it by more than the slack, which each lane checks on its own
+          // 8 scores; the cross-lane row max is needed only then.
+          const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))) * p.scale_log2;
+          if (__ballot(lmax > m_run[cb] + kRescaleSlack)) {
+            const float m_new = fmaxf(m_run[cb], rows_max(lmax));
             const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[cb] - m_new);
             l_run[cb] *= alpha;
 #pragma unroll
             for (int n = 0; n < NT; ++n) o[cb][n] *= alpha;
             m_run[cb] = m_new;
           }
-          float pj[4];
+          const float neg_m = m_run[cb] == -INFINITY ? 0.f : -m_run[cb];
+          u16x8 pb, pb_lo;
+          float pj[8];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) pj[j] = sv[j] == -INFINITY ? 0.f : fast_exp2(sv[j] - m_run[cb]);
-          l_run[cb] += (pj[0] + pj[1]) + (pj[2] + pj[3]);
-          u16x4 pb, pb_lo;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) pb[j] = T::from_f32(pj[j]);
-          if constexpr (kSplitP) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) pb_lo[j] = T::from_f32(pj[j] - T::to_f32(pb[j]));
+          for (int j = 0; j < 8; ++j) {
+            pj[j] = fast_exp2(fmaf(sv[j], p.scale_log2, neg_m));
+            pb[j] = T::from_f32(pj[j]);
+            if constexpr (kSplitP) pb_lo[j] = T::from_f32(pj[j] - T::to_f32(pb[j]));
           }
+          l_run[cb] += ((pj[0] + pj[1]) + (pj[2] + pj[3])) + ((pj[4] + pj[5]) + (pj[6] + pj[7]));
 #pragma unroll
           for (int n = 0; n < NT; ++n) {
-            u16x4 a = {va[0][n], va[1][n], va[2][n], va[3][n]};
-            o[cb][n] = T::mma_k16(a, pb, o[cb][n]);
-            if constexpr (kSplitP) o[cb][n] = T::mma_k16(a, pb_lo, o[cb][n]);
+            o[cb][n] = T::mma_k32(va[n], pb, o[cb][n]);
+            if constexpr (kSplitP) o[cb][n] = T::mma_k32(va[n], pb_lo, o[cb][n]);
           }
         }
       }
@@ -317,12 +361,13 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
     const int t = row / G;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = p.out + (int64_t)(q0 + t) * p.out_stride + (int64_t)(h * G + row % G) * D;
+    // lane holds O[row][16n + 4gq + i] in o[cb][n][i]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      VT w;
+    for (int n = 0; n < NT; ++n) {
+      u16x4 w;
 #pragma unroll
-      for (int n = 0; n < NT; ++n) w[n] = T::from_f32(o[cb][n][i] * inv);
-      *reinterpret_cast<VT*>(orow + NT * (4 * gq + i)) = w;
+      for (int i = 0; i < 4; ++i) w[i] = T::from_f32(o[cb][n][i] * inv);
+      *reinterpret_cast<u16x4*>(orow + 16 * n + 4 * gq) = w;
     }
   }
 }
