@@ -26,9 +26,10 @@
 namespace nslg {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerWG = kWaves * kRowsPerWave;  // 128
+constexpr int kRowsPerWG = kWaves * kRowsPerWave;  // 256
 constexpr int kKeys = 64;                          // keys per LDS tile
 constexpr int kPageWin = 2048;                     // page ids per LDS window
 constexpr float kRescaleSlack = 8.0f;
@@ -51,6 +52,9 @@ struct PrefillParams {
   float scale_log2;
   uint16_t* out;
   int64_t out_stride;
+  int32_t row_tiles;  // row-tile slots per KV head (an upper bound over the batch)
+  int32_t num_work;   // row_tiles * num_kv_heads
+  int32_t per_xcd;    // ceil(num_work / 8)
 };
 
 template <int N>
@@ -97,7 +101,7 @@ __device__ inline bool locate_tile(const PrefillParams& p, int g, int& b, int& t
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p) {
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
   constexpr int kPitch = D + 8;  // LDS row pitch in elements (16 B pad vs bank conflicts)
@@ -110,9 +114,14 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int h = blockIdx.y;
+  // XCD-aware order: workgroup i runs on XCD i % 8, so work item
+  // w = (i % 8) * per_xcd + i / 8 gives each XCD a contiguous run of row tiles of
+  // one KV head, which read the same K/V and so share that XCD's L2.
+  const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+  if (w >= p.num_work) return;
+  const int h = w / p.row_tiles;
   int b = 0, tile = 0;
-  if (!locate_tile(p, blockIdx.x, b, tile)) return;  // uniform across the workgroup
+  if (!locate_tile(p, w - h * p.row_tiles, b, tile)) return;  // uniform across the workgroup
   b = __builtin_amdgcn_readfirstlane(b);
   tile = __builtin_amdgcn_readfirstlane(tile);
 
@@ -172,14 +181,14 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
 
   // ---- cooperative tile loads: 64 keys x D for K and V, 16 B per thread-chunk ------
   constexpr int kChunks = D / 8;                       // 16 B chunks per row
-  constexpr int kPerThread = kKeys * kChunks / 256;    // 4 (D=128) or 2 (D=64)
+  constexpr int kPerThread = kKeys * kChunks / kThreads;  // 2 (D=128) or 1 (D=64)
   u32x4 kreg[kPerThread], vreg[kPerThread];
   int win_base = -1;
 
   auto load_pages = [&](int first_key) {
     // page ids for keys [first_key, first_key + kPageWin*ps), one window
     const int pg0 = first_key / ps;
-    for (int i = tid; i < kPageWin; i += 256) {
+    for (int i = tid; i < kPageWin; i += kThreads) {
       int v = 0;
       if (pg0 + i < np_seq) {
         v = idx[pg0 + i];
@@ -189,7 +198,7 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
     }
     win_base = pg0;
   };
-  // thread tid moves 16-byte chunk tid % kChunks of keys tid / kChunks + (256 / kChunks) i
+  // thread tid moves 16-byte chunk tid % kChunks of keys tid / kChunks + (kThreads / kChunks) i
   const int f_ch16 = (tid % kChunks) * 16;
   const int f_key = tid / kChunks;
   const bool ps_pow2 = (ps & (ps - 1)) == 0;
@@ -199,7 +208,7 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
     const int key0 = kt * kKeys;
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
-      int kabs = key0 + f_key + (256 / kChunks) * i;
+      int kabs = key0 + f_key + (kThreads / kChunks) * i;
       kabs = kabs < kv_end ? kabs : kv_end - 1;
       int pg, slot;
       if (ps_pow2) {
@@ -218,7 +227,7 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(PrefillParams p) {
   auto stash = [&](int stage) {
 #pragma unroll
     for (int i = 0; i < kPerThread; ++i) {
-      const int e = (f_key + (256 / kChunks) * i) * kPitch + f_ch16 / 2;
+      const int e = (f_key + (kThreads / kChunks) * i) * kPitch + f_ch16 / 2;
       *reinterpret_cast<u32x4*>(&k_lds[stage][e]) = kreg[i];
       *reinterpret_cast<u32x4*>(&v_lds[stage][e]) = vreg[i];
     }
@@ -381,8 +390,7 @@ inline int64_t grid_tiles(int64_t total_q, int32_t batch, int group) {
 
 template <typename T, int D>
 int launch_prefill(const PrefillParams& p, int64_t tiles, hipStream_t s) {
-  dim3 grid((unsigned)tiles, p.num_kv_heads);
-  paged_prefill_kernel<T, D><<<grid, 256, 0, s>>>(p);
+  paged_prefill_kernel<T, D><<<dim3((unsigned)(8 * p.per_xcd)), kThreads, 0, s>>>(p);
   return check_launch("paged_prefill");
 }
 
@@ -456,6 +464,10 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.out = (uint16_t*)out;
   p.out_stride = out_stride;
+  if (tiles * num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
+  p.row_tiles = (int32_t)tiles;
+  p.num_work = (int32_t)(tiles * num_kv_heads);
+  p.per_xcd = (p.num_work + 7) / 8;
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) return head_dim == 64 ? launch_prefill<F16, 64>(p, tiles, s) : launch_prefill<F16, 128>(p, tiles, s);
   return head_dim == 64 ? launch_prefill<BF16, 64>(p, tiles, s) : launch_prefill<BF16, 128>(p, tiles, s);
