@@ -698,29 +698,51 @@ class PagedCacheContext(CacheContext):
             q_rows = np.arange(B, dtype=np.int64)
             qo = np.arange(B + 1, dtype=np.int64)
         else:
-            slot = np.full((B, iw), -1, np.int32)
+            ncnt = np.fromiter(self.new_token_counts, np.int64, B)
+            start = np.fromiter(self.start_positions, np.int64, B)
+            have = np.fromiter((st.n_pages for st in states), np.int64, B)
+            # copy-on-write first, in batch order: a sequence writes its pages
+            # start//ps .. (start+n-1)//ps (those it has); shared ones are copied
             for b, st in enumerate(states):
-                n = self.new_token_counts[b]
+                n = int(ncnt[b])
                 if n <= 0:
                     continue
-                ap = np.arange(st.num_tokens, st.num_tokens + n, dtype=np.int64)
-                pi = ap // ps
-                for p in range(int(pi[0]), min(int(pi[-1]) + 1, st.n_pages)):
-                    if pool.is_shared(int(st.bt[p])):
-                        _cow(st, p)
-                ok = pi < st.n_pages
-                pids = np.where(ok, st.bt[np.minimum(pi, max(st.n_pages - 1, 0))] if st.n_pages else 0, 0)
-                sls = np.where(ok, ap % ps, 0)
-                o = self.input_offsets[b]
-                slot[b, o:o + n] = (pids * ps + sls).astype(np.int32)
-                if ok.any():
-                    np.maximum.at(pool.tokens_used, pids[ok], sls[ok] + 1)
+                p0 = int(start[b]) // ps
+                p1 = min((int(start[b]) + n - 1) // ps + 1, st.n_pages)
+                if p1 > p0 and bool((pool.ref_count[st.bt[p0:p1]] > 1).any()):
+                    for p in range(p0, p1):
+                        if pool.is_shared(int(st.bt[p])):
+                            _cow(st, p)
             # CSR block table (kv_cache.py:598-615)
-            lens = np.asarray(self.seq_lens, np.int64)
+            lens = start + ncnt
             npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
             indptr = np.zeros(B + 1, np.int64)
             np.cumsum(npg, out=indptr[1:])
             indices = self._csr_indices(states, npg)
+            # per new token: absolute position, page, slot; past a sequence's pages the
+            # write goes to the null page's slot 0 (kv_cache.py:583-584)
+            slot = np.full(B * iw, -1, np.int32)
+            T = int(ncnt.sum())
+            if T:
+                rep = np.repeat(np.arange(B), ncnt)
+                first = np.zeros(B, np.int64)
+                np.cumsum(ncnt[:-1], out=first[1:])
+                t_in = np.arange(T, dtype=np.int64) - first[rep]
+                ap = start[rep] + t_in
+                pi = ap // ps
+                ok = pi < have[rep]
+                pids = np.where(ok, indices[indptr[rep] + pi], 0).astype(np.int64)
+                sls = np.where(ok, ap - pi * ps, 0)
+                offs = np.fromiter(self.input_offsets, np.int64, B)
+                slot[rep * iw + offs[rep] + t_in] = (pids * ps + sls).astype(np.int32)
+                # tokens_used: each written page once, with its last (largest) slot;
+                # the pages written are distinct after copy-on-write
+                wp, ws = pids[ok], sls[ok]
+                if wp.size:
+                    last = np.flatnonzero(np.append(wp[1:] != wp[:-1], True))
+                    pu = wp[last]
+                    pool.tokens_used[pu] = np.maximum(pool.tokens_used[pu], ws[last] + 1)
+            slot = slot.reshape(B, iw)
             lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
             if B == 0:
                 lpl = np.zeros(1, np.int64)
