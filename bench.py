@@ -468,6 +468,17 @@ def run_radix(args):
         st.num_tokens = PRE
     mgr.release_sequence("owner")
     assert mgr.pool.ref_count[owner_pages[full]] == B
+    # warm the ragged prefill path (first use loads the gather/scatter kernels) on a
+    # throwaway cache, so the timed forward below measures the work, not the loading
+    scratch = PagedKVCache(KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D,
+                                         page_size=PS, max_pages=64, dtype=torch.float16, device=dev,
+                                         enable_prefix_caching=False, backend="paged"))
+    for sid in ("w0", "w1"):
+        scratch.allocate_sequence(sid)
+    wctx = scratch.begin_forward(["w0", "w1"], [5, 3])
+    wctx.attend(0, randn(2, 5, HQ, D), randn(2, 5, HKV, D), randn(2, 5, HKV, D), HQ, HKV)
+    scratch.end_forward(wctx)
+    del scratch, wctx
     # suffix prefill with copy-on-write of the shared page
     S = max(suffix)
     q, k, v = randn(B, S, HQ, D), randn(B, S, HKV, D), randn(B, S, HKV, D)
