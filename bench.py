@@ -293,9 +293,18 @@ def cpu_baseline_sample(lens, seed, budget_s=12.0, max_steps=32):
         model = open("/proc/cpuinfo").read().split("model name")[1].split(":")[1].split("\n")[0].strip()
     except Exception:
         model = "unknown"
+    # the reference's own CPU case: B=1, 512-token context, 64 decode steps, fp32
+    # (median of 5 repeats after 8 warmup steps)
+    sec, _ = O.timed_contiguous_decode(num_steps=64, prefill=512, Hq=HQ, Hkv=HKV, D=D, seed=seed, warmup=8,
+                                       repeats=5, threads=threads)
+    lens1 = [512 + 8 + i + 1 for i in range(64)]
+    b1 = np.mean([2 * HKV * D * 4 * L + 2 * HKV * D * 4 * 2 + 2 * HQ * D * 4 for L in lens1])
+    contiguous_b1 = {"ms_per_step": round(sec * 1e3, 4), "tok_s_layer": round(1.0 / sec, 1),
+                     "GB_s": round(float(b1) / sec / 1e9, 3), "context": "521..584 tokens", "repeats": 5}
     return {
         "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
+        "contiguous_b1_ctx512": contiguous_b1,
         "tok_s_layer": round(B * steps / dt, 2),
         "ms_per_step": round(dt / steps * 1e3, 3),
         "cores": threads,
