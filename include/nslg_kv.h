@@ -177,6 +177,31 @@ int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr
                        void* workspace, size_t workspace_bytes,
                        nslg_stream_t stream);
 
+/*
+ * Device-side plan of one decode step in which every sequence gains one token:
+ * the CSR block table, slot mapping and positions of the next step from those of
+ * this one. Replaces, for a steady decode batch, the per-step rebuild of the CSR
+ * in FlashInferCacheContext._plan_flashinfer (nanoslg/kv_cache.py:598-615) and the
+ * write plan of FlashInferCacheContext.__init__ (kv_cache.py:575-594) when no page
+ * is shared (copy-on-write still goes through the host plan).
+ *
+ *   kv_indptr/kv_indices/kv_last_page_len   this step's CSR (device), batch rows
+ *   new_page        HOST int32[batch]: the page sequence b opens this step (when its
+ *                   last page is full or it has none), else -1; a sequence that
+ *                   needs a page and gets -1 writes to the null page 0, slot 0
+ *   *_out           the next step's CSR (device; indices capacity kv_indptr[batch]
+ *                   + the pages opened), must not alias the inputs
+ *   slot_mapping_out[b]  page * page_size + slot of sequence b's new token
+ *   positions_out[b]     its position (the sequence's length minus one)
+ *   new_pages_out   the pages opened, in batch order (for nslg_zero_pages)
+ * batch <= 512. Bit-exact with the host plan.
+ */
+int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
+                          const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                          const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
+                          int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
+                          int32_t* positions_out, int32_t* new_pages_out, nslg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

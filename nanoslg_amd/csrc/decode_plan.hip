@@ -1,0 +1,134 @@
+// Device-side plan of one decode step: the CSR block table, slot mapping and
+// positions of step i+1 from those of step i, for a batch in which every sequence
+// gains exactly one token.
+//
+// The host only says which sequences opened a page this step and which page it
+// got (a few entries per step at batch 64, passed in the kernel arguments), so a
+// steady decode step moves no plan bytes over PCIe and the compute stream never
+// waits on a copy. Workgroup b rebuilds sequence b's segment: its offset is the
+// prefix sum of the new page counts (recomputed per workgroup from kv_indptr,
+// which is a few hundred bytes), its page ids are copied and the new page, if
+// any, is appended; lane 0 writes the sequence's last-page length, the slot of the
+// new token and its position, and the id of the new page into the list of pages
+// to zero.
+#include "nslg_common.h"
+
+namespace nslg {
+namespace {
+
+constexpr int kMaxPlanBatch = 512;
+
+struct PlanStepArgs {
+  const int32_t* indptr_in;
+  const int32_t* indices_in;
+  const int32_t* last_len_in;
+  int32_t* indptr_out;
+  int32_t* indices_out;
+  int32_t* last_len_out;
+  int32_t* slot_out;
+  int32_t* pos_out;
+  int32_t* new_pages_out;
+  int32_t batch;
+  int32_t page_size;
+  int32_t new_page[kMaxPlanBatch];  // page opened by sequence b this step, or -1
+};
+
+// Pages of sequence s before the step, and whether this step opens one.
+__device__ inline void seq_step(const PlanStepArgs& a, int s, int& np_in, int& lpl_in, bool& opens) {
+  np_in = a.indptr_in[s + 1] - a.indptr_in[s];
+  lpl_in = np_in > 0 ? a.last_len_in[s] : a.page_size;
+  lpl_in = lpl_in < 1 ? 1 : (lpl_in > a.page_size ? a.page_size : lpl_in);
+  opens = lpl_in == a.page_size;
+}
+
+__global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs a) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // offset of sequence b's segment in the new table, and the number of new pages
+  // opened by sequences before b (its index in the zero list); the first wave
+  // computes both, the other waves only copy
+  __shared__ int seg_out_sh, new_before_sh;
+  if (tid < 64) {
+    int pages = 0, opened = 0;
+    for (int s = lane; s < b; s += 64) {
+      int np_in, lpl_in;
+      bool opens;
+      seq_step(a, s, np_in, lpl_in, opens);
+      pages += np_in + (opens ? 1 : 0);
+      opened += opens ? 1 : 0;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      pages += __shfl_xor(pages, off, 64);
+      opened += __shfl_xor(opened, off, 64);
+    }
+    if (tid == 0) {
+      seg_out_sh = pages;
+      new_before_sh = opened;
+    }
+  }
+  __syncthreads();
+  const int seg_out = seg_out_sh;
+  int np_in, lpl_in;
+  bool opens;
+  seq_step(a, b, np_in, lpl_in, opens);
+  const int seg_in = a.indptr_in[b];
+  for (int i = tid; i < np_in; i += blockDim.x) a.indices_out[seg_out + i] = a.indices_in[seg_in + i];
+  if (tid == 0) {
+    int page;  // the page the new token goes to
+    int lpl;
+    if (opens) {
+      page = a.new_page[b];
+      if (page < 0) page = 0;  // no page given: the null page (the sink of writes past a table)
+      a.indices_out[seg_out + np_in] = page;
+      a.new_pages_out[new_before_sh] = page;
+      lpl = 1;
+    } else {
+      page = a.indices_in[seg_in + np_in - 1];
+      lpl = lpl_in + 1;
+    }
+    const int np_out = np_in + (opens ? 1 : 0);
+    a.last_len_out[b] = lpl;
+    a.indptr_out[b + 1] = seg_out + np_out;
+    if (b == 0) a.indptr_out[0] = 0;
+    a.slot_out[b] = page * a.page_size + (lpl - 1);
+    a.pos_out[b] = (np_out - 1) * a.page_size + (lpl - 1);
+  }
+}
+
+}  // namespace
+}  // namespace nslg
+
+using namespace nslg;
+
+extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
+                                     const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                                     const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
+                                     int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
+                                     int32_t* positions_out, int32_t* new_pages_out, nslg_stream_t stream) {
+  if (batch < 0 || page_size <= 0) return fail(NSLG_EINVAL, "decode_plan_step: bad sizes");
+  if (batch == 0) return NSLG_OK;
+  if (batch > kMaxPlanBatch)
+    return fail(NSLG_EUNSUPPORTED, "decode_plan_step: batch %d > %d", batch, kMaxPlanBatch);
+  if (!kv_indptr || !kv_indices || !kv_last_page_len || !new_page || !kv_indptr_out || !kv_indices_out ||
+      !kv_last_page_len_out || !slot_mapping_out || !positions_out || !new_pages_out)
+    return fail(NSLG_EINVAL, "decode_plan_step: null pointer");
+  if (kv_indices_out == kv_indices || kv_indptr_out == kv_indptr || kv_last_page_len_out == kv_last_page_len)
+    return fail(NSLG_EINVAL, "decode_plan_step: output tables must not alias the input ones");
+  PlanStepArgs a;
+  a.indptr_in = kv_indptr;
+  a.indices_in = kv_indices;
+  a.last_len_in = kv_last_page_len;
+  a.indptr_out = kv_indptr_out;
+  a.indices_out = kv_indices_out;
+  a.last_len_out = kv_last_page_len_out;
+  a.slot_out = slot_mapping_out;
+  a.pos_out = positions_out;
+  a.new_pages_out = new_pages_out;
+  a.batch = batch;
+  a.page_size = page_size;
+  for (int b = 0; b < batch; ++b) a.new_page[b] = new_page[b];
+  decode_plan_step_kernel<<<batch, 256, 0, as_stream(stream)>>>(a);
+  return check_launch("decode_plan_step");
+}

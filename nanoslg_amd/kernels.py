@@ -204,6 +204,35 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     return out
 
 
+def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                     new_page, page_size: int, num_new: int):
+    """Next decode step's plan on the device (every sequence gains one token).
+
+    new_page: host int32 array [B], the page sequence b opens this step or -1; num_new:
+    how many entries are >= 0. Returns device int32 tensors (indptr [B+1], indices,
+    last_page_len [B], slot_mapping [B], positions [B], new_pages [num_new])."""
+    import numpy as np
+    _require_gpu(kv_indptr, kv_indices, kv_last_page_len)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, n)
+    B = kv_indptr.numel() - 1
+    new_page = np.ascontiguousarray(new_page, dtype=np.int32)
+    if new_page.shape != (B,):
+        raise ValueError(f"decode_plan_step: new_page must have {B} entries")
+    total_in = kv_indices.numel()
+    cap = total_in + num_new
+    buf = torch.empty(B + 1 + cap + 3 * B + max(num_new, 1), dtype=torch.int32, device=kv_indptr.device)
+    o = [0, B + 1, B + 1 + cap, 2 * B + 1 + cap, 3 * B + 1 + cap, 4 * B + 1 + cap]
+    indptr, indices, lpl = buf[o[0]:o[1]], buf[o[1]:o[2]], buf[o[2]:o[3]]
+    slot, pos, new = buf[o[3]:o[4]], buf[o[4]:o[5]], buf[o[5]:o[5] + num_new]
+    rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                                          B, int(page_size), new_page.ctypes.data, indptr.data_ptr(),
+                                          indices.data_ptr(), lpl.data_ptr(), slot.data_ptr(), pos.data_ptr(),
+                                          buf[o[5]:].data_ptr(), _stream(kv_indptr))
+    _lib.check(rc, "nslg_decode_plan_step")
+    return indptr, indices, lpl, slot, pos, new
+
+
 class DecodeLaunch:
     """Append + split-K decode for every layer of one decode forward.
 

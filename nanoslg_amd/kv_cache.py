@@ -323,6 +323,21 @@ class _ForwardPlan:
         self._slot_by_S: Dict[int, torch.Tensor] = {iw: self.slot}
         self._pos_long: Optional[torch.Tensor] = None
 
+    @classmethod
+    def from_device(cls, batch, slot, pos, indptr, indices, lpl, qo_indptr, q_rows, zero_ids, total_pages):
+        """A decode plan whose tables were built on the device (decode_plan_step)."""
+        self = cls.__new__(cls)
+        self.slot, self.pos_i32, self.indptr, self.indices, self.lpl = slot, pos, indptr, indices, lpl
+        self.qo_indptr, self.q_rows = qo_indptr, q_rows
+        self.cow_src = self.cow_dst = slot[:0]
+        self.zero_ids = zero_ids
+        self.batch, self.iw = batch, 1
+        self.total_pages = int(total_pages)
+        self.total_q = batch
+        self._slot_by_S = {1: slot}
+        self._pos_long = None
+        return self
+
     def slots_for(self, S: int) -> torch.Tensor:
         s = self._slot_by_S.get(S)
         if s is None:
@@ -663,6 +678,15 @@ class PagedCacheContext(CacheContext):
             st.bt[p] = new
             pool.release(pid)
 
+        self._decode_launch = None
+        if self._is_decode and iw == 1:
+            plan = cache._advance_decode_plan(self.seq_ids, states, zero_pages)
+            if plan is not None:
+                self.cow_pairs = []
+                self._max_q, self._uniform_rows = 1, True
+                self._plan = plan
+                cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
+                return
         if self._is_decode and iw == 1:
             # One token per sequence, vectorised over the batch. The page written by
             # sequence b is the last page of its CSR segment; only a page that is shared
@@ -748,7 +772,6 @@ class PagedCacheContext(CacheContext):
                 lpl = np.zeros(1, np.int64)
             pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
         self.cow_pairs = list(zip(cow_src, cow_dst))
-        self._decode_launch = None
         if indices.size == 0:
             indices = np.zeros(1, np.int32)
         self._max_q = max(self.new_token_counts) if B else 0
@@ -761,6 +784,8 @@ class PagedCacheContext(CacheContext):
             cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
             cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
+        if self._is_decode and iw == 1:
+            cache._record_decode_plan(self.seq_ids, self._plan, self.seq_lens)
 
     @staticmethod
     def _csr_indices(states, npg) -> np.ndarray:
@@ -827,9 +852,58 @@ class PagedKVCache(KVCacheManager):
         self.seqs: Dict[str, _PagedSeqState] = {}
         self.workspace = self.kernels.Workspace(self.pool.device, 128 << 20)
         self._pending_zero: List[int] = []
+        self._dev_plan = None  # the last decode forward's plan: (ids, plan, lens), see below
+        self._decode_rows: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+
+    # ---- decode plans built on the device ---------------------------------------------
+    def _record_decode_plan(self, seq_ids, plan, seq_lens) -> None:
+        self._dev_plan = (tuple(seq_ids), plan, np.asarray(seq_lens, np.int64))
+
+    def _advance_decode_plan(self, seq_ids, states, zero_pages) -> Optional[_ForwardPlan]:
+        """This decode forward's plan built on the device from the previous one
+        (kernels.decode_plan_step), when the batch is the one the previous decode
+        forward planned, every sequence gained exactly that token, and no written page
+        is shared; otherwise None and the host builds the plan. The result is the same
+        plan as the host's, bit for bit."""
+        prev = self._dev_plan
+        kern = self.kernels
+        if prev is None or prev[0] != tuple(seq_ids) or not hasattr(kern, "decode_plan_step"):
+            return None
+        B, ps, pool = len(states), self.cfg.page_size, self.pool
+        if B == 0 or B > 512:
+            return None
+        start = np.fromiter((st.num_tokens for st in states), np.int64, B)
+        if not np.array_equal(start, prev[2]):
+            return None
+        npg = start // ps + 1
+        if not np.array_equal(np.fromiter((st.n_pages for st in states), np.int64, B), npg):
+            return None
+        opens = start % ps == 0
+        pids = np.fromiter((int(st.bt[k - 1]) for st, k in zip(states, npg.tolist())), np.int64, B)
+        if bool((pool.ref_count[pids] > 1).any()):
+            return None  # a shared page is written: copy-on-write goes through the host plan
+        new_page = np.where(opens, pids, -1).astype(np.int32)
+        n_new = int(opens.sum())
+        if sorted(zero_pages or []) != sorted(pids[opens].tolist()):
+            return None
+        sl = start % ps
+        pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
+        plan = prev[1]
+        indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
+                                                                    new_page, ps, n_new)
+        rows = self._decode_rows.get(B)
+        if rows is None:
+            qo, qr = _upload_i32([np.arange(B + 1, dtype=np.int32), np.arange(B, dtype=np.int32)], pool.device)
+            rows = self._decode_rows[B] = (qo, qr)
+        out = _ForwardPlan.from_device(B, slot, pos, indptr, indices, lpl, rows[0], rows[1], new,
+                                       plan.total_pages + n_new)
+        if n_new:
+            kern.zero_pages(pool.k, pool.v, new)
+        return out
 
     def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
         """kv_cache.py:707-722: radix match (full pages), pin, allocate the rest."""
+        self._dev_plan = None
         tids = list(token_ids or [])
         total = len(tids) if tids else num_tokens
         plen, ppages = 0, []
@@ -854,6 +928,8 @@ class PagedKVCache(KVCacheManager):
 
     def begin_forward(self, seq_ids, ntoks, offsets=None):
         ps = self.cfg.page_size
+        if any(n != 1 for n in ntoks):
+            self._dev_plan = None
         for s, n in zip(seq_ids, ntoks):  # extend_sequence, inlined
             st = self.seqs[s]
             need = -(-(st.num_tokens + n) // ps)
@@ -868,6 +944,7 @@ class PagedKVCache(KVCacheManager):
 
     def release_sequence(self, seq_id):
         """kv_cache.py:739-751: cache full pages in the tree, unpin, release."""
+        self._dev_plan = None
         st = self.seqs.get(seq_id)
         if st is None:
             return

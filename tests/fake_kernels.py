@@ -110,3 +110,28 @@ class DecodeLaunch:
         k_layer, v_layer = self.k_pool[layer], self.v_pool[layer]
         append_kv(k_new, v_new, slots, k_layer, v_layer)
         return paged_decode(q, k_layer, v_layer, indptr, indices, lpl, total, sm_scale=self.sm_scale)
+
+
+def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new):
+    """As nanoslg_amd.kernels.decode_plan_step, in plain Python on the CPU."""
+    CALLS.append(("decode_plan_step", int(kv_indptr.numel() - 1)))
+    ip, idx, lpl = kv_indptr.tolist(), kv_indices.tolist(), kv_last_page_len.tolist()
+    out_ip, out_idx, out_lpl, slots, pos, new = [0], [], [], [], [], []
+    for b in range(len(ip) - 1):
+        seg = idx[ip[b]:ip[b + 1]]
+        last = min(max(lpl[b] if seg else page_size, 1), page_size)
+        if last == page_size:
+            page = int(new_page[b]) if new_page[b] >= 0 else 0
+            seg = seg + [page]
+            new.append(page)
+            last = 1
+        else:
+            page = seg[-1]
+            last += 1
+        out_idx += seg
+        out_ip.append(len(out_idx))
+        out_lpl.append(last)
+        slots.append(page * page_size + last - 1)
+        pos.append((len(seg) - 1) * page_size + last - 1)
+    t = lambda x: torch.tensor(x, dtype=torch.int32)  # noqa: E731
+    return t(out_ip), t(out_idx), t(out_lpl), t(slots), t(pos), t(new)

@@ -20,7 +20,8 @@ def test_header_declares_the_hot_path():
     syms = declared_symbols()
     for name in ["nslg_append_kv", "nslg_zero_pages", "nslg_copy_pages", "nslg_gather_kv",
                  "nslg_paged_decode", "nslg_paged_decode_workspace_size", "nslg_paged_prefill",
-                 "nslg_paged_prefill_workspace_size", "nslg_version", "nslg_last_error"]:
+                 "nslg_paged_prefill_workspace_size", "nslg_decode_plan_step", "nslg_version",
+                 "nslg_last_error"]:
         assert name in syms
 
 
@@ -51,6 +52,12 @@ def test_host_side_argument_checks():
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 34, 8, 128, 0.1, 0, 256, 4096,
                                None, 0, None)
     assert rc == -1  # Hq not a multiple of Hkv
+    # device decode planner: too large a batch, null pointers, aliased outputs
+    assert lib.nslg_decode_plan_step(1, 1, 1, 513, 16, 1, 2, 2, 2, 2, 2, 2, None) == -2
+    assert lib.nslg_decode_plan_step(None, 1, 1, 4, 16, 1, 2, 2, 2, 2, 2, 2, None) == -1
+    assert lib.nslg_decode_plan_step(1, 1, 1, 4, 16, 1, 2, 1, 2, 2, 2, 2, None) == -1
+    assert lib.nslg_decode_plan_step(None, None, None, 0, 16, None, None, None, None, None, None, None,
+                                     None) == 0
 
 
 def test_decode_workspace_size_monotone():

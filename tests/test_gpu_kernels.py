@@ -417,3 +417,45 @@ def test_decode_launch_matches_separate_calls():
         launch(0, q[:2], kn, vn)
     with pytest.raises(IndexError):
         launch(L, q, kn, vn)
+
+
+@pytest.mark.parametrize("B,ps", [(64, 16), (1, 16), (37, 32), (512, 8)])
+def test_decode_plan_step_bit_exact(B, ps):
+    """The device-built next-step plan equals the CSR the oracle builds from the
+    extended block tables (kv_cache.py:598-615), with slots and positions of the new
+    tokens; sequences with a full last page or no page open the page they are given,
+    or the null page when given none."""
+    _log(f"decode plan step B={B} ps={ps}")
+    from nanoslg_amd import kernels as K
+    rng = np.random.default_rng(73 + B)
+    lens = [int(x) for x in rng.integers(0, 3000, size=B)]
+    for b in range(0, B, 5):
+        lens[b] = ps * (b % 7)  # full last page (or empty)
+    npg = [math.ceil(L / ps) for L in lens]
+    perm = rng.permutation(np.arange(1, sum(npg) + B + 10)).tolist()
+    tables, off = [], 0
+    for n in npg:
+        tables.append(perm[off:off + n])
+        off += n
+    spare = perm[off:]
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    opens = [L % ps == 0 for L in lens]
+    new_page = np.full(B, -1, np.int32)
+    for b in range(B):
+        if opens[b] and b % 11 != 3:  # a few openers get no page: the null page
+            new_page[b] = spare.pop()
+    exp_tables = [t + ([int(new_page[b]) if new_page[b] >= 0 else 0] if opens[b] else []) for b, t in enumerate(tables)]
+    exp_lens = [L + 1 for L in lens]
+    e_indptr, e_indices, e_lpl = O.plan_csr(exp_tables, exp_lens, ps)
+    e_slot = [exp_tables[b][L // ps] * ps + L % ps for b, L in enumerate(lens)]
+    e_new = [t[-1] for b, t in enumerate(exp_tables) if opens[b]]
+    out = K.decode_plan_step(torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV),
+                             torch.from_numpy(lpl).to(DEV), new_page, ps, int(sum(opens)))
+    torch.cuda.synchronize()
+    ip, ix, lp, sl, pos, new = (t.cpu().numpy() for t in out)
+    assert np.array_equal(ip, e_indptr)
+    assert np.array_equal(ix[:e_indptr[-1]], e_indices[:e_indptr[-1]])
+    assert np.array_equal(lp, e_lpl)
+    assert np.array_equal(sl, np.array(e_slot, np.int32))
+    assert np.array_equal(pos, np.array(lens, np.int32))
+    assert np.array_equal(new, np.array(e_new, np.int32))

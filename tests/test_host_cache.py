@@ -346,3 +346,57 @@ def test_stats_and_reset():
     mgr.seqs["a"].num_tokens = 9
     mgr.reset()
     assert mgr.stats["active_seqs"] == 0 and mgr.stats["radix"] == 2 and mgr.pool.num_free == 13
+
+
+def test_device_decode_plan_matches_host_plan():
+    """Steady decode steps build their plan from the previous one (decode_plan_step);
+    each such plan equals, entry for entry, the plan the host builds for the same
+    step, and pages, refcounts and tokens_used stay identical. Batch changes, prefill
+    and shared pages fall back to the host plan."""
+    g = torch.Generator().manual_seed(11)
+    fast, _ = make(ps=4, pages=96, prefix=False)
+    slow, _ = make(ps=4, pages=96, prefix=False)
+    slow._advance_decode_plan = lambda *a: None
+    ids = ["a", "b", "c", "d"]
+    for m in (fast, slow):
+        for s, n in zip(ids, [5, 8, 1, 3]):
+            m.allocate_sequence(s, num_tokens=n)
+
+    def step(ntok, sids, expect_fast=None):
+        S = max(ntok)
+        B = len(sids)
+        q = torch.randn(B, S, HQ, D, generator=g)
+        k = torch.randn(B, S, HKV, D, generator=g)
+        v = torch.randn(B, S, HKV, D, generator=g)
+        FK.CALLS.clear()
+        c1 = fast.begin_forward(sids, ntok)
+        used_fast = any(name == "decode_plan_step" for name, _ in FK.CALLS)
+        c2 = slow.begin_forward(sids, ntok)
+        if expect_fast is not None:
+            assert used_fast == expect_fast
+        p1, p2 = c1.plan, c2.plan
+        for name in ("indptr", "indices", "lpl", "slot", "pos_i32", "zero_ids"):
+            a, b = getattr(p1, name), getattr(p2, name)
+            assert torch.equal(a.to(torch.int64), b.to(torch.int64)), name
+        assert p1.total_pages == p2.total_pages
+        o1 = c1.attend(0, q, k, v, HQ, HKV)
+        o2 = c2.attend(0, q, k, v, HQ, HKV)
+        assert torch.equal(o1, o2)
+        fast.end_forward(c1)
+        slow.end_forward(c2)
+        assert np.array_equal(fast.pool.ref_count, slow.pool.ref_count)
+        assert np.array_equal(fast.pool.tokens_used, slow.pool.tokens_used)
+
+    step([5, 8, 1, 3], ids, expect_fast=False)       # prefill
+    step([1, 1, 1, 1], ids, expect_fast=False)       # first decode: host plan
+    for _ in range(13):                               # crosses page boundaries
+        step([1, 1, 1, 1], ids, expect_fast=True)
+    for m in (fast, slow):
+        m.release_sequence("b")
+    step([1, 1, 1], ["a", "c", "d"], expect_fast=False)  # batch changed
+    step([1, 1, 1], ["a", "c", "d"], expect_fast=True)
+    # a shared last page (refcount 2) must go through copy-on-write on the host
+    for m in (fast, slow):
+        m.pool.add_ref(int(m.seqs["c"].bt[m.seqs["c"].n_pages - 1]))
+    step([1, 1, 1], ["a", "c", "d"], expect_fast=False)
+    step([1, 1, 1], ["a", "c", "d"], expect_fast=True)
