@@ -193,14 +193,19 @@ int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr
  *                   + the pages opened), must not alias the inputs
  *   slot_mapping_out[b]  page * page_size + slot of sequence b's new token
  *   positions_out[b]     its position (the sequence's length minus one)
- *   new_pages_out   the pages opened, in batch order (for nslg_zero_pages)
+ *   new_pages_out   the pages opened, in batch order
+ *   k_pool, v_pool  NULL, or the [L, P, page_size, Hkv, D] pools: then the opened
+ *                   pages are also zeroed in every layer, K and V, in the same launch
+ *                   (the zero-on-alloc of PagePool.alloc, kv_cache.py:411)
  * batch <= 512. Bit-exact with the host plan.
  */
 int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
                           const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
                           const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
                           int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
-                          int32_t* positions_out, int32_t* new_pages_out, nslg_stream_t stream);
+                          int32_t* positions_out, int32_t* new_pages_out, void* k_pool, void* v_pool,
+                          int32_t num_layers, int64_t num_pages, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t dtype, nslg_stream_t stream);
 
 #ifdef __cplusplus
 }

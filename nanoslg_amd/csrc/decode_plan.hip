@@ -10,13 +10,16 @@
 // which is a few hundred bytes), its page ids are copied and the new page, if
 // any, is appended; lane 0 writes the sequence's last-page length, the slot of the
 // new token and its position, and the id of the new page into the list of pages
-// to zero.
+// to zero. When the pool is given, further workgroups zero the opened pages in
+// every layer (the zero-on-alloc), 16 KiB each, so the step needs no separate
+// zeroing launch.
 #include "nslg_common.h"
 
 namespace nslg {
 namespace {
 
 constexpr int kMaxPlanBatch = 512;
+constexpr int kZeroBytes = 16 << 10;  // bytes zeroed per workgroup
 
 struct PlanStepArgs {
   const int32_t* indptr_in;
@@ -30,8 +33,42 @@ struct PlanStepArgs {
   int32_t* new_pages_out;
   int32_t batch;
   int32_t page_size;
+  // zero-on-alloc of the opened pages (k_pool == nullptr: none)
+  char* k_pool;
+  char* v_pool;
+  int64_t num_pages;
+  int64_t page_bytes;  // bytes of one page in one layer (a multiple of 16)
+  int32_t num_layers;
+  int32_t zero_parts;  // ceil(page_bytes / kZeroBytes)
   int32_t new_page[kMaxPlanBatch];  // page opened by sequence b this step, or -1
 };
+
+// Workgroup z of the zeroing part: opened page j, layer, K or V, 16 KiB part.
+__device__ void zero_part(const PlanStepArgs& a, int z) {
+  const int part = z % a.zero_parts;
+  z /= a.zero_parts;
+  const int kv = z & 1;
+  z >>= 1;
+  const int layer = z % a.num_layers;
+  const int j = z / a.num_layers;
+  int page = -1, seen = 0;
+  for (int b = 0; b < a.batch; ++b) {  // the j-th opened page, from the kernel arguments
+    if (a.new_page[b] >= 0) {
+      if (seen == j) {
+        page = a.new_page[b];
+        break;
+      }
+      ++seen;
+    }
+  }
+  if (page < 0 || (int64_t)page >= a.num_pages) return;
+  char* base = (kv ? a.v_pool : a.k_pool) + ((int64_t)layer * a.num_pages + page) * a.page_bytes;
+  const int64_t off0 = (int64_t)part * kZeroBytes;
+  const int64_t end = min(off0 + (int64_t)kZeroBytes, a.page_bytes);
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (int64_t off = off0 + 16 * (int64_t)threadIdx.x; off < end; off += 16 * (int64_t)blockDim.x)
+    *reinterpret_cast<u32x4*>(base + off) = zero;
+}
 
 // Pages of sequence s before the step, and whether this step opens one.
 __device__ inline void seq_step(const PlanStepArgs& a, int s, int& np_in, int& lpl_in, bool& opens) {
@@ -42,6 +79,10 @@ __device__ inline void seq_step(const PlanStepArgs& a, int s, int& np_in, int& l
 }
 
 __global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs a) {
+  if ((int)blockIdx.x >= a.batch) {
+    zero_part(a, blockIdx.x - a.batch);
+    return;
+  }
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -106,7 +147,10 @@ extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv
                                      const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
                                      const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
                                      int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
-                                     int32_t* positions_out, int32_t* new_pages_out, nslg_stream_t stream) {
+                                     int32_t* positions_out, int32_t* new_pages_out, void* k_pool,
+                                     void* v_pool, int32_t num_layers, int64_t num_pages,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                     nslg_stream_t stream) {
   if (batch < 0 || page_size <= 0) return fail(NSLG_EINVAL, "decode_plan_step: bad sizes");
   if (batch == 0) return NSLG_OK;
   if (batch > kMaxPlanBatch)
@@ -128,7 +172,33 @@ extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv
   a.new_pages_out = new_pages_out;
   a.batch = batch;
   a.page_size = page_size;
-  for (int b = 0; b < batch; ++b) a.new_page[b] = new_page[b];
-  decode_plan_step_kernel<<<batch, 256, 0, as_stream(stream)>>>(a);
+  int opened = 0;
+  for (int b = 0; b < batch; ++b) {
+    a.new_page[b] = new_page[b];
+    opened += new_page[b] >= 0 ? 1 : 0;
+  }
+  a.k_pool = (char*)k_pool;
+  a.v_pool = (char*)v_pool;
+  a.num_layers = 0;
+  a.num_pages = 0;
+  a.page_bytes = 0;
+  a.zero_parts = 1;
+  int64_t zero_groups = 0;
+  if (k_pool || v_pool) {
+    if (!k_pool || !v_pool || num_layers <= 0 || num_pages <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+      return fail(NSLG_EINVAL, "decode_plan_step: bad pool for zeroing");
+    const int eb = elem_bytes(dtype);
+    if (!eb) return fail(NSLG_EINVAL, "decode_plan_step: dtype %d", dtype);
+    const int64_t pb = (int64_t)page_size * num_kv_heads * head_dim * eb;
+    if (pb % 16 || ((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)
+      return fail(NSLG_EINVAL, "decode_plan_step: pool pages must be 16-byte aligned");
+    a.num_layers = num_layers;
+    a.num_pages = num_pages;
+    a.page_bytes = pb;
+    a.zero_parts = (int32_t)((pb + kZeroBytes - 1) / kZeroBytes);
+    zero_groups = (int64_t)opened * num_layers * 2 * a.zero_parts;
+    if (batch + zero_groups > 0x7fffffff) return fail(NSLG_EINVAL, "decode_plan_step: too much to zero");
+  }
+  decode_plan_step_kernel<<<(unsigned)(batch + zero_groups), 256, 0, as_stream(stream)>>>(a);
   return check_launch("decode_plan_step");
 }

@@ -205,12 +205,15 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
 
 
 def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
-                     new_page, page_size: int, num_new: int):
+                     new_page, page_size: int, num_new: int, k_pool: Optional[torch.Tensor] = None,
+                     v_pool: Optional[torch.Tensor] = None):
     """Next decode step's plan on the device (every sequence gains one token).
 
     new_page: host int32 array [B], the page sequence b opens this step or -1; num_new:
-    how many entries are >= 0. Returns device int32 tensors (indptr [B+1], indices,
-    last_page_len [B], slot_mapping [B], positions [B], new_pages [num_new])."""
+    how many entries are >= 0. With k_pool/v_pool ([L, P, ps, Hkv, D]) the opened pages
+    are zeroed in every layer in the same launch. Returns device int32 tensors (indptr
+    [B+1], indices, last_page_len [B], slot_mapping [B], positions [B], new_pages
+    [num_new])."""
     import numpy as np
     _require_gpu(kv_indptr, kv_indices, kv_last_page_len)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
@@ -225,10 +228,18 @@ def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_
     o = [0, B + 1, B + 1 + cap, 2 * B + 1 + cap, 3 * B + 1 + cap, 4 * B + 1 + cap]
     indptr, indices, lpl = buf[o[0]:o[1]], buf[o[1]:o[2]], buf[o[2]:o[3]]
     slot, pos, new = buf[o[3]:o[4]], buf[o[4]:o[5]], buf[o[5]:o[5] + num_new]
+    if k_pool is not None:
+        _require_gpu(k_pool, v_pool)
+        L, P, ps_, Hkv, D = _pool_geom(k_pool, v_pool)
+        if ps_ != page_size:
+            raise ValueError("decode_plan_step: pool page size differs")
+        pool_args = (k_pool.data_ptr(), v_pool.data_ptr(), L, P, Hkv, D, dtype_code(k_pool.dtype))
+    else:
+        pool_args = (None, None, 0, 0, 0, 0, 0)
     rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
                                           B, int(page_size), new_page.ctypes.data, indptr.data_ptr(),
                                           indices.data_ptr(), lpl.data_ptr(), slot.data_ptr(), pos.data_ptr(),
-                                          buf[o[5]:].data_ptr(), _stream(kv_indptr))
+                                          buf[o[5]:].data_ptr(), *pool_args, _stream(kv_indptr))
     _lib.check(rc, "nslg_decode_plan_step")
     return indptr, indices, lpl, slot, pos, new
 

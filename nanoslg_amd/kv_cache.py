@@ -890,16 +890,13 @@ class PagedKVCache(KVCacheManager):
         pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
         plan = prev[1]
         indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
-                                                                    new_page, ps, n_new)
+                                                                    new_page, ps, n_new, pool.k, pool.v)
         rows = self._decode_rows.get(B)
         if rows is None:
             qo, qr = _upload_i32([np.arange(B + 1, dtype=np.int32), np.arange(B, dtype=np.int32)], pool.device)
             rows = self._decode_rows[B] = (qo, qr)
-        out = _ForwardPlan.from_device(B, slot, pos, indptr, indices, lpl, rows[0], rows[1], new,
-                                       plan.total_pages + n_new)
-        if n_new:
-            kern.zero_pages(pool.k, pool.v, new)
-        return out
+        return _ForwardPlan.from_device(B, slot, pos, indptr, indices, lpl, rows[0], rows[1], new,
+                                        plan.total_pages + n_new)
 
     def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
         """kv_cache.py:707-722: radix match (full pages), pin, allocate the rest."""

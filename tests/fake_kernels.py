@@ -112,7 +112,8 @@ class DecodeLaunch:
         return paged_decode(q, k_layer, v_layer, indptr, indices, lpl, total, sm_scale=self.sm_scale)
 
 
-def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new):
+def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, k_pool=None,
+                     v_pool=None):
     """As nanoslg_amd.kernels.decode_plan_step, in plain Python on the CPU."""
     CALLS.append(("decode_plan_step", int(kv_indptr.numel() - 1)))
     ip, idx, lpl = kv_indptr.tolist(), kv_indices.tolist(), kv_last_page_len.tolist()
@@ -133,5 +134,9 @@ def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_siz
         out_lpl.append(last)
         slots.append(page * page_size + last - 1)
         pos.append((len(seg) - 1) * page_size + last - 1)
+    if k_pool is not None and new:
+        ids = torch.tensor(new, dtype=torch.long)
+        k_pool[:, ids] = 0
+        v_pool[:, ids] = 0
     t = lambda x: torch.tensor(x, dtype=torch.int32)  # noqa: E731
     return t(out_ip), t(out_idx), t(out_lpl), t(slots), t(pos), t(new)

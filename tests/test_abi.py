@@ -53,11 +53,15 @@ def test_host_side_argument_checks():
                                None, 0, None)
     assert rc == -1  # Hq not a multiple of Hkv
     # device decode planner: too large a batch, null pointers, aliased outputs
-    assert lib.nslg_decode_plan_step(1, 1, 1, 513, 16, 1, 2, 2, 2, 2, 2, 2, None) == -2
-    assert lib.nslg_decode_plan_step(None, 1, 1, 4, 16, 1, 2, 2, 2, 2, 2, 2, None) == -1
-    assert lib.nslg_decode_plan_step(1, 1, 1, 4, 16, 1, 2, 1, 2, 2, 2, 2, None) == -1
+    z = (None, None, 0, 0, 0, 0, 0)
+    assert lib.nslg_decode_plan_step(1, 1, 1, 513, 16, 1, 2, 2, 2, 2, 2, 2, *z, None) == -2
+    assert lib.nslg_decode_plan_step(None, 1, 1, 4, 16, 1, 2, 2, 2, 2, 2, 2, *z, None) == -1
+    assert lib.nslg_decode_plan_step(1, 1, 1, 4, 16, 1, 2, 1, 2, 2, 2, 2, *z, None) == -1
     assert lib.nslg_decode_plan_step(None, None, None, 0, 16, None, None, None, None, None, None, None,
-                                     None) == 0
+                                     *z, None) == 0
+    nopage = (ctypes.c_int32 * 4)(-1, -1, -1, -1)
+    assert lib.nslg_decode_plan_step(1, 1, 1, 4, 16, nopage, 2, 2, 2, 2, 2, 2, 256, None, 1, 10, 8, 128, 0,
+                                     None) == -1  # half a pool
 
 
 def test_decode_workspace_size_monotone():

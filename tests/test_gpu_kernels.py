@@ -459,3 +459,46 @@ def test_decode_plan_step_bit_exact(B, ps):
     assert np.array_equal(sl, np.array(e_slot, np.int32))
     assert np.array_equal(pos, np.array(lens, np.int32))
     assert np.array_equal(new, np.array(e_new, np.int32))
+
+
+@pytest.mark.parametrize("L,ps,Hkv,D,B", [(2, 16, 8, 128, 64), (3, 8, 2, 64, 37), (1, 32, 16, 128, 5)])
+def test_decode_plan_step_zeroes_opened_pages(L, ps, Hkv, D, B):
+    """Given the pools, the planner launch also zeroes every opened page in every
+    layer, K and V (the zero-on-alloc, kv_cache.py:411), 16 KiB per workgroup, and
+    touches no other page; the plan itself is the one built without the pools."""
+    _log(f"decode plan step zeroing L={L} ps={ps} Hkv={Hkv} D={D} B={B}")
+    from nanoslg_amd import kernels as K
+    rng = np.random.default_rng(91 + B)
+    lens = [int(x) for x in rng.integers(1, 200, size=B)]
+    for b in range(0, B, 3):
+        lens[b] = ps * (1 + b % 4)  # full last page: opens one
+    npg = [math.ceil(n / ps) for n in lens]
+    P = sum(npg) + B + 4
+    perm = rng.permutation(np.arange(1, P)).tolist()
+    tables, off = [], 0
+    for n in npg:
+        tables.append(perm[off:off + n])
+        off += n
+    spare = perm[off:]
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    opens = [n % ps == 0 for n in lens]
+    new_page = np.full(B, -1, np.int32)
+    for b in range(B):
+        if opens[b]:
+            new_page[b] = spare.pop()
+    g = torch.Generator().manual_seed(5)
+    k_pool = torch.randn(L, P, ps, Hkv, D, generator=g).half().to(DEV)
+    v_pool = torch.randn(L, P, ps, Hkv, D, generator=g).half().to(DEV)
+    k_exp, v_exp = k_pool.clone(), v_pool.clone()
+    opened = torch.tensor([int(p) for p in new_page if p >= 0], dtype=torch.long, device=DEV)
+    k_exp[:, opened] = 0
+    v_exp[:, opened] = 0
+    args = (torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV), torch.from_numpy(lpl).to(DEV),
+            new_page, ps, int(sum(opens)))
+    plain = K.decode_plan_step(*args)
+    fused = K.decode_plan_step(*args, k_pool, v_pool)
+    torch.cuda.synchronize()
+    for a, b in zip(plain, fused):
+        assert torch.equal(a, b)
+    assert torch.equal(k_pool, k_exp)
+    assert torch.equal(v_pool, v_exp)
