@@ -59,7 +59,7 @@ struct DecodeParams {
   int32_t chunk_budget;  // > 0: search the smallest length with <= this many chunks
   int32_t max_chunks;
   int32_t head_groups;   // workgroups per chunk (grid y)
-  int32_t* chunk_out;    // the length used, for the merge launch
+  int2* meta;            // per sequence: first chunk, chunk count (for the merge launch)
   uint16_t* out;
   int64_t out_stride;
   float* part_o;   // [max_chunks, Hq, D]
@@ -260,12 +260,12 @@ paged_decode_kernel(DecodeParams p) {
   const LaneLens lens(p.indptr, p.last_len, p.batch, p.page_size);
   int ct = p.chunk_tokens;
   if (p.chunk_budget > 0) ct = fit_chunk_tokens(lens, 64, ct, p.chunk_budget);
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *p.chunk_out = ct;
   int b = 0, cstart = 0, nchunks = 0;
   if (!locate_chunk(lens, ct, chunk, b, cstart, nchunks)) return;
   b = __builtin_amdgcn_readfirstlane(b);
   cstart = __builtin_amdgcn_readfirstlane(cstart);
   nchunks = __builtin_amdgcn_readfirstlane(nchunks);
+  if (chunk == cstart && blockIdx.y == 0 && threadIdx.x == 0) p.meta[b] = make_int2(cstart, nchunks);
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
   // chunk c of the sequence's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
   const int ntiles_seq = (len + 15) >> 4;
@@ -462,7 +462,7 @@ struct MergeParams {
   int32_t batch;
   int32_t page_size;
   int32_t num_qo_heads;
-  const int32_t* chunk_in;  // the chunk length the decode launch used
+  const int2* meta;  // per sequence: first chunk, chunk count, from the decode launch
   int32_t max_chunks;
   const float* part_o;
   const float* part_ml;
@@ -470,44 +470,53 @@ struct MergeParams {
   int64_t out_stride;
 };
 
-// Merge of the split-K partials: one wave per (sequence, query head), lane ->
-// D/64 consecutive d. Sequences with several chunks are merged; empty sequences
-// get zero rows; single-chunk sequences were finished by the decode kernel.
+// Merge of the split-K partials: one wave per (sequence, query head). Sequences
+// with several chunks are merged; empty sequences get zero rows; single-chunk
+// sequences were finished by the decode kernel. The wave reads its sequence's
+// chunk range (one round of loads), then the chunks' (m, l) with lanes over
+// chunks and the first rows of O with lanes over (chunk, d) in one more round:
+// O row c is D floats, D/4 lanes read it as float4s, 64/(D/4) rows per load.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
-  constexpr int PER = D / 64;
-  typedef typename RowVec<PER>::type OutVec;
+  constexpr int LPC = D / 4;     // lanes per O row
+  constexpr int CPI = 64 / LPC;  // O rows per load instruction
+  constexpr int kBatch = 8;      // load instructions per lane in flight
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int hq = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (hq >= p.num_qo_heads) return;
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
-  const int ct = max(16, *p.chunk_in);
-  int nchunks = (len + ct - 1) / ct;
-  uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + lane * PER;
-  if (nchunks == 0) {
+  const int2 mt = p.meta[b];
+  const int sub = lane / LPC;
+  const int d0 = 4 * (lane % LPC);
+  uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + d0;
+  if (len == 0) {
     // A sequence with no tokens attends to nothing: its output rows are zero.
-    OutVec z;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) z[j] = 0;
-    *reinterpret_cast<OutVec*>(orow) = z;
+    if (sub == 0) *reinterpret_cast<u16x4*>(orow) = u16x4{0, 0, 0, 0};
     return;
   }
-  if (nchunks == 1) return;
-  int before = 0;
-  for (int s = lane; s < b; s += 64) {
-    const int ls = seq_len_of(p.indptr, p.last_len, s, p.page_size);
-    before += (ls + ct - 1) / ct;
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off, 64);
-  const int cstart = before;
-  if (cstart >= p.max_chunks) return;
+  const int cstart = mt.x;
+  int nchunks = mt.y;
+  if (nchunks <= 1 || cstart < 0 || cstart >= p.max_chunks) return;
   if (cstart + nchunks > p.max_chunks) nchunks = p.max_chunks - cstart;
 
   const float* ml = p.part_ml + ((int64_t)cstart * p.num_qo_heads + hq) * 2;
   const int64_t ml_stride = (int64_t)p.num_qo_heads * 2;
-  // pass 1, lanes over chunks: the running max M and the denominator sum_c 2^(m_c - M) l_c
+  const float* po = p.part_o + ((int64_t)cstart * p.num_qo_heads + hq) * D + d0;
+  const int64_t po_stride = (int64_t)p.num_qo_heads * D;
+  f32x4 oc[kBatch];
+  float mc[kBatch];
+  auto load_rows = [&](int c0) {
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int c = min(c0 + CPI * k + sub, nchunks - 1);
+      oc[k] = *reinterpret_cast<const f32x4*>(po + c * po_stride);
+      mc[k] = ml[c * ml_stride];
+    }
+  };
+  load_rows(0);  // in flight with the (m, l) pass below
+
+  // the running max M and the denominator sum_c 2^(m_c - M) l_c, lanes over chunks
   float mmax = -INFINITY, lsum = 0.f;
   for (int c = lane; c < nchunks; c += 64) {
     const float2 v = *reinterpret_cast<const float2*>(ml + c * ml_stride);
@@ -525,34 +534,28 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
     mmax = m_new;
   }
 
-  // pass 2: sum_c 2^(m_c - M) O_c, eight chunks' loads in flight at a time
-  const float* po = p.part_o + ((int64_t)cstart * p.num_qo_heads + hq) * D + lane * PER;
-  const int64_t po_stride = (int64_t)p.num_qo_heads * D;
-  float acc[PER];
+  // sum_c 2^(m_c - M) O_c over the lane's rows, then over the CPI rows of a load
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nchunks; c0 += CPI * kBatch) {
+    if (c0 > 0) load_rows(c0);
 #pragma unroll
-  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
-  for (int c0 = 0; c0 < nchunks; c0 += 8) {
-    float mc[8];
-    float oc[8][PER];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int c = min(c0 + k, nchunks - 1);
-      mc[k] = ml[c * ml_stride];
-#pragma unroll
-      for (int j = 0; j < PER; ++j) oc[k][j] = po[c * po_stride + j];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float w = c0 + k < nchunks ? fast_exp2(mc[k] - mmax) : 0.f;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) acc[j] += w * oc[k][j];
+    for (int k = 0; k < kBatch; ++k) {
+      const float w = c0 + CPI * k + sub < nchunks ? fast_exp2(mc[k] - mmax) : 0.f;
+      acc += w * oc[k];
     }
   }
-  const float inv = 1.f / lsum;
-  OutVec w16;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) w16[j] = T::from_f32(acc[j] * inv);
-  *reinterpret_cast<OutVec*>(orow) = w16;
+  for (int off = LPC; off < 64; off <<= 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], off, 64);
+  }
+  if (sub == 0) {
+    const float inv = 1.f / lsum;
+    u16x4 w16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(acc[j] * inv);
+    *reinterpret_cast<u16x4*>(orow) = w16;
+  }
 }
 
 // Resident workgroup slots of the decode kernel on the current device (CUs x
@@ -663,9 +666,10 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
   const DecodeShape sh = dtype == NSLG_BF16
                              ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
                              : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
-  // partials [max_chunks, Hq, D] and [max_chunks, Hq, 2] fp32, then 256 bytes holding
-  // the chunk length the decode launch chose
-  return (size_t)(sh.max_chunks * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) + 256;
+  // partials [max_chunks, Hq, D] and [max_chunks, Hq, 2] fp32, then each sequence's
+  // chunk range (int32 pairs), rounded up to 256 bytes
+  return (size_t)(sh.max_chunks * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) +
+         (((size_t)batch * 8 + 255) & ~(size_t)255);
 }
 
 extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_pool,
@@ -732,7 +736,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   float* ws = (float*)workspace;
   p.part_o = ws;
   p.part_ml = ws + mc * num_qo_heads * head_dim;
-  p.chunk_out = reinterpret_cast<int32_t*>(ws + mc * num_qo_heads * (head_dim + 2));
+  p.meta = reinterpret_cast<int2*>(ws + mc * num_qo_heads * (head_dim + 2));
 
   MergeParams mp;
   mp.indptr = kv_indptr;
@@ -740,7 +744,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   mp.batch = batch;
   mp.page_size = page_size;
   mp.num_qo_heads = num_qo_heads;
-  mp.chunk_in = p.chunk_out;
+  mp.meta = p.meta;
   mp.max_chunks = (int32_t)mc;
   mp.part_o = p.part_o;
   mp.part_ml = p.part_ml;
