@@ -207,6 +207,36 @@ int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
                           int32_t num_layers, int64_t num_pages, int32_t num_kv_heads,
                           int32_t head_dim, int32_t dtype, nslg_stream_t stream);
 
+/*
+ * Fused rotary position embedding + K/V append. Replaces, per layer, the position
+ * gather and the two apply_rotary_emb calls of _attention_forward
+ * (nanoslg/models.py:96-103, apply_rotary_emb :69-83) together with the cache write
+ * of attend (kv_cache.py:661-674 paged, :301-310 contiguous); the positions are the
+ * forward's (get_position_ids, kv_cache.py:567-573, 635-637).
+ *
+ *   q               [num_rows] rows of Hq*D elements at stride q_stride
+ *   q_out           rotated q, rows at stride q_out_stride; may be q itself (in
+ *                   place), must not overlap it otherwise
+ *   k_new, v_new    [num_rows] rows of Hkv*D elements at k_stride / v_stride
+ *   positions       int32[num_rows] (device): the row's position; clamped into the
+ *                   table (callers check the range, as indexing the table would)
+ *   slot_mapping    int32[num_rows] (device): page*page_size+slot of the row's K/V;
+ *                   negative (padding) or >= pool_slots: the row's K/V are not written
+ *   cos_table, sin_table   fp32 [table_rows] rows of >= D floats at table_stride
+ *                   (the model's precomputed tables, models.py:37-66)
+ *   k_pool, v_pool  one layer, pool_slots rows of Hkv*D elements
+ * q_out and the pool's K rows = rnd(rnd(x*c) + rnd(rot(x)*s)) in the 16-bit type
+ * with c, s the table values rounded to it, rot(x) = cat(-x[D/2:], x[:D/2]):
+ * bit-exact with the eager expression. V rows are copied. f16/bf16, D in {64,128,256}.
+ */
+int nslg_rope_append(const void* q, int64_t q_stride, void* q_out, int64_t q_out_stride,
+                     const void* k_new, int64_t k_stride, const void* v_new, int64_t v_stride,
+                     const int32_t* positions, const int32_t* slot_mapping, int64_t num_rows,
+                     const float* cos_table, const float* sin_table, int64_t table_stride,
+                     int64_t table_rows, int32_t num_qo_heads, int32_t num_kv_heads,
+                     int32_t head_dim, void* k_pool, void* v_pool, int64_t pool_slots,
+                     int32_t dtype, nslg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,5 +16,6 @@ from .kv_cache import (  # noqa: F401
     PagedKVCache,
     PagePool,
     RadixTree,
+    attention_forward,
     create_cache_manager,
 )

@@ -41,6 +41,9 @@ SIGNATURES = {
     "nslg_decode_plan_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p]),
+    "nslg_rope_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                   c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+                                   c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "nslg_paged_prefill_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int64, c_int32]),
     "nslg_paged_prefill": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_int32,
                                      c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,

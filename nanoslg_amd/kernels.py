@@ -88,6 +88,62 @@ def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: torch.Tens
     _lib.check(rc, "nslg_append_kv")
 
 
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, D: int):
+    """fp32 [R, >=D] tables with unit inner stride and a common row stride (a
+    16-bit table is widened exactly; the kernel rounds it back)."""
+    if cos.dtype != torch.float32:
+        cos = cos.float()
+    if sin.dtype != torch.float32:
+        sin = sin.float()
+    if cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] < D:
+        raise ValueError(f"rope tables must be [rows, >= {D}] and of one shape")
+    if cos.stride(1) != 1 or cos.stride(0) != sin.stride(0) or sin.stride(1) != 1:
+        cos, sin = cos.contiguous(), sin.contiguous()
+    return cos, sin
+
+
+def rope_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, positions: torch.Tensor,
+                slot_mapping: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_pool: torch.Tensor,
+                v_pool: torch.Tensor, q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotary position embedding of q and k_new at `positions`, and the append of the
+    rotated k and of v_new into one pool layer at `slot_mapping`, in one launch.
+
+    q [..., Hq, D] rows; k_new/v_new [..., Hkv, D] with as many rows; positions and
+    slot_mapping int32, one per row (slot < 0: padding, not written); cos/sin the
+    model's [max_positions, D] tables. Returns q rotated, shaped like q (q_out, or a
+    new tensor; q_out may be q). A position outside the tables raises IndexError."""
+    _require_gpu(q, k_new, v_new, positions, slot_mapping, cos, sin, k_pool, v_pool)
+    _i32(positions, "positions")
+    _i32(slot_mapping, "slot_mapping")
+    if not (q.dtype == k_new.dtype == v_new.dtype == k_pool.dtype == v_pool.dtype):
+        raise TypeError("rope_append: q, k/v and the pool must share one dtype")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()) or k_pool.shape != v_pool.shape:
+        raise ValueError("rope_append: pool layers must be contiguous and of one shape")
+    Hkv, D = k_pool.shape[-2], k_pool.shape[-1]
+    nq, qs, Hq = _rows(q, "q")
+    nk, ks, hk = _rows(k_new, "k_new")
+    nv, vs, hv = _rows(v_new, "v_new")
+    if q.shape[-1] != D or tuple(k_new.shape[-2:]) != (Hkv, D) or tuple(v_new.shape[-2:]) != (Hkv, D):
+        raise ValueError("rope_append: trailing dims must be [Hq, D] / [Hkv, D] of the pool")
+    T = positions.numel()
+    if nq != T or nk != T or nv != T or slot_mapping.numel() != T:
+        raise ValueError(f"rope_append: {T} positions for {nq} q / {nk} k / {nv} v rows, "
+                         f"{slot_mapping.numel()} slots")
+    cos, sin = _rope_tables(cos, sin, D)
+    if q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if q_out.shape != q.shape or q_out.dtype != q.dtype:
+        raise ValueError("rope_append: q_out must be shaped like q")
+    no, qos, _ = _rows(q_out, "q_out")
+    rc = _lib.load().nslg_rope_append(q.data_ptr(), qs, q_out.data_ptr(), qos, k_new.data_ptr(), ks,
+                                      v_new.data_ptr(), vs, positions.data_ptr(), slot_mapping.data_ptr(), T,
+                                      cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], Hq, Hkv, D,
+                                      k_pool.data_ptr(), v_pool.data_ptr(), k_pool.numel() // (Hkv * D),
+                                      dtype_code(q.dtype), _stream(q))
+    _lib.check(rc, "nslg_rope_append")
+    return q_out
+
+
 def _pool_geom(k_pool: torch.Tensor, v_pool: torch.Tensor):
     if k_pool.shape != v_pool.shape or k_pool.dtype != v_pool.dtype:
         raise ValueError("k/v pools must have the same shape and dtype")
@@ -282,9 +338,12 @@ class DecodeLaunch:
         self.ws = (workspace or Workspace(self.device)).get(need)
         self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
 
-    def __call__(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
+    def __call__(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                 rope: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
         """q [B, Hq, D] (rows may be strided), k_new/v_new [B, ..., Hkv, D] rows of one
-        token each; returns [B, Hq, D] for pool layer `layer`."""
+        token each; returns [B, Hq, D] for pool layer `layer`. With rope = (cos, sin,
+        positions int32 [B]) q and k_new are first rotated (nslg_rope_append replaces
+        nslg_append_kv)."""
         if not 0 <= layer < self.L:
             raise IndexError(f"layer {layer} out of range [0, {self.L})")
         for t in (q, k_new, v_new):
@@ -301,11 +360,27 @@ class DecodeLaunch:
         off = layer * self.layer_bytes
         kp, vp = self.kp0 + off, self.vp0 + off
         lib = self.lib
-        rc = lib.nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, self.slots, B, kp, vp,
-                                self.P * self.ps, self.Hkv, D, self.code, stream)
-        _lib.check(rc, "nslg_append_kv")
+        if rope is None:
+            rc = lib.nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, self.slots, B, kp, vp,
+                                    self.P * self.ps, self.Hkv, D, self.code, stream)
+            _lib.check(rc, "nslg_append_kv")
+            q_ptr, q_stride = q.data_ptr(), q.stride(0)
+        else:
+            cos, sin, pos = rope
+            if pos.device != self.device or pos.dtype != torch.int32 or pos.numel() != B or not pos.is_contiguous():
+                raise ValueError(f"DecodeLaunch: positions must be {B} contiguous int32 on {self.device}")
+            cos, sin = _rope_tables(cos, sin, D)
+            if cos.device != self.device:
+                raise ValueError(f"DecodeLaunch: rope tables must be on {self.device}")
+            q_rot = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
+            rc = lib.nslg_rope_append(q.data_ptr(), q.stride(0), q_rot.data_ptr(), Hq * D, k_new.data_ptr(), ks,
+                                      v_new.data_ptr(), vs, pos.data_ptr(), self.slots, B, cos.data_ptr(),
+                                      sin.data_ptr(), cos.stride(0), cos.shape[0], Hq, self.Hkv, D, kp, vp,
+                                      self.P * self.ps, self.code, stream)
+            _lib.check(rc, "nslg_rope_append")
+            q_ptr, q_stride = q_rot.data_ptr(), Hq * D
         out = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
-        rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), kp, vp, self.P, self.ps, self.indptr, self.indices,
+        rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
                                    self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
                                    out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
         _lib.check(rc, "nslg_paged_decode")

@@ -350,6 +350,22 @@ class _ForwardPlan:
             self._slot_by_S[S] = s
         return s
 
+    def pos_for(self, S: int) -> torch.Tensor:
+        """int32 positions of the [B, S] input grid, flattened (zeros on padding)."""
+        if S == self.iw:
+            return self.pos_i32
+        p = self._pos_by_S.get(S) if hasattr(self, "_pos_by_S") else None
+        if p is None:
+            grid = self.pos_i32.view(self.batch, self.iw)
+            if S < self.iw:
+                p = grid[:, :S].contiguous().view(-1)
+            else:
+                p = torch.cat([grid, grid.new_zeros(self.batch, S - self.iw)], 1).view(-1)
+            if not hasattr(self, "_pos_by_S"):
+                self._pos_by_S = {}
+            self._pos_by_S[S] = p
+        return p
+
     def positions_long(self) -> torch.Tensor:
         if self._pos_long is None:
             self._pos_long = self.pos_i32.view(self.batch, self.iw).long()
@@ -822,6 +838,37 @@ class PagedCacheContext(CacheContext):
             return launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
+        return self._prefill(q, k_layer, v_layer)
+
+    def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
+        """The position part of the model's attention forward fused with attend
+        (models.py:96-105): q and k_new are rotated at this forward's positions
+        (get_position_ids) with the model's cos/sin tables, the rotated k and v are
+        written into the pages of `layer_idx` in the same launch, then attention runs
+        as in attend(). Same result as attend() on q and k_new rotated by the eager
+        apply_rotary_emb, bit for bit."""
+        cache, pool, plan = self.cache, self.cache.pool, self._plan
+        kern = cache.kernels
+        B, S = q.shape[0], q.shape[1]
+        if self.max_kv_len > cos.shape[0]:
+            raise IndexError(f"position {self.max_kv_len - 1} is outside the rope tables ({cos.shape[0]} rows)")
+        pos = plan.pos_for(S)
+        if self._is_decode and S == 1:
+            launch = self._decode_launch
+            if launch is None:
+                launch = self._decode_launch = kern.DecodeLaunch(
+                    pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
+                    q.shape[2], workspace=cache.workspace)
+            return launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, pos)).reshape(B, 1, -1)
+        k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+        q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
+        return self._prefill(q_rot, k_layer, v_layer)
+
+    def _prefill(self, q, k_layer, v_layer):
+        """Causal attention of the forward's rows (K/V already written)."""
+        cache, plan = self.cache, self._plan
+        kern = cache.kernels
+        B, S = q.shape[0], q.shape[1]
         Hq, D = q.shape[2], q.shape[3]
         if self._uniform_rows and S == self._iw:
             q_rag = q.reshape(B * S, Hq, D)
@@ -1049,10 +1096,30 @@ class ContiguousCacheContext(CacheContext):
 
     def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
         cache, plan = self.cache, self._plan
+        k_layer, v_layer = cache.paged_view(layer_idx)
+        cache.kernels.append_kv(k_new, v_new, plan.slots_for(q.shape[1]), k_layer, v_layer)
+        return self._attend_written(q, k_layer, v_layer)
+
+    def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
+        """attend() with the position part of the model's attention forward fused into
+        the cache write (models.py:96-105): q and k_new rotated at this forward's
+        positions with the model's cos/sin tables, the rotated k and v written into
+        the sequence slots of `layer_idx` in one launch. Same result as attend() on
+        the eagerly rotated q and k_new, bit for bit."""
+        cache, plan = self.cache, self._plan
+        if self.max_kv_len > cos.shape[0]:
+            raise IndexError(f"position {self.max_kv_len - 1} is outside the rope tables ({cos.shape[0]} rows)")
+        S = q.shape[1]
+        k_layer, v_layer = cache.paged_view(layer_idx)
+        q_rot = cache.kernels.rope_append(q, k_new, v_new, plan.pos_for(S), plan.slots_for(S), cos, sin,
+                                          k_layer, v_layer)
+        return self._attend_written(q_rot, k_layer, v_layer)
+
+    def _attend_written(self, q, k_layer, v_layer):
+        """Attention of the forward's rows over the slots (K/V already written)."""
+        cache, plan = self.cache, self._plan
         kern = cache.kernels
         B, S = q.shape[0], q.shape[1]
-        k_layer, v_layer = cache.paged_view(layer_idx)
-        kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         if self._is_decode and S == 1:
             out = kern.paged_decode(q[:, 0], k_layer, v_layer, plan.indptr, plan.indices, plan.lpl,
                                     plan.total_pages, workspace=cache.workspace)
@@ -1163,3 +1230,12 @@ def create_cache_manager(hf_config, parallel_config, device, dtype, model_config
 # the reference's class names, for callers that import them directly
 FlashInferPagedKVCache = PagedKVCache
 FlashInferCacheContext = PagedCacheContext
+
+
+def attention_forward(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, layer_idx: int, n_heads: int,
+                      n_kv_heads: int, cos: torch.Tensor, sin: torch.Tensor, cache_ctx: CacheContext) -> torch.Tensor:
+    """Drop-in for the model's _attention_forward (models.py:86-105), same arguments
+    and result: positions from the context, rotary embedding of q and k_new with the
+    model's cos/sin tables, the cache write and attention, with the rotation and the
+    write in one kernel launch (the context's attend_rope)."""
+    return cache_ctx.attend_rope(layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads)

@@ -19,6 +19,24 @@ tests live in tests/test_oracle.py):
                                                 against is_causal SDPA
   position_ids           kv_cache.py:267-278, 292-295, 567-573, 635-637
                                                 pinned by closed form
+  rope_inv_freq / rope_tables
+                         models.py:37-66        pinned against transformers'
+                                                own llama3 inverse frequencies
+                                                (a library routine), closed
+                                                forms (theta^(-2i/dim), the
+                                                three wavelength bands, t = 0
+                                                row = (1, 0), angle t * f)
+  apply_rotary_ref / rope_forward_ref
+                         models.py:69-83, 96-103
+                                                pinned by the float64 rotation
+                                                (rotate_f64) within 16-bit
+                                                rounding, position 0 = identity,
+                                                rotation by a quarter turn, and
+                                                planted sign / half mistakes
+                                                that the checks must catch
+  rotate_f64             (the rotation of each (d, d + D/2) pair in float64)
+                                                pinned by norm preservation and
+                                                composition R(a) R(b) = R(a + b)
   ContiguousRef          kv_cache.py:227-379    the CPU baseline (config 1);
                                                 pinned against PagedRef on the
                                                 same inputs and against
@@ -133,6 +151,83 @@ def position_ids(start_positions, new_token_counts, input_offsets, S: Optional[i
     if S < iw:
         return pos[:, :S]
     return torch.cat([pos, pos.new_zeros(B, S - iw)], 1)
+
+
+# --------------------------------------------------------------------------------------
+# rotary position embedding (nanoslg/models.py:37-105)
+# --------------------------------------------------------------------------------------
+
+
+def rope_inv_freq(dim: int, theta: float, rope_scaling: Optional[dict] = None) -> torch.Tensor:
+    """float32 inverse frequencies [dim/2] of the tables (models.py:40-59).
+
+    f_i = 1 / theta^(2i/dim) in float32. With a "llama3" rope_scaling, each f is
+    kept when its wavelength 2*pi/f is below original_max_position_embeddings /
+    high_freq_factor, divided by `factor` when it is above original /
+    low_freq_factor, and blended linearly in between (s = (original / wavelength
+    - low) / (high - low); (1 - s) f / factor + s f), each step a float32 scalar op
+    as the reference's per-element loop does."""
+    freqs = 1.0 / (theta ** (torch.arange(0, dim, 2)[: dim // 2].float() / dim))
+    if rope_scaling and rope_scaling.get("rope_type") == "llama3":
+        factor = rope_scaling.get("factor", 8.0)
+        lo = rope_scaling.get("low_freq_factor", 1.0)
+        hi = rope_scaling.get("high_freq_factor", 4.0)
+        old_ctx = rope_scaling.get("original_max_position_embeddings", 8192)
+        lo_wl, hi_wl = old_ctx / lo, old_ctx / hi
+        scaled = []
+        for i in range(freqs.numel()):
+            f = freqs[i]  # a 0-d float32 tensor: every op below is a float32 op
+            wl = 2 * math.pi / f
+            if wl < hi_wl:
+                scaled.append(f)
+            elif wl > lo_wl:
+                scaled.append(f / factor)
+            else:
+                s = (old_ctx / wl - lo) / (hi - lo)
+                scaled.append((1 - s) * f / factor + s * f)
+        freqs = torch.stack(scaled).to(torch.float32)
+    return freqs
+
+
+def rope_tables(dim: int, max_seq_len: int, theta: float, rope_scaling: Optional[dict] = None):
+    """fp32 (cos, sin), each [max_seq_len, dim] (models.py:37-66): angles t * f for
+    t < max_seq_len (float32 outer product with rope_inv_freq), the dim/2 angles
+    repeated to dim, then cos and sin."""
+    freqs = rope_inv_freq(dim, theta, rope_scaling)
+    t = torch.arange(max_seq_len, dtype=torch.float32)
+    ang = torch.outer(t, freqs)
+    ang = torch.cat((ang, ang), dim=-1)
+    return ang.cos(), ang.sin()
+
+
+def apply_rotary_ref(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, S, H, D] rotated with per-row cos/sin [B, S, D] (models.py:69-83): the
+    tables are cast to x's dtype and the expression x*c + cat(-x2, x1)*s is
+    evaluated as eager tensor ops in that dtype (each product and the sum rounded
+    to it)."""
+    c = cos[:, :, None, :].to(dtype=x.dtype)
+    s = sin[:, :, None, :].to(dtype=x.dtype)
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    return x * c + torch.cat((-x2, x1), dim=-1) * s
+
+
+def rope_forward_ref(q: torch.Tensor, k_new: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     pos_ids: torch.Tensor):
+    """The position part of _attention_forward (models.py:96-103): gather the table
+    rows at pos_ids [B, S], rotate q and k_new. Returns (q_rot, k_rot)."""
+    c, s = cos[pos_ids], sin[pos_ids]
+    return apply_rotary_ref(q, c, s), apply_rotary_ref(k_new, c, s)
+
+
+def rotate_f64(x: np.ndarray, pos: np.ndarray, inv_freq: np.ndarray) -> np.ndarray:
+    """Closed form of the rotation in float64: element pairs (d, d + D/2) of each row
+    turned by the angle pos * inv_freq[d] (x [N, H, D], pos [N])."""
+    half = x.shape[-1] // 2
+    ang = pos.astype(np.float64)[:, None] * inv_freq.astype(np.float64)[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x1, x2 = x[..., :half].astype(np.float64), x[..., half:].astype(np.float64)
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
 
 
 # --------------------------------------------------------------------------------------

@@ -105,11 +105,32 @@ class DecodeLaunch:
         self.args = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages)
         self.sm_scale = sm_scale
 
-    def __call__(self, layer, q, k_new, v_new):
+    def __call__(self, layer, q, k_new, v_new, rope=None):
         slots, indptr, indices, lpl, total = self.args
         k_layer, v_layer = self.k_pool[layer], self.v_pool[layer]
-        append_kv(k_new, v_new, slots, k_layer, v_layer)
+        if rope is None:
+            append_kv(k_new, v_new, slots, k_layer, v_layer)
+        else:
+            cos, sin, pos = rope
+            q = rope_append(q, k_new, v_new, pos, slots, cos, sin, k_layer, v_layer)
         return paged_decode(q, k_layer, v_layer, indptr, indices, lpl, total, sm_scale=self.sm_scale)
+
+
+def rope_append(q, k_new, v_new, positions, slot_mapping, cos, sin, k_pool, v_pool, q_out=None):
+    """As nanoslg_amd.kernels.rope_append: the oracle's eager rotation, then append."""
+    CALLS.append(("rope_append", int(positions.numel())))
+    Hq, D = q.shape[-2], q.shape[-1]
+    Hkv = k_pool.shape[-2]
+    T = positions.numel()
+    pos = positions.reshape(1, T).long()
+    qr, kr = kv_oracle.rope_forward_ref(q.reshape(1, T, Hq, D), k_new.reshape(1, T, Hkv, D), cos.float(),
+                                        sin.float(), pos)
+    append_kv(kr.reshape(T, Hkv, D), v_new.reshape(T, Hkv, D), slot_mapping, k_pool, v_pool)
+    out = qr.reshape(q.shape)
+    if q_out is not None:
+        q_out.copy_(out)
+        return q_out
+    return out
 
 
 def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, k_pool=None,

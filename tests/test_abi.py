@@ -20,7 +20,8 @@ def test_header_declares_the_hot_path():
     syms = declared_symbols()
     for name in ["nslg_append_kv", "nslg_zero_pages", "nslg_copy_pages", "nslg_gather_kv",
                  "nslg_paged_decode", "nslg_paged_decode_workspace_size", "nslg_paged_prefill",
-                 "nslg_paged_prefill_workspace_size", "nslg_decode_plan_step", "nslg_version",
+                 "nslg_paged_prefill_workspace_size", "nslg_decode_plan_step", "nslg_rope_append",
+                 "nslg_version",
                  "nslg_last_error"]:
         assert name in syms
 
@@ -62,6 +63,29 @@ def test_host_side_argument_checks():
     nopage = (ctypes.c_int32 * 4)(-1, -1, -1, -1)
     assert lib.nslg_decode_plan_step(1, 1, 1, 4, 16, nopage, 2, 2, 2, 2, 2, 2, 256, None, 1, 10, 8, 128, 0,
                                      None) == -1  # half a pool
+
+
+def test_rope_append_argument_checks():
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    # fused RoPE + append: unsupported head_dim, null pointers, misaligned stride, overlapping q_out
+    A = 4096  # a 16-byte aligned stand-in address (never dereferenced: rejected first)
+    ok = dict(q=A, qs=4096, qo=A, qos=4096, k=A, ks=1024, v=A, vs=1024, pos=A, slot=A, n=4, cos=A, sin=A,
+              ts=128, tr=100, hq=32, hkv=8, d=128, kp=A, vp=A, slots=64, dt=0)
+
+    def rope(**kw):
+        a = dict(ok, **kw)
+        return lib.nslg_rope_append(a["q"], a["qs"], a["qo"], a["qos"], a["k"], a["ks"], a["v"], a["vs"], a["pos"],
+                                    a["slot"], a["n"], a["cos"], a["sin"], a["ts"], a["tr"], a["hq"], a["hkv"],
+                                    a["d"], a["kp"], a["vp"], a["slots"], a["dt"], None)
+    assert rope(d=96, ts=96) == -2
+    assert rope(dt=2) == -2
+    assert rope(pos=None) == -1
+    assert rope(qs=4092) == -1  # row stride smaller than Hq*D
+    assert rope(ks=1028) == -1  # not a multiple of 8 elements
+    assert rope(qo=A + 64) == -1  # q_out overlaps q
+    assert rope(ts=64) == -1  # table rows shorter than D
+    assert rope(n=0) == 0
 
 
 def test_decode_workspace_size_monotone():

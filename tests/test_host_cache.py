@@ -400,3 +400,49 @@ def test_device_decode_plan_matches_host_plan():
         m.pool.add_ref(int(m.seqs["c"].bt[m.seqs["c"].n_pages - 1]))
     step([1, 1, 1], ["a", "c", "d"], expect_fast=False)
     step([1, 1, 1], ["a", "c", "d"], expect_fast=True)
+
+
+@pytest.mark.parametrize("backend", ["paged", "contiguous"])
+def test_attend_rope_equals_attend_on_rotated_inputs(backend):
+    """attend_rope (rotation fused into the cache write) gives the same outputs and
+    cache contents as the model's own sequence: positions from get_position_ids,
+    eager rotation of q and k_new (models.py:96-103), then attend. Ragged prefill with
+    input offsets, then decode steps (the device-planned ones included)."""
+    g = torch.Generator().manual_seed(21)
+    cos, sin = O.rope_tables(D, 512, 10000.0)
+    cfg = dict(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=4, max_pages=64,
+               dtype=torch.float16, device=None, backend=backend, max_batch_size=4, max_seq_len=128)
+    if backend == "paged":
+        a, b = (KC.PagedKVCache(KC.KVCacheConfig(**cfg), kernels=FK) for _ in range(2))
+    else:
+        a, b = (KC.ContiguousKVCache(KC.KVCacheConfig(**cfg), kernels=FK) for _ in range(2))
+    ids = ["x", "y", "z"]
+    for m in (a, b):
+        for s, n in zip(ids, [6, 9, 3]):
+            m.allocate_sequence(s, num_tokens=n)
+    steps = [([6, 9, 3], [2, 0, 1])] + [([1, 1, 1], None)] * 6
+    for ntok, offs in steps:
+        offs = offs or [0] * len(ids)
+        S = max(o + n for o, n in zip(offs, ntok))
+        q = torch.randn(3, S, HQ, D, generator=g).half()
+        k = torch.randn(3, S, HKV, D, generator=g).half()
+        v = torch.randn(3, S, HKV, D, generator=g).half()
+        ca, cb = a.begin_forward(ids, ntok, offs), b.begin_forward(ids, ntok, offs)
+        for layer in range(L):
+            oa = KC.attention_forward(q, k, v, layer, HQ, HKV, cos, sin, ca)
+            pos = cb.get_position_ids(S)
+            qr, kr = O.rope_forward_ref(q, k, cos, sin, pos)
+            ob = cb.attend(layer, qr, kr, v, HQ, HKV)
+            for bi in range(3):
+                rows = slice(offs[bi], offs[bi] + ntok[bi])
+                assert torch.equal(oa[bi, rows], ob[bi, rows])
+        a.end_forward(ca)
+        b.end_forward(cb)
+        if backend == "paged":
+            assert torch.equal(a.pool.k, b.pool.k) and torch.equal(a.pool.v, b.pool.v)
+        else:
+            assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    with pytest.raises(IndexError):
+        short = O.rope_tables(D, 8, 10000.0)
+        c = a.begin_forward(ids, [1, 1, 1])
+        KC.attention_forward(q[:, :1], k[:, :1], v[:, :1], 0, HQ, HKV, short[0], short[1], c)
