@@ -16,7 +16,7 @@ step, so the pass that gives `value` runs without them).
 `cpu_baseline` = the CPU restatement of the reference's contiguous SDPA path on a
 bounded sample of the same workload, on this host's cores.
 
-  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch|radix|prefill]
+  python bench.py [--steps 256] [--warmup 16] [--workload kv_pressure|small_batch|radix|prefill|rope]
   python bench.py --workload copy_calibration   (a plain 1 GiB copy, for counter scaling)
 """
 from __future__ import annotations
@@ -46,7 +46,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--workload", default="kv_pressure",
-                    choices=["kv_pressure", "small_batch", "radix", "prefill", "copy_calibration"])
+                    choices=["kv_pressure", "small_batch", "radix", "prefill", "rope", "copy_calibration"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
@@ -684,6 +684,127 @@ def run_prefill(args):
     return res
 
 
+def _eager_rope(x, cos, sin, pos_ids):
+    """The model's rotation as eager tensor ops (nanoslg/models.py:69-83, 96-103), for
+    timing beside the fused kernel."""
+    import torch
+    c = cos[pos_ids][:, :, None, :].to(dtype=x.dtype)
+    s = sin[pos_ids][:, :, None, :].to(dtype=x.dtype)
+    half = x.shape[-1] // 2
+    return x * c + torch.cat((-x[..., half:], x[..., :half]), dim=-1) * s
+
+
+def run_rope(args):
+    """Fused rotary embedding + K/V append (nslg_rope_append) against the model's
+    sequence it replaces (gather cos/sin at the positions, eager rotation of q and
+    k_new, then the append kernel), per layer, at two shapes: a decode step of 64
+    sequences (positions log-uniform in [2048, 32768]) and a prefill chunk of 8 x 512
+    tokens. Both write the same pool bytes and q (checked here). One step = one call
+    of each at each shape; time per call from a loop of `--steps` calls."""
+    import torch
+    from nanoslg_amd import kernels
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    R = 32768
+    # Llama-3.1 tables (theta 500000, llama3 scaling), float32 [R, D] on the device
+    f = 1.0 / (500000.0 ** (torch.arange(0, D, 2)[: D // 2].float() / D))
+    wl = 2 * math.pi / f
+    s_ = (8192 / wl - 1.0) / 3.0
+    f = torch.where(wl < 2048, f, torch.where(wl > 8192, f / 8, (1 - s_) * f / 8 + s_ * f))
+    ang = torch.outer(torch.arange(R, dtype=torch.float32), f)
+    ang = torch.cat((ang, ang), -1)
+    cos, sin = ang.cos().to(dev), ang.sin().to(dev)
+    P = 8192
+    k_pool = torch.zeros(P, PS, HKV, D, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros_like(k_pool)
+    rng = np.random.default_rng(args.seed)
+    out = {}
+    for name, B, S in (("decode_b64", 64, 1), ("prefill_8x512", 8, 512)):
+        T = B * S
+        if S == 1:
+            pos = np.exp(rng.uniform(math.log(2048), math.log(32768), size=B)).astype(np.int64).reshape(B, 1)
+        else:
+            pos = (np.arange(S)[None, :] + rng.integers(0, R - S, size=(B, 1))).astype(np.int64)
+        pos_ids = torch.from_numpy(pos).to(dev)
+        pos32 = pos_ids.reshape(-1).to(torch.int32)
+        slots = torch.from_numpy(rng.permutation(P * PS)[:T].astype(np.int32)).to(dev)
+        q = torch.randn(B, S, HQ, D, generator=g, device=dev, dtype=torch.float16)
+        k = torch.randn(B, S, HKV, D, generator=g, device=dev, dtype=torch.float16)
+        v = torch.randn(B, S, HKV, D, generator=g, device=dev, dtype=torch.float16)
+
+        def eager():
+            qr = _eager_rope(q, cos, sin, pos_ids)
+            kr = _eager_rope(k, cos, sin, pos_ids)
+            kernels.append_kv(kr, v, slots, k_pool, v_pool)
+            return qr
+
+        q_out = torch.empty_like(q)
+
+        def fused():
+            return kernels.rope_append(q, k, v, pos32, slots, cos, sin, k_pool, v_pool, q_out=q_out)
+
+        qa = eager().clone()
+        ka = k_pool.clone()
+        qb = fused()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(qa, qb) and torch.equal(ka, k_pool))
+        res = {"tokens": T, "bit_exact_with_eager": same}
+        for label, fn in (("eager", eager), ("fused", fused)):
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                fn()
+            torch.cuda.synchronize()
+            res[f"{label}_us"] = round((time.perf_counter() - t0) / args.steps * 1e6, 2)
+        # kernel-only time of the fused launch, from events on its stream
+        st = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(args.steps):
+            fused()
+        e1.record(st)
+        torch.cuda.synchronize()
+        res["fused_kernel_us"] = round(e0.elapsed_time(e1) / args.steps * 1e3, 2)
+        nbytes = T * (HQ * D * 2 * 2 + HKV * D * 2 * 4 + D * 4 * 2 + 8)
+        res["algorithmic_bytes"] = nbytes
+        res["fused_GB_s"] = round(nbytes / (res["fused_kernel_us"] * 1e-6) / 1e9, 1)
+        res["speedup"] = round(res["eager_us"] / res["fused_us"], 2)
+        _log(f"{name}: {res}")
+        out[name] = res
+    big = out["prefill_8x512"]
+    return {
+        "metric": "fused RoPE + K/V append: achieved HBM GB/s (prefill chunk) and us per layer",
+        "value": big["fused_GB_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round((big["fused_us"] + out["decode_b64"]["fused_us"]) / 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: Q/K/V ~ N(0,1), seeded; Llama-3.1 rope tables (theta 5e5, llama3 scaling)",
+        "config": {"workload": "rope_append", "shapes": {"decode_b64": "64 x 1", "prefill_8x512": "8 x 512"},
+                   "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "page_size": PS, "layers": 1},
+        "shapes": out,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "nslg_rope_append at the 8 x 512 prefill chunk",
+            "timing": f"HIP events on the launch stream around {args.steps} back-to-back calls",
+            "achieved": big["fused_GB_s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(big["fused_GB_s"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": big["fused_kernel_us"],
+            "algorithmic_bytes_per_launch": big["algorithmic_bytes"],
+        },
+    }
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -702,6 +823,9 @@ def main():
         return
     if args.workload == "radix":
         print(json.dumps(run_radix(args)), flush=True)
+        return
+    if args.workload == "rope":
+        print(json.dumps(run_rope(args)), flush=True)
         return
     if args.workload in ("kv_pressure", "small_batch"):
         res, lens = run_decode(args)
