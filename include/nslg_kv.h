@@ -147,6 +147,44 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
                       nslg_stream_t stream);
 
 /*
+ * Paged decode for a batch in which groups of sequences share their first pages
+ * (a radix prefix: the same page ids, kv_cache.py:459-472, 707-716). Same result
+ * as nslg_paged_decode (within the attention tolerance: the split differs); the
+ * shared K/V of a group is read once for all its members instead of once per
+ * member: the group's prefix is one more work unit whose MFMA tiles carry the
+ * query heads of all members (G = Hq/Hkv columns each, 16 columns in all).
+ * Replaces the same FlashInfer decode run (kv_cache.py:617-621, 650).
+ *
+ *   seq_group_slot      int32[batch] (device): 16 * g + m when sequence b is member
+ *                       m of group g, else -1; must agree with group_members
+ *   num_groups          1..32
+ *   group_prefix_pages  HOST int32[num_groups]: pages shared by the group's members,
+ *                       >= 1; every member's first group_prefix_pages[g] page ids
+ *                       are the same and its length is at least that many pages
+ *   group_members       HOST int32[num_groups * 16]: member sequences of group g at
+ *                       [16 g, 16 g + n_g), -1 after them; 1 <= n_g <= 16 / G;
+ *                       a sequence is in at most one group
+ * The workspace holds 16 / G partial slots per chunk:
+ * nslg_paged_decode_grouped_workspace_size(...) bytes.
+ */
+size_t nslg_paged_decode_grouped_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                                int32_t num_kv_heads, int32_t head_dim,
+                                                int64_t total_pages, int32_t page_size,
+                                                int32_t dtype, int32_t num_groups);
+
+int nslg_paged_decode_grouped(const void* q, int64_t q_stride,
+                              const void* k_pool, const void* v_pool, int64_t num_pages,
+                              int32_t page_size, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                              int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                              int32_t dtype, const int32_t* seq_group_slot, int32_t num_groups,
+                              const int32_t* group_prefix_pages, const int32_t* group_members,
+                              void* out, int64_t out_stride,
+                              void* workspace, size_t workspace_bytes,
+                              nslg_stream_t stream);
+
+/*
  * Paged causal prefill attention over a ragged batch of new tokens whose K/V
  * are already appended to the pool (chunked prefill).
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with

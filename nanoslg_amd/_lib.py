@@ -38,6 +38,12 @@ SIGNATURES = {
                                     c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,
                                     c_void_p]),
+    "nslg_paged_decode_grouped_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
+                                                            c_int32, c_int32]),
+    "nslg_paged_decode_grouped": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
+                                            c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                            c_int32, c_float, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
+                                            c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "nslg_decode_plan_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p]),

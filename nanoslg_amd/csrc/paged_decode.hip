@@ -62,8 +62,29 @@ struct DecodeParams {
   int2* meta;            // per sequence: first chunk, chunk count (for the merge launch)
   uint16_t* out;
   int64_t out_stride;
-  float* part_o;   // [max_chunks, Hq, D]
-  float* part_ml;  // [max_chunks, Hq, 2]
+  float* part_o;   // [max_chunks, slot_members, Hq, D]
+  float* part_ml;  // [max_chunks, slot_members, Hq, 2]
+  int32_t slot_members;  // partial slots per (chunk, query head): 1, or the members of a group
+};
+
+// Prefix groups of a grouped decode call: sequences whose first pages are the same
+// pages (a shared radix prefix). The prefix of a group is one more work unit whose
+// chunks serve all its members at once: member m's query heads take MFMA columns
+// G*m .. G*m + G-1, so the shared K/V is read once per group instead of once per
+// member. Passed as kernel arguments; the host checks them.
+constexpr int kMaxGroups = 32;
+constexpr int kGroupCols = 16;  // MFMA columns
+
+template <bool kGrouped>
+struct GroupArgs {};
+
+template <>
+struct GroupArgs<true> {
+  const int32_t* seq_group_slot;  // [batch]: 16 * group + member, or -1
+  int2* group_meta;               // [num_groups]: first chunk and chunk count of the prefix
+  int32_t num_groups;
+  int32_t prefix_pages[kMaxGroups];
+  int16_t member_seq[kMaxGroups * kGroupCols];  // sequence of member m of group g, or -1
 };
 
 __device__ inline int seq_len_of(const int32_t* indptr, const int32_t* last_len, int s,
@@ -86,28 +107,57 @@ __device__ inline int wave_sum_i32(int x) {
   return (int)(c[0] + c[1]);
 }
 
-// Sequence lengths as the lanes see them: lane l holds sequence 64 i + l of
-// the batch in v[i] for the first 256 sequences (loaded once, so the searches
-// below do not go back to memory); later ones are read on demand.
+// Tokens of the prefix of group g (its first member's length bounds it, so the
+// prefix never reads past that member's block table).
+__device__ inline int group_prefix_tokens(const DecodeParams& p, const GroupArgs<true>& ga, int g) {
+  const int m0 = ga.member_seq[g * kGroupCols];
+  const int L0 = m0 >= 0 && m0 < p.batch ? seq_len_of(p.indptr, p.last_len, m0, p.page_size) : 0;
+  return min(ga.prefix_pages[g] * p.page_size, L0);
+}
+
+// Tokens of sequence b read through its group's prefix (0 outside a group).
+__device__ inline int seq_prefix_tokens(const DecodeParams& p, const GroupArgs<true>& ga, int b, int len) {
+  const int gs = ga.seq_group_slot[b];
+  const int g = gs >> 4;
+  if (gs < 0 || g >= ga.num_groups) return 0;
+  return min(ga.prefix_pages[g] * p.page_size, len);
+}
+
+// Work units of a call: sequence u's own tokens for u < batch (all of them, or those
+// after its group's prefix), then the prefix of group u - batch.
+template <bool kGrouped>
+__device__ inline int unit_len(const DecodeParams& p, const GroupArgs<kGrouped>& ga, int u) {
+  if (u < p.batch) {
+    int len = seq_len_of(p.indptr, p.last_len, u, p.page_size);
+    if constexpr (kGrouped) len -= seq_prefix_tokens(p, ga, u, len);
+    return len;
+  }
+  if constexpr (kGrouped) {
+    const int g = u - p.batch;
+    if (g < ga.num_groups) return group_prefix_tokens(p, ga, g);
+  }
+  return 0;
+}
+
+// Unit lengths as the lanes see them: lane l holds unit 64 i + l in v[i] for the
+// first 256 units (loaded once, so the searches below do not go back to memory);
+// later ones are read on demand.
+template <bool kGrouped>
 struct LaneLens {
   static constexpr int kRegs = 4;
   int v[kRegs];
-  const int32_t* indptr;
-  const int32_t* last_len;
-  int batch;
-  int page_size;
+  int units;
 
-  __device__ LaneLens(const int32_t* ip, const int32_t* ll, int b, int ps)
-      : indptr(ip), last_len(ll), batch(b), page_size(ps) {
+  __device__ LaneLens(const DecodeParams& p, const GroupArgs<kGrouped>& ga, int n) : units(n) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < kRegs; ++i) {
       const int s = 64 * i + lane;
-      v[i] = s < batch ? seq_len_of(indptr, last_len, s, page_size) : 0;
+      v[i] = s < units ? unit_len<kGrouped>(p, ga, s) : 0;
     }
   }
-  // length of sequence 64 i + lane (0 past the batch)
-  __device__ int at(int i) const {
+  // length of unit 64 i + lane (0 past the units)
+  __device__ int at(const DecodeParams& p, const GroupArgs<kGrouped>& ga, int i) const {
     if (i < kRegs) {
       int r = v[0];
 #pragma unroll
@@ -115,22 +165,24 @@ struct LaneLens {
       return r;
     }
     const int s = 64 * i + (threadIdx.x & 63);
-    return s < batch ? seq_len_of(indptr, last_len, s, page_size) : 0;
+    return s < units ? unit_len<kGrouped>(p, ga, s) : 0;
   }
 };
 
-// Smallest chunk length in [lo, hi] (multiples of 16) for which the batch's chunk
-// count sum_b ceil(L_b / len) is at most `budget`; `hi` is known to fit. The
+// Smallest chunk length in [lo, hi] (multiples of 16) for which the units' chunk
+// count sum_u ceil(L_u / len) is at most `budget`; `hi` is known to fit. The
 // count does not grow with the length, so a binary search finds it; all waves
 // compute the same value from the same lengths.
-__device__ inline int fit_chunk_tokens(const LaneLens& lens, int lo, int hi, int budget) {
+template <bool kGrouped>
+__device__ inline int fit_chunk_tokens(const DecodeParams& p, const GroupArgs<kGrouped>& ga,
+                                       const LaneLens<kGrouped>& lens, int lo, int hi, int budget) {
   int a = lo >> 4, z = hi >> 4;
-  const int groups = (lens.batch + 63) >> 6;
+  const int groups = (lens.units + 63) >> 6;
   while (a < z) {
     const int mid = (a + z) >> 1;
     const int ct = mid << 4;
     int cnt = 0;
-    for (int i = 0; i < groups; ++i) cnt += (lens.at(i) + ct - 1) / ct;
+    for (int i = 0; i < groups; ++i) cnt += (lens.at(p, ga, i) + ct - 1) / ct;
     cnt = __builtin_amdgcn_readfirstlane(wave_sum_i32(cnt));
     if (cnt <= budget)
       z = mid;
@@ -140,14 +192,16 @@ __device__ inline int fit_chunk_tokens(const LaneLens& lens, int lo, int hi, int
   return a << 4;
 }
 
-// Wave-wide search for the sequence owning global chunk `g`.
-__device__ inline bool locate_chunk(const LaneLens& lens, int chunk_tokens, int g, int& b, int& cstart,
-                                    int& nchunks) {
+// Wave-wide search for the unit owning global chunk `g`.
+template <bool kGrouped>
+__device__ inline bool locate_chunk(const DecodeParams& p, const GroupArgs<kGrouped>& ga,
+                                    const LaneLens<kGrouped>& lens, int chunk_tokens, int g, int& b,
+                                    int& cstart, int& nchunks) {
   const int lane = threadIdx.x & 63;
   int base = 0;
-  const int groups = (lens.batch + 63) >> 6;
+  const int groups = (lens.units + 63) >> 6;
   for (int i = 0; i < groups; ++i) {
-    const int len = lens.at(i);
+    const int len = lens.at(p, ga, i);
     const int nc = (len + chunk_tokens - 1) / chunk_tokens;
     int incl = nc;
 #pragma unroll
@@ -245,9 +299,9 @@ __device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, 
 // always relative to the same m.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename T, int D, bool kTileInPage, int kDepth>
+template <typename T, int D, bool kTileInPage, int kDepth, bool kGrouped>
 __global__ void __launch_bounds__(64 * kMaxWaves)
-paged_decode_kernel(DecodeParams p) {
+paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;  // P = hi + lo for bf16's 8-bit mantissa
@@ -257,33 +311,77 @@ paged_decode_kernel(DecodeParams p) {
   const int h = blockIdx.y * (blockDim.x >> 6) + wave;
   if (h >= p.num_kv_heads) return;
 
-  const LaneLens lens(p.indptr, p.last_len, p.batch, p.page_size);
+  int units = p.batch;
+  if constexpr (kGrouped) units += ga.num_groups;
+  const LaneLens<kGrouped> lens(p, ga, units);
   int ct = p.chunk_tokens;
-  if (p.chunk_budget > 0) ct = fit_chunk_tokens(lens, 64, ct, p.chunk_budget);
-  int b = 0, cstart = 0, nchunks = 0;
-  if (!locate_chunk(lens, ct, chunk, b, cstart, nchunks)) return;
-  b = __builtin_amdgcn_readfirstlane(b);
+  if (p.chunk_budget > 0) ct = fit_chunk_tokens<kGrouped>(p, ga, lens, 64, ct, p.chunk_budget);
+  int u = 0, cstart = 0, nchunks = 0;
+  if (!locate_chunk<kGrouped>(p, ga, lens, ct, chunk, u, cstart, nchunks)) return;
+  u = __builtin_amdgcn_readfirstlane(u);
   cstart = __builtin_amdgcn_readfirstlane(cstart);
   nchunks = __builtin_amdgcn_readfirstlane(nchunks);
-  if (chunk == cstart && blockIdx.y == 0 && threadIdx.x == 0) p.meta[b] = make_int2(cstart, nchunks);
-  const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
-  // chunk c of the sequence's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
+  // The unit: sequence b's tokens [base, base + len) (all of them, or those after its
+  // group's prefix), or group g's prefix [0, len), read through member 0's table.
+  int b = u, g = -1, base = 0, len = 0;
+  bool merged = false;  // the sequence's result also takes its group's prefix
+  if constexpr (kGrouped) {
+    if (u >= p.batch) {
+      g = u - p.batch;
+      b = ga.member_seq[g * kGroupCols];
+      len = group_prefix_tokens(p, ga, g);
+    } else {
+      const int L = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+      base = seq_prefix_tokens(p, ga, b, L);
+      len = L - base;
+      merged = ga.seq_group_slot[b] >= 0 && (ga.seq_group_slot[b] >> 4) < ga.num_groups;
+    }
+    b = __builtin_amdgcn_readfirstlane(b);
+    g = __builtin_amdgcn_readfirstlane(g);
+    base = __builtin_amdgcn_readfirstlane(base);
+    len = __builtin_amdgcn_readfirstlane(len);
+  } else {
+    len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+  }
+  if (chunk == cstart && blockIdx.y == 0 && threadIdx.x == 0) {
+    if constexpr (kGrouped) {
+      if (g >= 0)
+        ga.group_meta[g] = make_int2(cstart, nchunks);
+      else
+        p.meta[b] = make_int2(cstart, nchunks);
+    } else {
+      p.meta[b] = make_int2(cstart, nchunks);
+    }
+  }
+  // chunk c of the unit's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
   const int ntiles_seq = (len + 15) >> 4;
   const int c_local = chunk - cstart;
-  const int t_begin = 16 * (int)((int64_t)c_local * ntiles_seq / nchunks);
-  const int t_end = min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
+  const int t_begin = base + 16 * (int)((int64_t)c_local * ntiles_seq / nchunks);
+  const int t_end = base + min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
   const int t_last = t_end - 1;
   const int32_t* idx = p.indices + p.indptr[b];
 
+  // Column r of the MFMA tiles (lane l: r = l % 16) is query head h*G + r of sequence
+  // b; in a group's prefix it is head h*G + r%G of member r/G.
   const int r = lane & 15;
   const int gq = lane >> 4;
-  const int hq = h * p.group + r;
-  const bool head_ok = r < p.group;
+  int hq = h * p.group + r;
+  bool head_ok = r < p.group;
+  int col_seq = b;
+  int member = 0;
+  if constexpr (kGrouped) {
+    if (g >= 0) {
+      member = r / p.group;
+      hq = h * p.group + r % p.group;
+      col_seq = ga.member_seq[g * kGroupCols + member];
+      head_ok = col_seq >= 0 && col_seq < p.batch;
+    }
+  }
 
-  // Q^T operand: lane l holds Q[head l%16][32s + 8(l/16) .. +8]; zero for padding heads.
+  // Q^T operand: lane l holds Q[column l%16][32s + 8(l/16) .. +8]; zero for padding columns.
   u16x8 qb[kSteps];
   if (head_ok) {
-    const uint16_t* qrow = p.q + (int64_t)b * p.q_stride + (int64_t)hq * D;
+    const uint16_t* qrow = p.q + (int64_t)col_seq * p.q_stride + (int64_t)hq * D;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) qb[s] = *reinterpret_cast<const u16x8*>(qrow + 32 * s + 8 * gq);
   } else {
@@ -427,8 +525,8 @@ paged_decode_kernel(DecodeParams p) {
   const float l_tot = rows_sum(l_run);
   if (!head_ok) return;
 
-  // Lane l holds O[head r][d = NT*(4*gq + i) + n] in o[n][i].
-  if (nchunks == 1) {
+  // Lane l holds O[column r][d = NT*(4*gq + i) + n] in o[n][i].
+  if (nchunks == 1 && g < 0 && !merged) {
     const float inv = 1.f / l_tot;
     uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D;
 #pragma unroll
@@ -439,7 +537,7 @@ paged_decode_kernel(DecodeParams p) {
       *reinterpret_cast<typename RowVec<NT>::type*>(orow + NT * (4 * gq + i)) = w;
     }
   } else {
-    const int64_t slot = (int64_t)chunk * p.num_qo_heads + hq;
+    const int64_t slot = ((int64_t)chunk * p.slot_members + member) * p.num_qo_heads + hq;
     float* prow = p.part_o + slot * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -464,6 +562,7 @@ struct MergeParams {
   int32_t num_qo_heads;
   const int2* meta;  // per sequence: first chunk, chunk count, from the decode launch
   int32_t max_chunks;
+  int32_t slot_members;
   const float* part_o;
   const float* part_ml;
   uint16_t* out;
@@ -471,13 +570,14 @@ struct MergeParams {
 };
 
 // Merge of the split-K partials: one wave per (sequence, query head). Sequences
-// with several chunks are merged; empty sequences get zero rows; single-chunk
-// sequences were finished by the decode kernel. The wave reads its sequence's
-// chunk range (one round of loads), then the chunks' (m, l) with lanes over
-// chunks and the first rows of O with lanes over (chunk, d) in one more round:
-// O row c is D floats, D/4 lanes read it as float4s, 64/(D/4) rows per load.
-template <typename T, int D>
-__global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
+// with several partials (chunks of their own tokens, and of their group's prefix)
+// are merged; empty sequences get zero rows; sequences with a single chunk and no
+// group were finished by the decode kernel. The wave reads its sequence's chunk
+// ranges (one round of loads), then the partials' (m, l) with lanes over partials
+// and the first rows of O with lanes over (partial, d) in one more round: O row c
+// is D floats, D/4 lanes read it as float4s, 64/(D/4) rows per load.
+template <typename T, int D, bool kGrouped>
+__global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupArgs<kGrouped> ga) {
   constexpr int LPC = D / 4;     // lanes per O row
   constexpr int CPI = 64 / LPC;  // O rows per load instruction
   constexpr int kBatch = 8;      // load instructions per lane in flight
@@ -495,23 +595,43 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
     if (sub == 0) *reinterpret_cast<u16x4*>(orow) = u16x4{0, 0, 0, 0};
     return;
   }
+  // own chunks [cstart, cstart + nown) at member slot 0; the group prefix's chunks
+  // [gstart, gstart + ngrp) at the sequence's member slot
+  int own = len, member = 0, gstart = 0, ngrp = 0;
+  if constexpr (kGrouped) {
+    const int gs = ga.seq_group_slot[b];
+    const int g = gs >> 4;
+    if (gs >= 0 && g < ga.num_groups && (gs & 15) < p.slot_members) {
+      own = len - min(ga.prefix_pages[g] * p.page_size, len);
+      const int2 gm = ga.group_meta[g];
+      member = gs & 15;
+      gstart = gm.x;
+      ngrp = gm.y;
+      if (gstart < 0 || gstart >= p.max_chunks || ngrp < 0) ngrp = 0;
+      if (gstart + ngrp > p.max_chunks) ngrp = p.max_chunks - gstart;
+    }
+  }
   const int cstart = mt.x;
-  int nchunks = mt.y;
-  if (nchunks <= 1 || cstart < 0 || cstart >= p.max_chunks) return;
-  if (cstart + nchunks > p.max_chunks) nchunks = p.max_chunks - cstart;
+  int nown = own > 0 ? mt.y : 0;
+  if (nown > 0 && (cstart < 0 || cstart >= p.max_chunks)) nown = 0;
+  if (cstart + nown > p.max_chunks) nown = p.max_chunks - cstart;
+  if (ngrp == 0 && nown <= 1) return;
+  const int nchunks = nown + ngrp;
 
-  const float* ml = p.part_ml + ((int64_t)cstart * p.num_qo_heads + hq) * 2;
-  const int64_t ml_stride = (int64_t)p.num_qo_heads * 2;
-  const float* po = p.part_o + ((int64_t)cstart * p.num_qo_heads + hq) * D + d0;
-  const int64_t po_stride = (int64_t)p.num_qo_heads * D;
+  // partial k of the sequence -> its slot
+  auto slot_of = [&](int k) -> int64_t {
+    const int64_t ck = k < nown ? (int64_t)(cstart + k) * p.slot_members
+                                : (int64_t)(gstart + k - nown) * p.slot_members + member;
+    return ck * p.num_qo_heads + hq;
+  };
   f32x4 oc[kBatch];
   float mc[kBatch];
   auto load_rows = [&](int c0) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-      const int c = min(c0 + CPI * k + sub, nchunks - 1);
-      oc[k] = *reinterpret_cast<const f32x4*>(po + c * po_stride);
-      mc[k] = ml[c * ml_stride];
+      const int64_t sl = slot_of(min(c0 + CPI * k + sub, nchunks - 1));
+      oc[k] = *reinterpret_cast<const f32x4*>(p.part_o + sl * D + d0);
+      mc[k] = p.part_ml[sl * 2];
     }
   };
   load_rows(0);  // in flight with the (m, l) pass below
@@ -519,7 +639,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
   // the running max M and the denominator sum_c 2^(m_c - M) l_c, lanes over chunks
   float mmax = -INFINITY, lsum = 0.f;
   for (int c = lane; c < nchunks; c += 64) {
-    const float2 v = *reinterpret_cast<const float2*>(ml + c * ml_stride);
+    const float2 v = *reinterpret_cast<const float2*>(p.part_ml + slot_of(c) * 2);
     const float m_new = fmaxf(mmax, v.x);
     lsum = lsum * fast_exp2(mmax - m_new) + v.y * fast_exp2(v.x - m_new);
     mmax = m_new;
@@ -565,7 +685,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p) {
 constexpr int kMaxDevices = 64;
 constexpr int kDefaultSlots = 768;
 
-template <typename T, int D, bool kTileInPage>
+template <typename T, int D, bool kTileInPage, bool kGrouped>
 int decode_wg_slots(int waves) {
   static std::atomic<int> cache[kMaxDevices][kMaxWaves + 1];
   int dev = 0;
@@ -577,7 +697,7 @@ int decode_wg_slots(int waves) {
   if (v > 0) return v;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, kTileInPage, 2>,
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, kTileInPage, 2, kGrouped>,
                                                    64 * waves, 0) != hipSuccess ||
       cus <= 0 || per_cu <= 0) {
     (void)hipGetLastError();
@@ -596,90 +716,92 @@ struct DecodeShape {
   int64_t max_chunks;
 };
 
-// Chunk length for `total_tokens` (an upper bound of the batch's tokens) over
-// `batch` sequences. Sequence b gets ceil(L_b / len) chunks, at most
-// total / len + batch in all, so len = total / (capacity - batch) keeps every
-// chunk of the grid resident at once; the kernel then lowers it to the smallest
-// length that still fits `capacity` chunks for the actual lengths. A batch too
-// large for that (capacity <= 2 * batch) gets about `capacity` chunks per round
-// at the host's length. Lengths are multiples of 16 (tiles never straddle a
-// chunk) and at least 64.
-template <typename T, int D>
-DecodeShape decode_shape(int32_t batch, int32_t num_kv_heads, int64_t total_tokens, int page_size) {
+// Chunk length for `total_tokens` (an upper bound of the units' tokens) over
+// `units` work units (sequences, plus group prefixes). Unit u gets
+// ceil(L_u / len) chunks, at most total / len + units in all, so
+// len = total / (capacity - units) keeps every chunk of the grid resident at
+// once; the kernel then lowers it to the smallest length that still fits
+// `capacity` chunks for the actual lengths. Too many units for that
+// (capacity <= 2 * units) get about `capacity` chunks per round at the host's
+// length. Lengths are multiples of 16 (tiles never straddle a chunk) and at
+// least 64.
+template <typename T, int D, bool kGrouped>
+DecodeShape decode_shape(int32_t units, int32_t num_kv_heads, int64_t total_tokens, int page_size) {
   DecodeShape sh;
   sh.waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
   sh.head_groups = (num_kv_heads + sh.waves - 1) / sh.waves;
-  const int slots = page_size % 16 == 0 ? decode_wg_slots<T, D, true>(sh.waves)
-                                        : decode_wg_slots<T, D, false>(sh.waves);
+  const int slots = page_size % 16 == 0 ? decode_wg_slots<T, D, true, kGrouped>(sh.waves)
+                                        : decode_wg_slots<T, D, false, kGrouped>(sh.waves);
   int64_t capacity = slots / sh.head_groups;
   if (capacity < 1) capacity = 1;
-  const bool fit = capacity > 2 * (int64_t)batch;
-  const int64_t usable = fit ? capacity - batch : capacity;
+  const bool fit = capacity > 2 * (int64_t)units;
+  const int64_t usable = fit ? capacity - units : capacity;
   int64_t c = (total_tokens + usable - 1) / usable;
   c = ((c + 15) / 16) * 16;
   if (c < 64) c = 64;
   if (c > ((int64_t)1 << 30)) c = (int64_t)1 << 30;
   sh.chunk_tokens = (int)c;
   sh.chunk_budget = fit ? (int)capacity : 0;
-  sh.max_chunks = fit ? capacity : (total_tokens + c - 1) / c + batch;
+  sh.max_chunks = fit ? capacity : (total_tokens + c - 1) / c + units;
   return sh;
 }
 
-template <typename T, int D>
-int launch_decode(const DecodeParams& p, const MergeParams& mp, int waves, hipStream_t s) {
-  const dim3 grid((unsigned)p.max_chunks, (unsigned)p.head_groups);
-  if (p.page_size % 16 == 0)
-    paged_decode_kernel<T, D, true, 2><<<grid, 64 * waves, 0, s>>>(p);
-  else
-    paged_decode_kernel<T, D, false, 2><<<grid, 64 * waves, 0, s>>>(p);
-  int rc = check_launch("paged_decode");
-  if (rc) return rc;
-  decode_merge_kernel<T, D><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp);
-  return check_launch("paged_decode_merge");
-}
-
-template <typename T>
-DecodeShape decode_shape_for(int32_t head_dim, int32_t batch, int32_t num_kv_heads, int64_t total_tokens,
+template <typename T, bool kGrouped>
+DecodeShape decode_shape_for(int32_t head_dim, int32_t units, int32_t num_kv_heads, int64_t total_tokens,
                              int page_size) {
   switch (head_dim) {
-    case 64: return decode_shape<T, 64>(batch, num_kv_heads, total_tokens, page_size);
-    case 128: return decode_shape<T, 128>(batch, num_kv_heads, total_tokens, page_size);
-    default: return decode_shape<T, 256>(batch, num_kv_heads, total_tokens, page_size);
+    case 64: return decode_shape<T, 64, kGrouped>(units, num_kv_heads, total_tokens, page_size);
+    case 128: return decode_shape<T, 128, kGrouped>(units, num_kv_heads, total_tokens, page_size);
+    default: return decode_shape<T, 256, kGrouped>(units, num_kv_heads, total_tokens, page_size);
   }
 }
 
-}  // namespace
-}  // namespace nslg
-
-using namespace nslg;
-
-extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
-                                                   int32_t num_kv_heads, int32_t head_dim,
-                                                   int64_t total_pages, int32_t page_size,
-                                                   int32_t dtype) {
-  if (batch <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || total_pages < 0 ||
-      page_size <= 0)
-    return 0;
-  if (num_qo_heads % num_kv_heads) return 0;
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
-  const int64_t total_tokens = total_pages * page_size;
-  const DecodeShape sh = dtype == NSLG_BF16
-                             ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
-                             : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
-  // partials [max_chunks, Hq, D] and [max_chunks, Hq, 2] fp32, then each sequence's
-  // chunk range (int32 pairs), rounded up to 256 bytes
-  return (size_t)(sh.max_chunks * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) +
-         (((size_t)batch * 8 + 255) & ~(size_t)255);
+template <bool kGrouped>
+DecodeShape shape_of(int32_t dtype, int32_t head_dim, int32_t units, int32_t num_kv_heads, int64_t total_tokens,
+                     int page_size) {
+  return dtype == NSLG_BF16
+             ? decode_shape_for<BF16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size)
+             : decode_shape_for<F16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size);
 }
 
-extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_pool,
-                                 const void* v_pool, int64_t num_pages, int32_t page_size,
-                                 const int32_t* kv_indptr, const int32_t* kv_indices,
-                                 const int32_t* kv_last_page_len, int64_t total_pages,
-                                 int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
-                                 int32_t head_dim, float sm_scale, int32_t dtype, void* out,
-                                 int64_t out_stride, void* workspace, size_t workspace_bytes,
-                                 nslg_stream_t stream) {
+template <typename T, int D, bool kGrouped>
+int launch_decode(const DecodeParams& p, const MergeParams& mp, const GroupArgs<kGrouped>& ga, int waves,
+                  hipStream_t s) {
+  const dim3 grid((unsigned)p.max_chunks, (unsigned)p.head_groups);
+  if (p.page_size % 16 == 0)
+    paged_decode_kernel<T, D, true, 2, kGrouped><<<grid, 64 * waves, 0, s>>>(p, ga);
+  else
+    paged_decode_kernel<T, D, false, 2, kGrouped><<<grid, 64 * waves, 0, s>>>(p, ga);
+  int rc = check_launch("paged_decode");
+  if (rc) return rc;
+  decode_merge_kernel<T, D, kGrouped><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp, ga);
+  return check_launch("paged_decode_merge");
+}
+
+inline size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace: partials [max_chunks, slot_members, Hq, D] and [..., 2] fp32, then each
+// sequence's chunk range, then each group prefix's chunk range (int32 pairs), each
+// region rounded up to 256 bytes.
+size_t workspace_bytes_for(const DecodeShape& sh, int32_t batch, int32_t num_qo_heads, int32_t head_dim,
+                           int32_t slot_members, int32_t num_groups) {
+  return (size_t)(sh.max_chunks * slot_members * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) +
+         round256((size_t)batch * 8) + (num_groups > 0 ? round256((size_t)num_groups * 8) : 0);
+}
+
+bool shape_ok(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int64_t total_pages,
+              int32_t page_size) {
+  return batch > 0 && num_qo_heads > 0 && num_kv_heads > 0 && total_pages >= 0 && page_size > 0 &&
+         num_qo_heads % num_kv_heads == 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+template <bool kGrouped>
+int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void* v_pool, int64_t num_pages,
+                int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
+                const int32_t* kv_last_page_len, int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                int64_t out_stride, GroupArgs<kGrouped>& ga, int32_t num_groups, int32_t slot_members,
+                void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_pages < 0)
     return fail(NSLG_EINVAL, "paged_decode: bad sizes");
@@ -701,13 +823,10 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
     return fail(NSLG_EINVAL, "paged_decode: q/pool/out must be 16-byte aligned");
   const int64_t total_tokens = total_pages * page_size;
   if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
-  const DecodeShape sh = dtype == NSLG_BF16
-                             ? decode_shape_for<BF16>(head_dim, batch, num_kv_heads, total_tokens, page_size)
-                             : decode_shape_for<F16>(head_dim, batch, num_kv_heads, total_tokens, page_size);
-  const int ct = sh.chunk_tokens;
+  const DecodeShape sh =
+      shape_of<kGrouped>(dtype, head_dim, batch + num_groups, num_kv_heads, total_tokens, page_size);
   const int64_t mc = sh.max_chunks;
-  const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, total_pages,
-                                                       page_size, dtype);
+  const size_t need = workspace_bytes_for(sh, batch, num_qo_heads, head_dim, slot_members, num_groups);
   if (!workspace || workspace_bytes < need)
     return fail(NSLG_EWORKSPACE, "paged_decode: workspace %zu < %zu bytes", workspace_bytes, need);
   if (((uintptr_t)workspace) & 255) return fail(NSLG_EINVAL, "paged_decode: workspace must be 256-byte aligned");
@@ -727,16 +846,19 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   p.num_kv_heads = num_kv_heads;
   p.group = group;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  p.chunk_tokens = ct;
+  p.chunk_tokens = sh.chunk_tokens;
   p.chunk_budget = sh.chunk_budget;
   p.max_chunks = (int32_t)mc;
   p.head_groups = sh.head_groups;
   p.out = (uint16_t*)out;
   p.out_stride = out_stride;
-  float* ws = (float*)workspace;
-  p.part_o = ws;
-  p.part_ml = ws + mc * num_qo_heads * head_dim;
-  p.meta = reinterpret_cast<int2*>(ws + mc * num_qo_heads * (head_dim + 2));
+  p.slot_members = slot_members;
+  char* ws = (char*)workspace;
+  p.part_o = (float*)ws;
+  p.part_ml = p.part_o + mc * slot_members * num_qo_heads * head_dim;
+  char* meta = ws + (size_t)(mc * slot_members * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float));
+  p.meta = reinterpret_cast<int2*>(meta);
+  if constexpr (kGrouped) ga.group_meta = reinterpret_cast<int2*>(meta + round256((size_t)batch * 8));
 
   MergeParams mp;
   mp.indptr = kv_indptr;
@@ -746,6 +868,7 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   mp.num_qo_heads = num_qo_heads;
   mp.meta = p.meta;
   mp.max_chunks = (int32_t)mc;
+  mp.slot_members = slot_members;
   mp.part_o = p.part_o;
   mp.part_ml = p.part_ml;
   mp.out = p.out;
@@ -754,14 +877,113 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) {
     switch (head_dim) {
-      case 64: return launch_decode<F16, 64>(p, mp, sh.waves, s);
-      case 128: return launch_decode<F16, 128>(p, mp, sh.waves, s);
-      default: return launch_decode<F16, 256>(p, mp, sh.waves, s);
+      case 64: return launch_decode<F16, 64, kGrouped>(p, mp, ga, sh.waves, s);
+      case 128: return launch_decode<F16, 128, kGrouped>(p, mp, ga, sh.waves, s);
+      default: return launch_decode<F16, 256, kGrouped>(p, mp, ga, sh.waves, s);
     }
   }
   switch (head_dim) {
-    case 64: return launch_decode<BF16, 64>(p, mp, sh.waves, s);
-    case 128: return launch_decode<BF16, 128>(p, mp, sh.waves, s);
-    default: return launch_decode<BF16, 256>(p, mp, sh.waves, s);
+    case 64: return launch_decode<BF16, 64, kGrouped>(p, mp, ga, sh.waves, s);
+    case 128: return launch_decode<BF16, 128, kGrouped>(p, mp, ga, sh.waves, s);
+    default: return launch_decode<BF16, 256, kGrouped>(p, mp, ga, sh.waves, s);
   }
+}
+
+}  // namespace
+}  // namespace nslg
+
+using namespace nslg;
+
+extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                                   int32_t num_kv_heads, int32_t head_dim,
+                                                   int64_t total_pages, int32_t page_size,
+                                                   int32_t dtype) {
+  if (!shape_ok(batch, num_qo_heads, num_kv_heads, head_dim, total_pages, page_size)) return 0;
+  const DecodeShape sh = shape_of<false>(dtype, head_dim, batch, num_kv_heads, total_pages * page_size, page_size);
+  return workspace_bytes_for(sh, batch, num_qo_heads, head_dim, 1, 0);
+}
+
+extern "C" size_t nslg_paged_decode_grouped_workspace_size(int32_t batch, int32_t num_qo_heads,
+                                                           int32_t num_kv_heads, int32_t head_dim,
+                                                           int64_t total_pages, int32_t page_size,
+                                                           int32_t dtype, int32_t num_groups) {
+  if (!shape_ok(batch, num_qo_heads, num_kv_heads, head_dim, total_pages, page_size)) return 0;
+  if (num_groups < 1 || num_groups > kMaxGroups) return 0;
+  const int group = num_qo_heads / num_kv_heads;
+  if (group > kGroupCols) return 0;
+  const DecodeShape sh =
+      shape_of<true>(dtype, head_dim, batch + num_groups, num_kv_heads, total_pages * page_size, page_size);
+  return workspace_bytes_for(sh, batch, num_qo_heads, head_dim, kGroupCols / group, num_groups);
+}
+
+extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_pool,
+                                 const void* v_pool, int64_t num_pages, int32_t page_size,
+                                 const int32_t* kv_indptr, const int32_t* kv_indices,
+                                 const int32_t* kv_last_page_len, int64_t total_pages,
+                                 int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                 int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                 nslg_stream_t stream) {
+  GroupArgs<false> ga;
+  return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
+                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const void* k_pool,
+                                         const void* v_pool, int64_t num_pages, int32_t page_size,
+                                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                                         const int32_t* kv_last_page_len, int64_t total_pages,
+                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, float sm_scale, int32_t dtype,
+                                         const int32_t* seq_group_slot, int32_t num_groups,
+                                         const int32_t* group_prefix_pages, const int32_t* group_members,
+                                         void* out, int64_t out_stride, void* workspace,
+                                         size_t workspace_bytes, nslg_stream_t stream) {
+  if (num_groups < 1 || num_groups > kMaxGroups)
+    return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: %d groups (1..%d)", num_groups, kMaxGroups);
+  if (!seq_group_slot || !group_prefix_pages || !group_members)
+    return fail(NSLG_EINVAL, "paged_decode_grouped: null group table");
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
+    return fail(NSLG_EINVAL, "paged_decode_grouped: bad head counts");
+  const int group = num_qo_heads / num_kv_heads;
+  if (group > kGroupCols) return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: GQA group %d > 16", group);
+  const int max_members = kGroupCols / group;
+  GroupArgs<true> ga;
+  ga.seq_group_slot = seq_group_slot;
+  ga.group_meta = nullptr;
+  ga.num_groups = num_groups;
+  // host check of the group table: members are distinct sequences of the batch,
+  // at least one and at most 16 / G per group, listed first; prefixes are >= 1 page
+  for (int g = 0; g < kMaxGroups; ++g) {
+    ga.prefix_pages[g] = 0;
+    for (int m = 0; m < kGroupCols; ++m) ga.member_seq[g * kGroupCols + m] = -1;
+  }
+  for (int g = 0; g < num_groups; ++g) {
+    if (group_prefix_pages[g] < 1 || (int64_t)group_prefix_pages[g] * page_size >= ((int64_t)1 << 31))
+      return fail(NSLG_EINVAL, "paged_decode_grouped: group %d prefix of %d pages", g, group_prefix_pages[g]);
+    ga.prefix_pages[g] = group_prefix_pages[g];
+    bool ended = false;
+    int count = 0;
+    for (int m = 0; m < kGroupCols; ++m) {
+      const int sq = group_members[g * kGroupCols + m];
+      if (sq < 0) {
+        ended = true;
+        continue;
+      }
+      if (ended || sq >= batch || m >= max_members)
+        return fail(NSLG_EINVAL, "paged_decode_grouped: group %d member %d (sequence %d) invalid", g, m, sq);
+      for (int g2 = 0; g2 <= g; ++g2)
+        for (int m2 = 0; m2 < (g2 == g ? m : kGroupCols); ++m2)
+          if (group_members[g2 * kGroupCols + m2] == sq)
+            return fail(NSLG_EINVAL, "paged_decode_grouped: sequence %d in two group slots", sq);
+      ga.member_seq[g * kGroupCols + m] = (int16_t)sq;
+      ++count;
+    }
+    if (count == 0) return fail(NSLG_EINVAL, "paged_decode_grouped: group %d has no member", g);
+  }
+  if (batch > 32767) return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: batch %d > 32767", batch);
+  return decode_impl<true>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
+                           kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                           dtype, out, out_stride, ga, num_groups, max_members, workspace, workspace_bytes, stream);
 }

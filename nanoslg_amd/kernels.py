@@ -219,6 +219,39 @@ class Workspace:
         return self.buf
 
 
+class DecodeGroups:
+    """Prefix groups of a decode batch: sequences whose first pages are the same pages.
+
+    members: list of lists of batch indices (one list per group, at most 16 / G each),
+    prefix_pages: pages each group shares. Builds the device array seq_group_slot
+    (16 * group + member per sequence, -1 outside groups) and the host tables the
+    grouped decode entry point takes."""
+
+    MAX_GROUPS = 32
+
+    def __init__(self, batch: int, members, prefix_pages, device, seq_group_slot: Optional[torch.Tensor] = None):
+        import numpy as np
+        if not 1 <= len(members) <= self.MAX_GROUPS or len(prefix_pages) != len(members):
+            raise ValueError(f"DecodeGroups: 1..{self.MAX_GROUPS} groups, one prefix length each")
+        self.num_groups = len(members)
+        self.members = [list(map(int, m)) for m in members]
+        self.prefix_pages_np = np.ascontiguousarray(prefix_pages, dtype=np.int32)
+        table = np.full((self.num_groups, 16), -1, np.int32)
+        slot = np.full(batch, -1, np.int32)
+        for g, ms in enumerate(self.members):
+            if not 1 <= len(ms) <= 16:
+                raise ValueError("DecodeGroups: 1..16 members per group")
+            table[g, :len(ms)] = ms
+            for m, b in enumerate(ms):
+                if not 0 <= b < batch or slot[b] >= 0:
+                    raise ValueError(f"DecodeGroups: sequence {b} is not a distinct batch row")
+                slot[b] = 16 * g + m
+        self.members_np = np.ascontiguousarray(table.reshape(-1))
+        self.slot_np = slot
+        self.seq_group_slot = (seq_group_slot if seq_group_slot is not None
+                               else torch.from_numpy(slot).to(device))
+
+
 def paged_decode_workspace_size(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int,
                                 total_pages: int, page_size: int, dtype: torch.dtype) -> int:
     return int(_lib.load().nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim,
@@ -228,9 +261,11 @@ def paged_decode_workspace_size(batch: int, num_qo_heads: int, num_kv_heads: int
 def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                  total_pages: int, sm_scale: Optional[float] = None,
-                 out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None
-                 ) -> torch.Tensor:
-    """Decode attention. q: [B, Hq, D] (rows may be strided); returns [B, Hq, D]."""
+                 out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
+                 groups: Optional[DecodeGroups] = None) -> torch.Tensor:
+    """Decode attention. q: [B, Hq, D] (rows may be strided); returns [B, Hq, D].
+    With `groups`, the shared prefix pages of each group are read once for all its
+    members (nslg_paged_decode_grouped)."""
     _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
         _i32(t, n)
@@ -249,14 +284,32 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     if out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D or out.dtype != q.dtype:
         raise ValueError("paged_decode: bad out tensor")
     lib = _lib.load()
-    need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(total_pages), ps, dtype_code(q.dtype)))
-    ws = (workspace or Workspace(q.device)).get(need)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
-    rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
-                               kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
-                               int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
-                               out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
-    _lib.check(rc, "nslg_paged_decode")
+    if groups is None:
+        need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(total_pages), ps, dtype_code(q.dtype)))
+        ws = (workspace or Workspace(q.device)).get(need)
+        rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
+                                   kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                                   int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
+                                   out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+        _lib.check(rc, "nslg_paged_decode")
+        return out
+    _require_gpu(q, groups.seq_group_slot)
+    _i32(groups.seq_group_slot, "seq_group_slot")
+    if groups.seq_group_slot.numel() != B:
+        raise ValueError("paged_decode: one group slot per sequence")
+    need = int(lib.nslg_paged_decode_grouped_workspace_size(B, Hq, Hkv, D, int(total_pages), ps,
+                                                            dtype_code(q.dtype), groups.num_groups))
+    if need == 0:
+        raise ValueError("paged_decode: unsupported grouped decode shape")
+    ws = (workspace or Workspace(q.device)).get(need)
+    rc = lib.nslg_paged_decode_grouped(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
+                                       kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                                       int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
+                                       groups.seq_group_slot.data_ptr(), groups.num_groups,
+                                       groups.prefix_pages_np.ctypes.data, groups.members_np.ctypes.data,
+                                       out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+    _lib.check(rc, "nslg_paged_decode_grouped")
     return out
 
 
@@ -312,7 +365,7 @@ class DecodeLaunch:
     def __init__(self, k_pool: torch.Tensor, v_pool: torch.Tensor, slot_mapping: torch.Tensor,
                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                  total_pages: int, num_qo_heads: int, workspace: Optional[Workspace] = None,
-                 sm_scale: Optional[float] = None):
+                 sm_scale: Optional[float] = None, groups: Optional[DecodeGroups] = None):
         _require_gpu(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
         for t, n in ((slot_mapping, "slot_mapping"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
                      (kv_last_page_len, "kv_last_page_len")):
@@ -333,8 +386,20 @@ class DecodeLaunch:
         self.slots, self.indptr, self.indices, self.lpl = (slot_mapping.data_ptr(), kv_indptr.data_ptr(),
                                                            kv_indices.data_ptr(), kv_last_page_len.data_ptr())
         self.total_pages = int(total_pages)
-        need = int(self.lib.nslg_paged_decode_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages, ps,
-                                                             self.code))
+        self.groups = groups
+        if groups is None:
+            need = int(self.lib.nslg_paged_decode_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages, ps,
+                                                                 self.code))
+        else:
+            _require_gpu(k_pool, groups.seq_group_slot)
+            _i32(groups.seq_group_slot, "seq_group_slot")
+            if groups.seq_group_slot.numel() != B:
+                raise ValueError("DecodeLaunch: one group slot per sequence")
+            need = int(self.lib.nslg_paged_decode_grouped_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages,
+                                                                         ps, self.code, groups.num_groups))
+            if need == 0:
+                raise ValueError("DecodeLaunch: unsupported grouped decode shape")
+            self.keep = self.keep + (groups.seq_group_slot,)
         self.ws = (workspace or Workspace(self.device)).get(need)
         self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
 
@@ -380,10 +445,19 @@ class DecodeLaunch:
             _lib.check(rc, "nslg_rope_append")
             q_ptr, q_stride = q_rot.data_ptr(), Hq * D
         out = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
-        rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
-                                   self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
-                                   out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
-        _lib.check(rc, "nslg_paged_decode")
+        grp = self.groups
+        if grp is None:
+            rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
+                                       self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
+                                       out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
+            _lib.check(rc, "nslg_paged_decode")
+        else:
+            rc = lib.nslg_paged_decode_grouped(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
+                                               self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale,
+                                               self.code, grp.seq_group_slot.data_ptr(), grp.num_groups,
+                                               grp.prefix_pages_np.ctypes.data, grp.members_np.ctypes.data,
+                                               out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
+            _lib.check(rc, "nslg_paged_decode_grouped")
         return out
 
 

@@ -502,3 +502,94 @@ def test_decode_plan_step_zeroes_opened_pages(L, ps, Hkv, D, B):
         assert torch.equal(a, b)
     assert torch.equal(k_pool, k_exp)
     assert torch.equal(v_pool, v_exp)
+
+
+def _grouped_case(Hq, Hkv, ps, dtype, seed, group_sizes, prefix_pages, n_alone, own_max=300):
+    """A batch in which groups of sequences share their first pages (same page ids),
+    plus sequences of their own, in shuffled batch order. Returns the grouped and the
+    plain decode outputs and the oracle's."""
+    K = _k()
+    rng = np.random.default_rng(seed)
+    B = sum(group_sizes) + n_alone
+    order = rng.permutation(B).tolist()
+    members, lens, tables = [], [0] * B, [None] * B
+    next_page = iter(rng.permutation(np.arange(1, 20000)).tolist())
+    pos = 0
+    for gsz, pp in zip(group_sizes, prefix_pages):
+        shared = [next(next_page) for _ in range(pp)]
+        ms = order[pos:pos + gsz]
+        pos += gsz
+        members.append(ms)
+        for i, b in enumerate(ms):
+            own = 0 if i == 1 else int(rng.integers(1, own_max))  # member 1 has nothing past the prefix
+            lens[b] = pp * ps + own
+            tables[b] = shared + [next(next_page) for _ in range(math.ceil(own / ps))]
+    for b in order[pos:]:
+        lens[b] = int(rng.integers(1, 3000))
+        tables[b] = [next(next_page) for _ in range(math.ceil(lens[b] / ps))]
+    P = 20000
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(P, ps, Hkv, 128, generator=g).to(dtype)
+    v = torch.randn(P, ps, Hkv, 128, generator=g).to(dtype)
+    q = torch.randn(B, Hq, 128, generator=g).to(dtype)
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV),
+            torch.from_numpy(lpl).to(DEV), int(indptr[-1]))
+    groups = K.DecodeGroups(B, members, prefix_pages, DEV)
+    out_g = K.paged_decode(*args, groups=groups)
+    out_p = K.paged_decode(*args)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref([q[b:b + 1] for b in range(B)], k.view(-1, Hkv, 128), v.view(-1, Hkv, 128), ps,
+                                indptr, indices, lpl, [1] * B)
+    ref = torch.stack([r[0] for r in ref])
+    return out_g.cpu().float(), out_p.cpu().float(), ref
+
+
+@pytest.mark.parametrize("Hq,Hkv,ps,dtype,sizes,prefix", [
+    (32, 8, 16, torch.float16, [4, 4, 3], [127, 10, 1]),
+    (8, 8, 16, torch.float16, [16, 2], [40, 3]),
+    (64, 8, 16, torch.bfloat16, [2, 2], [64, 5]),
+    (32, 8, 8, torch.float16, [4, 2], [50, 7]),
+    (16, 1, 16, torch.float16, [1, 1], [20, 2]),
+])
+def test_decode_grouped_prefix(Hq, Hkv, ps, dtype, sizes, prefix):
+    """Groups of sequences sharing their first pages: the grouped decode (prefix read
+    once per group, members in the MFMA columns) against the oracle, and against the
+    plain decode of the same batch; a member with no token past the prefix included."""
+    _log(f"decode grouped Hq={Hq} Hkv={Hkv} ps={ps} {dtype} groups={sizes} prefix={prefix}")
+    out_g, out_p, ref = _grouped_case(Hq, Hkv, ps, dtype, 7 + Hq + ps, sizes, prefix, n_alone=5)
+    torch.testing.assert_close(out_g, ref, atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(out_p, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_decode_grouped_rejects_bad_groups():
+    K = _k()
+    lib = __import__("nanoslg_amd._lib", fromlist=["load"]).load()
+    import ctypes
+    B, Hq, Hkv, D, ps = 6, 32, 8, 128, 16
+    q = torch.zeros(B, Hq, D, dtype=torch.float16, device=DEV)
+    pool = torch.zeros(8, ps, Hkv, D, dtype=torch.float16, device=DEV)
+    ip = torch.arange(B + 1, dtype=torch.int32, device=DEV)
+    ix = torch.ones(B, dtype=torch.int32, device=DEV)
+    lp = torch.full((B,), ps, dtype=torch.int32, device=DEV)
+    slot = torch.full((B,), -1, dtype=torch.int32, device=DEV)
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
+
+    def call(num_groups, prefix, members):
+        pp = (ctypes.c_int32 * max(1, len(prefix)))(*prefix)
+        mm = (ctypes.c_int32 * (16 * max(1, num_groups)))(*([-1] * 16 * max(1, num_groups)))
+        for i, x in enumerate(members):
+            mm[i] = x
+        return lib.nslg_paged_decode_grouped(q.data_ptr(), Hq * D, pool.data_ptr(), pool.data_ptr(), 8, ps,
+                                             ip.data_ptr(), ix.data_ptr(), lp.data_ptr(), B, B, Hq, Hkv, D, 0.1, 0,
+                                             slot.data_ptr(), num_groups, pp, mm, q.data_ptr(), Hq * D,
+                                             ws.data_ptr(), ws.numel(), None)
+    assert call(0, [], []) == -2               # no group
+    assert call(33, [1] * 33, [0]) == -2       # too many groups
+    assert call(1, [0], [0, 1]) == -1          # empty prefix
+    assert call(1, [1], [0, 1, 2, 3, 4]) == -1  # 5 members > 16 / G = 4
+    assert call(1, [1], [0, 0]) == -1          # a sequence twice
+    assert call(1, [1], [-1, 2]) == -1         # members not listed first
+    assert call(1, [1], [0, 9]) == -1          # not a batch row
+    assert call(2, [1, 1], [0, 1] + [-1] * 14 + [1]) == -1  # a sequence in two groups
+    torch.cuda.synchronize()
