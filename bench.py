@@ -187,19 +187,20 @@ class EventTimedKernels:
         return getattr(self._k, name)
 
     def DecodeLaunch(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
-                     num_qo_heads, workspace=None, sm_scale=None):
+                     num_qo_heads, workspace=None, sm_scale=None, groups=None):
         """The per-forward launcher; while recording, each layer runs as append_kv and
         then an event-timed paged_decode (the same launches, the same results)."""
         real = self._k.DecodeLaunch(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len,
-                                    total_pages, num_qo_heads, workspace=workspace, sm_scale=sm_scale)
+                                    total_pages, num_qo_heads, workspace=workspace, sm_scale=sm_scale,
+                                    groups=groups)
         timed = self
 
-        def launch(layer, q, k_new, v_new):
-            if not timed.recording:
-                return real(layer, q, k_new, v_new)
+        def launch(layer, q, k_new, v_new, rope=None):
+            if not timed.recording or rope is not None:
+                return real(layer, q, k_new, v_new, rope=rope)
             timed._k.append_kv(k_new, v_new, slot_mapping, k_pool[layer], v_pool[layer])
             return timed.paged_decode(q, k_pool[layer], v_pool[layer], kv_indptr, kv_indices, kv_last_page_len,
-                                      total_pages, sm_scale=sm_scale, workspace=workspace)
+                                      total_pages, sm_scale=sm_scale, workspace=workspace, groups=groups)
         return launch
 
     def paged_decode(self, *args, **kw):
@@ -539,6 +540,25 @@ def run_radix(args):
     value = nbytes / wall / 1e9
     _log(f"suffix prefill + {cow} copy-on-writes: {suffix_ms:.2f} ms; decode {wall / steps * 1e3:.3f} ms/step, "
          f"{value:.1f} GB/s distinct, {eff / wall / 1e9:.1f} GB/s effective; decode call {mean_ms * 1e3:.1f} us")
+    # The decode call of one steady step with and without the prefix groups (the
+    # shared prefix read once per group of 4, or once per request), kernel time only:
+    # 10 calls captured in a HIP graph, replayed with events around the replays.
+    c = mgr.begin_forward(ids, [1] * B)
+    plan = c.plan
+    kl, vl = mgr.pool.k[0], mgr.pool.v[0]
+    qs = qd[0][:, 0]
+    ab = {}
+    for label, grp in (("grouped", plan.groups), ("per_request", None)):
+        if label == "grouped" and grp is None:
+            continue
+        out = torch.empty(B, HQ, D, dtype=torch.float16, device=dev)
+        ab[label] = _graph_time_us(torch, dev, lambda: kernels.paged_decode(
+            qs, kl, vl, plan.indptr, plan.indices, plan.lpl, plan.total_pages, out=out,
+            workspace=mgr.workspace, groups=grp))
+    ngroups = plan.groups.num_groups if plan.groups is not None else 0
+    _log(f"decode call, kernel time: {ab} ({ngroups} prefix groups)")
+    long_ab = _grouped_decode_ab(kernels, dev, B=16, prefix=16384, seed=args.seed)
+    _log(f"same with a 16384-token shared prefix: {long_ab}")
     return {
         "metric": "paged decode attn+append with a shared radix prefix: HBM GB/s (distinct pages) and tok/s/layer",
         "value": round(value, 2),
@@ -558,6 +578,9 @@ def run_radix(args):
         "decode_tok_s_layer": round(B * steps / wall, 1),
         "suffix_prefill_ms": round(suffix_ms, 3),
         "copy_on_write_pages": cow,
+        "prefix_groups": ngroups,
+        "decode_call_kernel_us": ab,
+        "decode_call_kernel_us_prefix16384": long_ab,
         "roofline": {
             "bound": "hbm",
             "kernel": "nslg_paged_decode (split-K decode kernel + LSE merge kernel)",
@@ -571,6 +594,72 @@ def run_radix(args):
             "algorithmic_bytes_per_launch": int(kbytes),
         },
     }
+
+
+def _graph_time_us(torch, dev, call, n=10, reps=20):
+    """Kernel time per call: n calls captured in a HIP graph, replayed `reps` times
+    with events around the replays (no host overhead in the figure)."""
+    call()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        call()
+        torch.cuda.current_stream(dev).synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(n):
+                call()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return round(e0.elapsed_time(e1) / (n * reps) * 1e3, 2)
+
+
+def _grouped_decode_ab(kernels, dev, B, prefix, seed):
+    """Decode of B requests sharing a `prefix`-token prefix (own suffixes U[128,1024]),
+    with the prefix grouped (read once per group of 4) and per request: kernel time
+    of each, straight on the kernels with a block table built here."""
+    import torch
+    rng = np.random.default_rng(seed + 1)
+    pp = prefix // PS
+    suf = rng.integers(128, 1025, size=B)
+    lens = [prefix + int(x) for x in suf]
+    own = [math.ceil(int(x) / PS) for x in suf]
+    P = pp + sum(own) + 8
+    perm = rng.permutation(np.arange(1, P)).tolist()
+    shared, off, tables = perm[:pp], pp, []
+    for n in own:
+        tables.append(shared + perm[off:off + n])
+        off += n
+    indptr = np.zeros(B + 1, np.int32)
+    np.cumsum([len(t) for t in tables], out=indptr[1:])
+    indices = np.concatenate(tables).astype(np.int32)
+    lpl = np.array([L - (len(t) - 1) * PS for L, t in zip(lens, tables)], np.int32)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn(P, PS, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn(P, PS, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn(B, HQ, D, generator=g, device=dev, dtype=torch.float16)
+    ip, ix, lp = (torch.from_numpy(a).to(dev) for a in (indptr, indices, lpl))
+    M = 16 // (HQ // HKV)
+    groups = kernels.DecodeGroups(B, [list(range(i, min(B, i + M))) for i in range(0, B, M)],
+                                  [pp] * ((B + M - 1) // M), dev)
+    ws = kernels.Workspace(dev)
+    out = torch.empty(B, HQ, D, dtype=torch.float16, device=dev)
+    res = {}
+    for label, grp in (("grouped", groups), ("per_request", None)):
+        res[label] = _graph_time_us(torch, dev, lambda: kernels.paged_decode(
+            q, k, v, ip, ix, lp, int(indptr[-1]), out=out, workspace=ws, groups=grp))
+    distinct = (pp + sum(own)) * PS * HKV * D * 2 * 2
+    res["distinct_GB_s_grouped"] = round(distinct / (res["grouped"] * 1e-6) / 1e9, 1)
+    return res
 
 
 PREFILL_B, PREFILL_LEN, PREFILL_CHUNK = 8, 4096, 512

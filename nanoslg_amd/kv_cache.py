@@ -311,12 +311,16 @@ class _ForwardPlan:
     """Device-side metadata of one forward, shared by every layer's attend()."""
 
     def __init__(self, device, batch, iw, slot_grid, positions, indptr, indices, lpl, qo_indptr,
-                 q_rows, cow_src, cow_dst, zero_ids=None):
+                 q_rows, cow_src, cow_dst, zero_ids=None, group_slot=None):
         zero_ids = np.zeros(0, np.int32) if zero_ids is None else np.asarray(zero_ids, np.int32)
+        parts = [slot_grid, positions, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst, zero_ids]
+        if group_slot is not None:
+            parts.append(group_slot)
+        up = _upload_i32(parts, device)
         (self.slot, self.pos_i32, self.indptr, self.indices, self.lpl, self.qo_indptr, self.q_rows,
-         self.cow_src, self.cow_dst, self.zero_ids) = _upload_i32(
-            [slot_grid, positions, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst, zero_ids],
-            device)
+         self.cow_src, self.cow_dst, self.zero_ids) = up[:10]
+        self.group_slot = up[10] if group_slot is not None else None
+        self.groups = None  # kernels.DecodeGroups of a decode batch with shared prefixes
         self.batch, self.iw = batch, iw
         self.total_pages = int(indptr[-1]) if len(indptr) else 0
         self.total_q = int(qo_indptr[-1]) if len(qo_indptr) else 0
@@ -324,9 +328,14 @@ class _ForwardPlan:
         self._pos_long: Optional[torch.Tensor] = None
 
     @classmethod
-    def from_device(cls, batch, slot, pos, indptr, indices, lpl, qo_indptr, q_rows, zero_ids, total_pages):
-        """A decode plan whose tables were built on the device (decode_plan_step)."""
+    def from_device(cls, batch, slot, pos, indptr, indices, lpl, qo_indptr, q_rows, zero_ids, total_pages,
+                    groups=None):
+        """A decode plan whose tables were built on the device (decode_plan_step); the
+        prefix groups carry over from the previous step (shared pages are never
+        written, so a group's prefix does not change while the batch stays)."""
         self = cls.__new__(cls)
+        self.groups = groups
+        self.group_slot = groups.seq_group_slot if groups is not None else None
         self.slot, self.pos_i32, self.indptr, self.indices, self.lpl = slot, pos, indptr, indices, lpl
         self.qo_indptr, self.q_rows = qo_indptr, q_rows
         self.cow_src = self.cow_dst = slot[:0]
@@ -703,6 +712,7 @@ class PagedCacheContext(CacheContext):
                 self._plan = plan
                 cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
                 return
+        groups = None
         if self._is_decode and iw == 1:
             # One token per sequence, vectorised over the batch. The page written by
             # sequence b is the last page of its CSR segment; only a page that is shared
@@ -737,6 +747,7 @@ class PagedCacheContext(CacheContext):
             pos = start.astype(np.int32)
             q_rows = np.arange(B, dtype=np.int64)
             qo = np.arange(B + 1, dtype=np.int64)
+            groups = cache._prefix_groups(states, npg)
         else:
             ncnt = np.fromiter(self.new_token_counts, np.int64, B)
             start = np.fromiter(self.start_positions, np.int64, B)
@@ -793,9 +804,13 @@ class PagedCacheContext(CacheContext):
         self._max_q = max(self.new_token_counts) if B else 0
         self._uniform_rows = int(qo[-1]) == B * iw  # every grid row carries a new token
 
+        group_spec = groups
         self._plan = _ForwardPlan(pool.device, B, iw, slot.reshape(-1), pos, indptr, indices, lpl, qo,
                                   q_rows, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32),
-                                  zero_pages)
+                                  zero_pages, group_slot=group_spec[2] if group_spec else None)
+        if group_spec:
+            self._plan.groups = cache.kernels.DecodeGroups(B, group_spec[0], group_spec[1], pool.device,
+                                                           seq_group_slot=self._plan.group_slot)
         if zero_pages:  # zero-on-alloc of the pages this forward's extensions took
             cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
@@ -834,7 +849,7 @@ class PagedCacheContext(CacheContext):
             if launch is None:
                 launch = self._decode_launch = kern.DecodeLaunch(
                     pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                    q.shape[2], workspace=cache.workspace)
+                    q.shape[2], workspace=cache.workspace, groups=plan.groups)
             return launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
@@ -858,7 +873,7 @@ class PagedCacheContext(CacheContext):
             if launch is None:
                 launch = self._decode_launch = kern.DecodeLaunch(
                     pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                    q.shape[2], workspace=cache.workspace)
+                    q.shape[2], workspace=cache.workspace, groups=plan.groups)
             return launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, pos)).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
@@ -906,6 +921,56 @@ class PagedKVCache(KVCacheManager):
     def _record_decode_plan(self, seq_ids, plan, seq_lens) -> None:
         self._dev_plan = (tuple(seq_ids), plan, np.asarray(seq_lens, np.int64))
 
+    MIN_GROUP_PAGES = 4
+
+    def _prefix_groups(self, states, npg):
+        """Rows of a decode batch whose first pages are the same pages (a shared radix
+        prefix): groups of 2 .. 16/G rows, each with the number of full pages all its
+        rows share below their last page (at least MIN_GROUP_PAGES), at most 32
+        groups. Returns (groups, prefix_pages, seq_group_slot) or None; the decode
+        then reads each group's shared pages once for all its rows."""
+        B = len(states)
+        if B < 2 or getattr(self.kernels, "DecodeGroups", None) is None:
+            return None
+        cfg = self.cfg
+        M = 16 // max(1, cfg.num_qo_heads // cfg.num_kv_heads)
+        if M < 2:
+            return None
+        first = np.fromiter((int(st.bt[0]) if st.n_pages else 0 for st in states), np.int64, B)
+        cand = np.nonzero((first > 0) & (self.pool.ref_count[first] > 1))[0]
+        if cand.size < 2:
+            return None
+        cand = cand[np.argsort(first[cand], kind="stable")]
+        keys = first[cand]
+        cuts = np.flatnonzero(np.diff(keys)) + 1
+        groups, prefixes = [], []
+        for run in np.split(cand, cuts):
+            run = run.tolist()
+            for s0 in range(0, len(run), M):
+                sub = run[s0:s0 + M]
+                if len(sub) < 2:
+                    continue
+                cap = min(int(npg[b]) - 1 for b in sub)  # full pages below each row's last page
+                if cap < self.MIN_GROUP_PAGES:
+                    continue
+                tabs = np.stack([states[b].bt[:cap] for b in sub])
+                same = (tabs == tabs[0]).all(axis=0)
+                common = cap if bool(same.all()) else int(np.argmin(same))
+                if common >= self.MIN_GROUP_PAGES:
+                    groups.append(sub)
+                    prefixes.append(common)
+                if len(groups) == 32:
+                    break
+            if len(groups) == 32:
+                break
+        if not groups:
+            return None
+        slot = np.full(B, -1, np.int32)
+        for g, sub in enumerate(groups):
+            for m, b in enumerate(sub):
+                slot[b] = 16 * g + m
+        return groups, prefixes, slot
+
     def _advance_decode_plan(self, seq_ids, states, zero_pages) -> Optional[_ForwardPlan]:
         """This decode forward's plan built on the device from the previous one
         (kernels.decode_plan_step), when the batch is the one the previous decode
@@ -943,7 +1008,7 @@ class PagedKVCache(KVCacheManager):
             qo, qr = _upload_i32([np.arange(B + 1, dtype=np.int32), np.arange(B, dtype=np.int32)], pool.device)
             rows = self._decode_rows[B] = (qo, qr)
         return _ForwardPlan.from_device(B, slot, pos, indptr, indices, lpl, rows[0], rows[1], new,
-                                        plan.total_pages + n_new)
+                                        plan.total_pages + n_new, groups=plan.groups)
 
     def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
         """kv_cache.py:707-722: radix match (full pages), pin, allocate the rest."""

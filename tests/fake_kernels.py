@@ -68,7 +68,7 @@ def _attend(q_list, qo_lens, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
 
 
 def paged_decode(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
-                 sm_scale=None, out=None, workspace=None):
+                 sm_scale=None, out=None, workspace=None, groups=None):
     CALLS.append(("paged_decode", int(q.shape[0])))
     B = q.shape[0]
     outs = _attend([q[b:b + 1] for b in range(B)], [1] * B, k_layer, v_layer, kv_indptr, kv_indices,
@@ -100,7 +100,8 @@ class DecodeLaunch:
     functions above."""
 
     def __init__(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
-                 num_qo_heads, workspace=None, sm_scale=None):
+                 num_qo_heads, workspace=None, sm_scale=None, groups=None):
+        CALLS.append(("DecodeLaunch", groups))
         self.k_pool, self.v_pool = k_pool, v_pool
         self.args = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages)
         self.sm_scale = sm_scale
@@ -161,3 +162,13 @@ def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_siz
         v_pool[:, ids] = 0
     t = lambda x: torch.tensor(x, dtype=torch.int32)  # noqa: E731
     return t(out_ip), t(out_idx), t(out_lpl), t(slots), t(pos), t(new)
+
+
+class DecodeGroups:
+    """As nanoslg_amd.kernels.DecodeGroups (the grouping does not change results)."""
+
+    def __init__(self, batch, members, prefix_pages, device, seq_group_slot=None):
+        self.num_groups = len(members)
+        self.members = [list(map(int, m)) for m in members]
+        self.prefix_pages = list(map(int, prefix_pages))
+        self.seq_group_slot = seq_group_slot

@@ -446,3 +446,40 @@ def test_attend_rope_equals_attend_on_rotated_inputs(backend):
         short = O.rope_tables(D, 8, 10000.0)
         c = a.begin_forward(ids, [1, 1, 1])
         KC.attention_forward(q[:, :1], k[:, :1], v[:, :1], 0, HQ, HKV, short[0], short[1], c)
+
+
+def test_decode_batch_with_shared_prefix_forms_groups():
+    """A decode batch of requests admitted on one cached prompt: their first pages are
+    the same pages, so the plan groups them (at most 16 / G rows per group, with the
+    full pages they share below their last page) and the decode gets the groups; the
+    steady steps planned on the device keep them. Outputs equal the oracle's."""
+    g = torch.Generator().manual_seed(8)
+    mgr, ref = make(ps=4, pages=160, prefix=True)
+    prompt = list(range(1, 30))  # 7 full pages + 1 token
+    for impl in (mgr, ref):
+        impl.allocate_sequence("p", token_ids=prompt)
+    forward_both(mgr, ref, ["p"], [len(prompt)], [0], g)
+    for impl in (mgr, ref):
+        impl.release_sequence("p")
+    ids = [f"r{i}" for i in range(10)]
+    for i, sid in enumerate(ids):
+        toks = prompt[:28] + [100 + i] * (3 + i)
+        for impl in (mgr, ref):
+            assert impl.allocate_sequence(sid, token_ids=toks) == 28
+    forward_both(mgr, ref, ids, [3 + i for i in range(10)], [0] * 10, g)
+    seen = []
+    for _ in range(6):
+        FK.CALLS.clear()
+        forward_both(mgr, ref, ids, [1] * 10, [0] * 10, g)
+        launches = [grp for name, grp in FK.CALLS if name == "DecodeLaunch"]
+        assert launches and launches[0] is not None
+        seen.append(launches[0])
+    grp = seen[0]
+    M = 16 // (HQ // HKV)
+    assert sorted(b for ms in grp.members for b in ms) == list(range(10))
+    assert all(2 <= len(ms) <= M for ms in grp.members)
+    assert grp.prefix_pages == [7] * grp.num_groups
+    for ms in grp.members:  # the rows of a group share their first 7 pages
+        tabs = [mgr.seqs[ids[b]].bt[:7].tolist() for b in ms]
+        assert all(t == tabs[0] for t in tabs)
+    assert all(s is grp for s in seen[1:])  # carried over by the device-planned steps
