@@ -23,7 +23,13 @@ def dtype_code(dt: torch.dtype) -> int:
         raise TypeError(f"unsupported KV dtype {dt}") from None
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The current HIP stream of t's device, as an integer handle."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -331,24 +337,32 @@ def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_
     new_page = np.ascontiguousarray(new_page, dtype=np.int32)
     if new_page.shape != (B,):
         raise ValueError(f"decode_plan_step: new_page must have {B} entries")
-    total_in = kv_indices.numel()
-    cap = total_in + num_new
-    buf = torch.empty(B + 1 + cap + 3 * B + max(num_new, 1), dtype=torch.int32, device=kv_indptr.device)
-    o = [0, B + 1, B + 1 + cap, 2 * B + 1 + cap, 3 * B + 1 + cap, 4 * B + 1 + cap]
-    indptr, indices, lpl = buf[o[0]:o[1]], buf[o[1]:o[2]], buf[o[2]:o[3]]
-    slot, pos, new = buf[o[3]:o[4]], buf[o[4]:o[5]], buf[o[5]:o[5] + num_new]
+    pool_args = (None, None, 0, 0, 0, 0, 0)
     if k_pool is not None:
         _require_gpu(k_pool, v_pool)
         L, P, ps_, Hkv, D = _pool_geom(k_pool, v_pool)
         if ps_ != page_size:
             raise ValueError("decode_plan_step: pool page size differs")
         pool_args = (k_pool.data_ptr(), v_pool.data_ptr(), L, P, Hkv, D, dtype_code(k_pool.dtype))
-    else:
-        pool_args = (None, None, 0, 0, 0, 0, 0)
+    return _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args)
+
+
+def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args):
+    """decode_plan_step without the argument checks, for callers whose inputs are the
+    previous plan's outputs (the cache manager). new_page: contiguous int32 numpy;
+    pool_args: (k_pool ptr, v_pool ptr, L, P, Hkv, D, dtype code) or all-null."""
+    B = kv_indptr.numel() - 1
+    cap = kv_indices.numel() + num_new
+    sizes = [B + 1, cap, B, B, B, num_new]
+    buf = torch.empty(sum(sizes) + 1, dtype=torch.int32, device=kv_indptr.device)
+    indptr, indices, lpl, slot, pos, new, _ = buf.split(sizes + [1])
+    base = buf.data_ptr()
+    o = [0]
+    for n in sizes:
+        o.append(o[-1] + 4 * n)  # byte offsets (an empty part still gets a real address)
     rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
-                                          B, int(page_size), new_page.ctypes.data, indptr.data_ptr(),
-                                          indices.data_ptr(), lpl.data_ptr(), slot.data_ptr(), pos.data_ptr(),
-                                          buf[o[5]:].data_ptr(), *pool_args, _stream(kv_indptr))
+                                          B, int(page_size), new_page.ctypes.data, base, base + o[1], base + o[2],
+                                          base + o[3], base + o[4], base + o[5], *pool_args, _stream(kv_indptr))
     _lib.check(rc, "nslg_decode_plan_step")
     return indptr, indices, lpl, slot, pos, new
 
@@ -358,50 +372,79 @@ class DecodeLaunch:
 
     What is the same for all layers of the forward (pools, block table, slot
     mapping, sizes, the workspace and its size) is checked and computed once, here;
-    each call checks that layer's tensors and issues nslg_append_kv then
-    nslg_paged_decode on the current stream. Same results as append_kv followed by
-    paged_decode on the layer's pool slices."""
+    each call checks that layer's tensors and issues nslg_append_kv (or
+    nslg_rope_append) then the decode on the current stream. Same results as
+    append_kv followed by paged_decode on the layer's pool slices.
+
+    A launcher can be re-bound to the next forward's plan (rebind) when the pools,
+    batch size and head count stay: the pool geometry is then not checked again."""
 
     def __init__(self, k_pool: torch.Tensor, v_pool: torch.Tensor, slot_mapping: torch.Tensor,
                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                  total_pages: int, num_qo_heads: int, workspace: Optional[Workspace] = None,
                  sm_scale: Optional[float] = None, groups: Optional[DecodeGroups] = None):
-        _require_gpu(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
-        for t, n in ((slot_mapping, "slot_mapping"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
-                     (kv_last_page_len, "kv_last_page_len")):
-            _i32(t, n)
+        _require_gpu(k_pool, v_pool)
         L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
-        B = kv_indptr.numel() - 1
-        if slot_mapping.numel() != B or kv_last_page_len.numel() < B:
-            raise ValueError("DecodeLaunch: one slot and one last-page length per sequence")
         if num_qo_heads % Hkv:
             raise ValueError(f"DecodeLaunch: Hq={num_qo_heads} is not a multiple of Hkv={Hkv}")
         self.lib = _lib.load()
         self.device, self.dtype = k_pool.device, k_pool.dtype
+        self.dev_index = k_pool.get_device()
         self.code = dtype_code(k_pool.dtype)
-        self.L, self.P, self.ps, self.Hkv, self.D, self.B, self.Hq = L, P, ps, Hkv, D, B, num_qo_heads
+        self.L, self.P, self.ps, self.Hkv, self.D, self.Hq = L, P, ps, Hkv, D, num_qo_heads
         self.layer_bytes = P * ps * Hkv * D * k_pool.element_size()
         self.kp0, self.vp0 = k_pool.data_ptr(), v_pool.data_ptr()
-        self.keep = (k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
+        self.pools = (k_pool, v_pool)
+        self.workspace = workspace or Workspace(self.device)
+        self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+        self.B = kv_indptr.numel() - 1
+        self.rebind(slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups, check=True)
+
+    def rebind(self, slot_mapping: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+               kv_last_page_len: torch.Tensor, total_pages: int, groups: Optional[DecodeGroups] = None,
+               check: bool = True) -> "DecodeLaunch":
+        """Point the launcher at another forward's plan of the same batch size."""
+        B = self.B
+        if check:
+            _require_gpu(self.pools[0], slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
+            for t, n in ((slot_mapping, "slot_mapping"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                         (kv_last_page_len, "kv_last_page_len")):
+                _i32(t, n)
+            if kv_indptr.numel() != B + 1 or slot_mapping.numel() != B or kv_last_page_len.numel() < B:
+                raise ValueError(f"DecodeLaunch: a plan of {B} sequences: one slot and one last-page length each")
+        self.keep = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
         self.slots, self.indptr, self.indices, self.lpl = (slot_mapping.data_ptr(), kv_indptr.data_ptr(),
                                                            kv_indices.data_ptr(), kv_last_page_len.data_ptr())
         self.total_pages = int(total_pages)
         self.groups = groups
+        lib = self.lib
         if groups is None:
-            need = int(self.lib.nslg_paged_decode_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages, ps,
-                                                                 self.code))
+            need = int(lib.nslg_paged_decode_workspace_size(B, self.Hq, self.Hkv, self.D, self.total_pages,
+                                                            self.ps, self.code))
         else:
-            _require_gpu(k_pool, groups.seq_group_slot)
-            _i32(groups.seq_group_slot, "seq_group_slot")
-            if groups.seq_group_slot.numel() != B:
-                raise ValueError("DecodeLaunch: one group slot per sequence")
-            need = int(self.lib.nslg_paged_decode_grouped_workspace_size(B, num_qo_heads, Hkv, D, self.total_pages,
-                                                                         ps, self.code, groups.num_groups))
+            if check:
+                _require_gpu(self.pools[0], groups.seq_group_slot)
+                _i32(groups.seq_group_slot, "seq_group_slot")
+                if groups.seq_group_slot.numel() != B:
+                    raise ValueError("DecodeLaunch: one group slot per sequence")
+            need = int(lib.nslg_paged_decode_grouped_workspace_size(B, self.Hq, self.Hkv, self.D, self.total_pages,
+                                                                    self.ps, self.code, groups.num_groups))
             if need == 0:
                 raise ValueError("DecodeLaunch: unsupported grouped decode shape")
             self.keep = self.keep + (groups.seq_group_slot,)
-        self.ws = (workspace or Workspace(self.device)).get(need)
-        self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+        self.ws = self.workspace.get(need)
+        return self
+
+    def _kv_rows(self, t: torch.Tensor, name: str) -> int:
+        """Row stride of k_new / v_new: [B, ..., Hkv, D] rows of one token each."""
+        sh = t.shape
+        if (len(sh) == 4 and sh[0] == self.B and sh[1] == 1 and sh[2] == self.Hkv and sh[3] == self.D
+                and t.stride(3) == 1 and t.stride(2) == self.D):
+            return t.stride(0)
+        n, stride, h = _rows(t, name)
+        if n != self.B or h != self.Hkv or sh[-1] != self.D:
+            raise ValueError(f"DecodeLaunch: {name} must hold {self.B} rows of [{self.Hkv}, {self.D}]")
+        return stride
 
     def __call__(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                  rope: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
@@ -411,17 +454,16 @@ class DecodeLaunch:
         nslg_append_kv)."""
         if not 0 <= layer < self.L:
             raise IndexError(f"layer {layer} out of range [0, {self.L})")
-        for t in (q, k_new, v_new):
-            if t.device != self.device or t.dtype != self.dtype:
-                raise ValueError(f"DecodeLaunch: tensors must be {self.dtype} on {self.device}")
+        dt, di = self.dtype, self.dev_index
+        if (q.dtype != dt or k_new.dtype != dt or v_new.dtype != dt or q.get_device() != di
+                or k_new.get_device() != di or v_new.get_device() != di):
+            raise ValueError(f"DecodeLaunch: tensors must be {self.dtype} on {self.device}")
         B, Hq, D = self.B, self.Hq, self.D
-        if tuple(q.shape) != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
+        if q.shape != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
             raise ValueError(f"DecodeLaunch: q must be [{B}, {Hq}, {D}] with a contiguous [Hq, D] block")
-        nk, ks, hk = _rows(k_new, "k_new")
-        nv, vs, hv = _rows(v_new, "v_new")
-        if nk != B or nv != B or hk != self.Hkv or hv != self.Hkv or k_new.shape[-1] != D or v_new.shape[-1] != D:
-            raise ValueError(f"DecodeLaunch: k_new/v_new must hold {B} rows of [{self.Hkv}, {D}]")
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        ks = self._kv_rows(k_new, "k_new")
+        vs = self._kv_rows(v_new, "v_new")
+        stream = _RAW_STREAM(di) if _RAW_STREAM is not None else torch.cuda.current_stream(self.device).cuda_stream
         off = layer * self.layer_bytes
         kp, vp = self.kp0 + off, self.vp0 + off
         lib = self.lib
@@ -432,10 +474,10 @@ class DecodeLaunch:
             q_ptr, q_stride = q.data_ptr(), q.stride(0)
         else:
             cos, sin, pos = rope
-            if pos.device != self.device or pos.dtype != torch.int32 or pos.numel() != B or not pos.is_contiguous():
+            if pos.get_device() != di or pos.dtype != torch.int32 or pos.numel() != B or not pos.is_contiguous():
                 raise ValueError(f"DecodeLaunch: positions must be {B} contiguous int32 on {self.device}")
             cos, sin = _rope_tables(cos, sin, D)
-            if cos.device != self.device:
+            if cos.get_device() != di:
                 raise ValueError(f"DecodeLaunch: rope tables must be on {self.device}")
             q_rot = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
             rc = lib.nslg_rope_append(q.data_ptr(), q.stride(0), q_rot.data_ptr(), Hq * D, k_new.data_ptr(), ks,

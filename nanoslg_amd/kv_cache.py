@@ -846,10 +846,8 @@ class PagedCacheContext(CacheContext):
         B, S = q.shape[0], q.shape[1]
         if self._is_decode and S == 1:
             launch = self._decode_launch
-            if launch is None:
-                launch = self._decode_launch = kern.DecodeLaunch(
-                    pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                    q.shape[2], workspace=cache.workspace, groups=plan.groups)
+            if launch is None or launch.bound_plan is not plan:
+                launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
@@ -870,10 +868,8 @@ class PagedCacheContext(CacheContext):
         pos = plan.pos_for(S)
         if self._is_decode and S == 1:
             launch = self._decode_launch
-            if launch is None:
-                launch = self._decode_launch = kern.DecodeLaunch(
-                    pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages,
-                    q.shape[2], workspace=cache.workspace, groups=plan.groups)
+            if launch is None or launch.bound_plan is not plan:
+                launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, pos)).reshape(B, 1, -1)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
@@ -915,11 +911,32 @@ class PagedKVCache(KVCacheManager):
         self.workspace = self.kernels.Workspace(self.pool.device, 128 << 20)
         self._pending_zero: List[int] = []
         self._dev_plan = None  # the last decode forward's plan: (ids, plan, lens), see below
+        self._launcher = None  # the last decode forward's kernels.DecodeLaunch
+        self._pool_args = None  # the pools as the device planner takes them
         self._decode_rows: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
 
     # ---- decode plans built on the device ---------------------------------------------
     def _record_decode_plan(self, seq_ids, plan, seq_lens) -> None:
         self._dev_plan = (tuple(seq_ids), plan, np.asarray(seq_lens, np.int64))
+
+    def _decode_launcher(self, plan: "_ForwardPlan", num_qo_heads: int):
+        """The decode launcher of a forward: the previous forward's, re-bound to this
+        plan, when the batch size and head count are the same (kernels.DecodeLaunch
+        checks the pool geometry once)."""
+        kern = self.kernels
+        prev = self._launcher
+        if (prev is not None and hasattr(prev, "rebind") and prev.B == plan.batch and prev.Hq == num_qo_heads
+                and prev.workspace is self.workspace):
+            prev.rebind(plan.slot, plan.indptr, plan.indices, plan.lpl, plan.total_pages, plan.groups,
+                        check=False)
+            prev.bound_plan = plan
+            return prev
+        pool = self.pool
+        launch = kern.DecodeLaunch(pool.k, pool.v, plan.slot, plan.indptr, plan.indices, plan.lpl,
+                                   plan.total_pages, num_qo_heads, workspace=self.workspace, groups=plan.groups)
+        launch.bound_plan = plan
+        self._launcher = launch
+        return launch
 
     MIN_GROUP_PAGES = 4
 
@@ -1001,8 +1018,16 @@ class PagedKVCache(KVCacheManager):
         sl = start % ps
         pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
         plan = prev[1]
-        indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
-                                                                    new_page, ps, n_new, pool.k, pool.v)
+        fast = getattr(kern, "_decode_plan_step", None)
+        if fast is not None:  # inputs are the previous plan's outputs: no argument checks
+            if self._pool_args is None:
+                L, P, _, Hkv, D = pool.k.shape
+                self._pool_args = (pool.k.data_ptr(), pool.v.data_ptr(), L, P, Hkv, D, kern.dtype_code(pool.k.dtype))
+            indptr, indices, lpl, slot, pos, new = fast(plan.indptr, plan.indices, plan.lpl, new_page, ps, n_new,
+                                                        self._pool_args)
+        else:
+            indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
+                                                                        new_page, ps, n_new, pool.k, pool.v)
         rows = self._decode_rows.get(B)
         if rows is None:
             qo, qr = _upload_i32([np.arange(B + 1, dtype=np.int32), np.arange(B, dtype=np.int32)], pool.device)
