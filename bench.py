@@ -188,20 +188,14 @@ class EventTimedKernels:
 
     def DecodeLaunch(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
                      num_qo_heads, workspace=None, sm_scale=None, groups=None):
-        """The per-forward launcher; while recording, each layer runs as append_kv and
-        then an event-timed paged_decode (the same launches, the same results)."""
+        """The per-forward launcher (re-bound from forward to forward as the product's
+        is); while recording, each layer runs as append_kv and then an event-timed
+        paged_decode (the same launches, the same results)."""
         real = self._k.DecodeLaunch(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len,
                                     total_pages, num_qo_heads, workspace=workspace, sm_scale=sm_scale,
                                     groups=groups)
-        timed = self
-
-        def launch(layer, q, k_new, v_new, rope=None):
-            if not timed.recording or rope is not None:
-                return real(layer, q, k_new, v_new, rope=rope)
-            timed._k.append_kv(k_new, v_new, slot_mapping, k_pool[layer], v_pool[layer])
-            return timed.paged_decode(q, k_pool[layer], v_pool[layer], kv_indptr, kv_indices, kv_last_page_len,
-                                      total_pages, sm_scale=sm_scale, workspace=workspace, groups=groups)
-        return launch
+        return _TimedLaunch(self, real, (k_pool, v_pool), sm_scale,
+                            (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups))
 
     def paged_decode(self, *args, **kw):
         if not self.recording:
@@ -232,6 +226,29 @@ class EventTimedKernels:
 
     def total_ms(self):
         return float(np.sum([a.elapsed_time(b) for a, b in self.events]))
+
+
+class _TimedLaunch:
+    """A kernels.DecodeLaunch whose decode calls are event-timed while recording."""
+
+    def __init__(self, timed, real, pools, sm_scale, plan):
+        self.timed, self.real, self.pools, self.sm_scale, self.plan = timed, real, pools, sm_scale, plan
+        self.B, self.Hq, self.workspace = real.B, real.Hq, real.workspace
+
+    def rebind(self, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups=None, check=True):
+        self.real.rebind(slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups, check=check)
+        self.plan = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups)
+        return self
+
+    def __call__(self, layer, q, k_new, v_new, rope=None):
+        timed = self.timed
+        if not timed.recording or rope is not None:
+            return self.real(layer, q, k_new, v_new, rope=rope)
+        slots, indptr, indices, lpl, total_pages, groups = self.plan
+        k_pool, v_pool = self.pools
+        timed._k.append_kv(k_new, v_new, slots, k_pool[layer], v_pool[layer])
+        return timed.paged_decode(q, k_pool[layer], v_pool[layer], indptr, indices, lpl, total_pages,
+                                  sm_scale=self.sm_scale, workspace=self.workspace, groups=groups)
 
 
 def copy_calibration():
@@ -349,7 +366,15 @@ def run_decode(args):
     torch.cuda.synchronize()
     lens_before = w.seq_lens()
     churn_at = args.steps // 2 if w.churn_frac > 0 else -1
+    # Every sequence gains one token per step and the churn re-admits sequences at
+    # their lengths, so the bytes of step i follow from the lengths before the loop;
+    # they are summed here, outside the timed region.
     nbytes = [0, 0, 0, 0]
+    for i in range(args.steps):
+        lens_i = [L + 1 + i for L in lens_before]
+        tp = sum(math.ceil(L / PS) for L in lens_i)
+        for j, x in enumerate(step_bytes(lens_i, w.B, tp)):
+            nbytes[j] += x
     kbytes = 0
     churn_s = 0.0
     t0 = time.perf_counter()
@@ -361,13 +386,10 @@ def run_decode(args):
             w.churn()
             torch.cuda.synchronize()
             churn_s = time.perf_counter() - c0
-        lens_i = [L + 1 for L in w.seq_lens()]
-        tp = sum(math.ceil(L / PS) for L in lens_i)
-        for j, x in enumerate(step_bytes(lens_i, w.B, tp)):
-            nbytes[j] += x
         w.step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0 - churn_s
+    assert w.seq_lens() == [L + args.steps for L in lens_before]
     ms_step = wall / args.steps * 1e3
     total_bytes = sum(nbytes)
     value = total_bytes / wall / 1e9
@@ -518,16 +540,19 @@ def run_radix(args):
     torch.cuda.synchronize()
     shared_bytes = full * PS * HKV * D * 2 * 2
     nbytes = eff = kbytes = 0
-    t0 = time.perf_counter()
-    for i in range(steps):
-        L = lens()
+    L0 = lens()
+    for i in range(steps):  # bytes of each step, from the lengths (one token per step)
+        L = [x + i for x in L0]
         tp = sum(math.ceil(x / PS) for x in L)
         kv, app, qo, csr = step_bytes(L, B, tp)
         nbytes += kv - (B - 1) * shared_bytes + app + qo + csr
         eff += kv + app + qo + csr
+    t0 = time.perf_counter()
+    for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    assert lens() == [x + steps for x in L0]
     timed.recording = True
     for i in range(steps):
         L = lens()
