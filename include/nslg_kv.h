@@ -246,6 +246,30 @@ int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
                           int32_t head_dim, int32_t dtype, nslg_stream_t stream);
 
 /*
+ * Device-side write plan of a multi-token forward: expands the forward's
+ * per-sequence tables into the per-token arrays the append and the prefill take.
+ * Replaces the per-token loop of FlashInferCacheContext.__init__ (slot of every new
+ * token, nanoslg/kv_cache.py:575-594, writes past the table to the null page's slot
+ * 0, :583-584), the positions of get_position_ids (:567-573, 635-637) and the ragged
+ * layout of _pack_q / qo_indptr (:622-632, 676-691).
+ *
+ *   kv_indptr/kv_indices   this forward's CSR block table (device; after copy-on-write)
+ *   start, new_tokens, input_offsets, pages_allocated   int32[batch] (device)
+ *   input_width            iw = max(input_offsets[b] + new_tokens[b])
+ *   slot_mapping_out, positions_out   int32[batch * iw]: grid row b*iw + off_b + t
+ *                          gets page*page_size+slot and start_b + t; other rows -1
+ *                          and 0
+ *   ragged_rows_out        int32[sum(new_tokens)]: grid row of ragged row qo_b + t
+ *   qo_indptr_out          int32[batch + 1]
+ * Bit-exact with the host plan.
+ */
+int nslg_forward_plan(const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* start,
+                      const int32_t* new_tokens, const int32_t* input_offsets,
+                      const int32_t* pages_allocated, int32_t batch, int32_t input_width,
+                      int32_t page_size, int32_t* slot_mapping_out, int32_t* positions_out,
+                      int32_t* ragged_rows_out, int32_t* qo_indptr_out, nslg_stream_t stream);
+
+/*
  * Fused rotary position embedding + K/V append. Replaces, per layer, the position
  * gather and the two apply_rotary_emb calls of _attention_forward
  * (nanoslg/models.py:96-103, apply_rotary_emb :69-83) together with the cache write

@@ -367,6 +367,41 @@ def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_si
     return indptr, indices, lpl, slot, pos, new
 
 
+def forward_plan(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, start: torch.Tensor, new_tokens: torch.Tensor,
+                 input_offsets: torch.Tensor, pages_allocated: torch.Tensor, input_width: int, page_size: int,
+                 total_tokens: int):
+    """Per-token write plan of a multi-token forward on the device (nslg_forward_plan).
+
+    All inputs int32 on the device ([B+1] CSR pointers, the CSR ids, four [B] per-sequence
+    arrays); total_tokens = sum(new_tokens). Returns (slot_mapping [B*iw],
+    positions [B*iw], ragged_rows [total_tokens], qo_indptr [B+1]), int32."""
+    _require_gpu(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (start, "start"),
+                 (new_tokens, "new_tokens"), (input_offsets, "input_offsets"), (pages_allocated, "pages_allocated")):
+        _i32(t, n)
+    B = kv_indptr.numel() - 1
+    for t in (start, new_tokens, input_offsets, pages_allocated):
+        if t.numel() != B:
+            raise ValueError(f"forward_plan: per-sequence arrays must have {B} entries")
+    return _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B,
+                         int(input_width), int(page_size), int(total_tokens))
+
+
+def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
+    """forward_plan without the argument checks (the cache manager's own tables)."""
+    sizes = [B * iw, B * iw, T, B + 1]
+    buf = torch.empty(sum(sizes) + 1, dtype=torch.int32, device=kv_indptr.device)
+    slot, pos, rows, qo, _ = buf.split(sizes + [1])
+    base = buf.data_ptr()
+    o1, o2 = 4 * B * iw, 8 * B * iw
+    o3 = o2 + 4 * T
+    rc = _lib.load().nslg_forward_plan(kv_indptr.data_ptr(), kv_indices.data_ptr(), start.data_ptr(),
+                                       new_tokens.data_ptr(), input_offsets.data_ptr(), pages_allocated.data_ptr(),
+                                       B, iw, page_size, base, base + o1, base + o2, base + o3, _stream(kv_indptr))
+    _lib.check(rc, "nslg_forward_plan")
+    return slot, pos, rows, qo
+
+
 class DecodeLaunch:
     """Append + split-K decode for every layer of one decode forward.
 

@@ -347,6 +347,23 @@ class _ForwardPlan:
         self._pos_long = None
         return self
 
+    @classmethod
+    def from_tensors(cls, batch, iw, slot, pos, indptr, indices, lpl, qo_indptr, q_rows, cow_src, cow_dst, zero_ids,
+                     total_pages, total_q):
+        """A plan whose per-token arrays were expanded on the device (forward_plan)."""
+        self = cls.__new__(cls)
+        self.slot, self.pos_i32, self.indptr, self.indices, self.lpl = slot, pos, indptr, indices, lpl
+        self.qo_indptr, self.q_rows = qo_indptr, q_rows
+        self.cow_src, self.cow_dst, self.zero_ids = cow_src, cow_dst, zero_ids
+        self.batch, self.iw = batch, iw
+        self.total_pages = int(total_pages)
+        self.total_q = int(total_q)
+        self._slot_by_S = {iw: slot}
+        self._pos_long = None
+        self.groups = None
+        self.group_slot = None
+        return self
+
     def slots_for(self, S: int) -> torch.Tensor:
         s = self._slot_by_S.get(S)
         if s is None:
@@ -770,11 +787,16 @@ class PagedCacheContext(CacheContext):
             indptr = np.zeros(B + 1, np.int64)
             np.cumsum(npg, out=indptr[1:])
             indices = self._csr_indices(states, npg)
+            T = int(ncnt.sum())
+            device_plan = T >= self.DEVICE_PLAN_TOKENS and hasattr(cache.kernels, "_forward_plan")
+            if device_plan:
+                # per-token slots, positions and the ragged layout are expanded on the
+                # device (kernels.forward_plan); here only tokens_used, per written page
+                self._pages_used(pool, states, start, ncnt, have, indices, indptr, ps)
             # per new token: absolute position, page, slot; past a sequence's pages the
             # write goes to the null page's slot 0 (kv_cache.py:583-584)
             slot = np.full(B * iw, -1, np.int32)
-            T = int(ncnt.sum())
-            if T:
+            if T and not device_plan:
                 rep = np.repeat(np.arange(B), ncnt)
                 first = np.zeros(B, np.int64)
                 np.cumsum(ncnt[:-1], out=first[1:])
@@ -797,6 +819,10 @@ class PagedCacheContext(CacheContext):
             lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
             if B == 0:
                 lpl = np.zeros(1, np.int64)
+            if device_plan:
+                self._plan_on_device(cache, B, iw, T, start, ncnt, have, indptr, indices, lpl, cow_src, cow_dst,
+                                     zero_pages)
+                return
             pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
         self.cow_pairs = list(zip(cow_src, cow_dst))
         if indices.size == 0:
@@ -817,6 +843,50 @@ class PagedCacheContext(CacheContext):
             cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
         if self._is_decode and iw == 1:
             cache._record_decode_plan(self.seq_ids, self._plan, self.seq_lens)
+
+    DEVICE_PLAN_TOKENS = 256  # forwards with at least this many new tokens expand their plan on the device
+
+    @staticmethod
+    def _pages_used(pool, states, start, ncnt, have, indices, indptr, ps) -> None:
+        """tokens_used of the pages this forward writes (kv_cache.py:593): each page
+        once, with its last slot written; per page rather than per token."""
+        n = np.maximum(ncnt, 0)
+        p0 = start // ps
+        plast = (start + n - 1) // ps
+        pend = np.minimum(plast, have - 1)  # pages past the allocated ones are not counted
+        cnt = np.where(n > 0, np.maximum(pend - p0 + 1, 0), 0)
+        tot = int(cnt.sum())
+        if not tot:
+            return
+        B = len(states)
+        rep = np.repeat(np.arange(B), cnt)
+        first = np.zeros(B, np.int64)
+        np.cumsum(cnt[:-1], out=first[1:])
+        pi = p0[rep] + (np.arange(tot, dtype=np.int64) - first[rep])
+        pid = indices[indptr[rep] + pi].astype(np.int64)
+        last = np.where(pi == plast[rep], (start + n - 1 - plast * ps)[rep], ps - 1)
+        pool.tokens_used[pid] = np.maximum(pool.tokens_used[pid], last + 1)
+
+    def _plan_on_device(self, cache, B, iw, T, start, ncnt, have, indptr, indices, lpl, cow_src, cow_dst,
+                        zero_pages) -> None:
+        """Upload the forward's small tables and expand the per-token plan on the device."""
+        pool = cache.pool
+        offs = np.fromiter(self.input_offsets, np.int64, B)
+        up = _upload_i32([indptr, indices, lpl, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32),
+                          np.asarray(zero_pages if zero_pages else [], np.int32), start, ncnt, offs, have],
+                         pool.device)
+        d_indptr, d_indices, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have = up
+        slot, pos, rows, qo = cache.kernels._forward_plan(d_indptr, d_indices, d_start, d_n, d_off, d_have, B, iw,
+                                                          cache.cfg.page_size, T)
+        self.cow_pairs = list(zip(cow_src, cow_dst))
+        self._max_q = max(self.new_token_counts) if B else 0
+        self._uniform_rows = T == B * iw
+        self._plan = _ForwardPlan.from_tensors(B, iw, slot, pos, d_indptr, d_indices, d_lpl, qo, rows, d_cs, d_cd,
+                                               d_zero, int(indptr[-1]), T)
+        if zero_pages:
+            cache.kernels.zero_pages(pool.k, pool.v, d_zero)
+        if cow_src:
+            cache.kernels.copy_pages(pool.k, pool.v, d_cs, d_cd)
 
     @staticmethod
     def _csr_indices(states, npg) -> np.ndarray:

@@ -172,3 +172,22 @@ class DecodeGroups:
         self.members = [list(map(int, m)) for m in members]
         self.prefix_pages = list(map(int, prefix_pages))
         self.seq_group_slot = seq_group_slot
+
+
+def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
+    """As nanoslg_amd.kernels._forward_plan, in plain Python on the CPU."""
+    CALLS.append(("forward_plan", T))
+    ip, idx = kv_indptr.tolist(), kv_indices.tolist()
+    st, n, off, have = start.tolist(), new_tokens.tolist(), input_offsets.tolist(), pages_allocated.tolist()
+    slot, pos, rows, qo = [-1] * (B * iw), [0] * (B * iw), [0] * T, [0]
+    for b in range(B):
+        for t in range(max(n[b], 0)):
+            ap = st[b] + t
+            pi = ap // page_size
+            r = b * iw + off[b] + t
+            slot[r] = idx[ip[b] + pi] * page_size + ap - pi * page_size if pi < have[b] else 0
+            pos[r] = ap
+            rows[qo[-1] + t] = r
+        qo.append(qo[-1] + max(n[b], 0))
+    t = lambda x: torch.tensor(x, dtype=torch.int32)  # noqa: E731
+    return t(slot), t(pos), t(rows), t(qo)

@@ -199,3 +199,51 @@ def test_factory_on_gpu():
     m = types.SimpleNamespace(kv_backend="auto", page_size=16)  # pages sized from free memory
     mgr = KC.create_cache_manager(hf, None, "cuda:0", torch.float16, m)
     assert 64 <= mgr.cfg.max_pages <= 65536
+
+
+def test_forward_plan_on_device_equals_host_plan(monkeypatch):
+    """Multi-token forwards (ragged, with input offsets, over shared prefixes) planned
+    with the per-token arrays expanded on the device equal, entry for entry, the host
+    plan of the same forward; tokens_used, pool bytes and outputs are identical."""
+    _log("forward plan device vs host")
+    from nanoslg_amd import kv_cache as KC
+    g = torch.Generator().manual_seed(17)
+    mk = lambda: make(ps=16, pages=600, prefix=True)[0]  # noqa: E731
+    host, dev = mk(), mk()
+    prompt = list(range(3, 300))
+    for m in (host, dev):
+        m.allocate_sequence("p", token_ids=prompt)
+    steps = [(["p"], [297], [0])]
+    ids = ["a", "b", "c"]
+    for ntok, offs in [([40, 400, 7], [3, 0, 20]), ([1, 1, 1], None), ([300, 2, 33], [0, 10, 0])]:
+        steps.append((ids, ntok, offs))
+    for sids, ntok, offs in steps:
+        offs = offs or [0] * len(sids)
+        S = max(o + n for o, n in zip(offs, ntok))
+        q = torch.randn(len(sids), S, HQ, D, generator=g).half().to(DEV)
+        k = torch.randn(len(sids), S, HKV, D, generator=g).half().to(DEV)
+        v = torch.randn(len(sids), S, HKV, D, generator=g).half().to(DEV)
+        if sids == ids and "a" not in host.seqs:
+            for m in (host, dev):
+                m.release_sequence("p")
+                for i, s in enumerate(ids):
+                    m.allocate_sequence(s, token_ids=prompt[:200] + [900 + i] * (5 + i))
+        outs, plans = [], []
+        for m, thr in ((host, 10 ** 9), (dev, 1)):
+            monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", thr)
+            c = m.begin_forward(sids, ntok, offs)
+            outs.append([c.attend(layer, q, k, v, HQ, HKV) for layer in range(L)])
+            plans.append(c.plan)
+            m.end_forward(c)
+        torch.cuda.synchronize()
+        a, b = plans
+        for name in ("slot", "pos_i32", "indptr", "indices", "lpl", "qo_indptr", "q_rows"):
+            x, y = getattr(a, name).cpu().long(), getattr(b, name).cpu().long()
+            if name == "indices":
+                n = int(a.indptr[-1])
+                x, y = x[:n], y[:n]
+            assert torch.equal(x, y), name
+        for oa, ob in zip(*outs):
+            assert torch.equal(oa, ob)
+        assert np.array_equal(host.pool.tokens_used, dev.pool.tokens_used)
+    assert torch.equal(host.pool.k, dev.pool.k) and torch.equal(host.pool.v, dev.pool.v)

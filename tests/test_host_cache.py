@@ -483,3 +483,21 @@ def test_decode_batch_with_shared_prefix_forms_groups():
         tabs = [mgr.seqs[ids[b]].bt[:7].tolist() for b in ms]
         assert all(t == tabs[0] for t in tabs)
     assert all(s is grp for s in seen[1:])  # carried over by the device-planned steps
+
+
+@pytest.mark.parametrize("scenario", ["prefill_then_decode", "cow_order", "radix_random", "positions",
+                                      "csr", "attend_rope"])
+def test_forward_plan_expanded_on_the_device_matches(scenario, monkeypatch):
+    """The same scenarios with every multi-token forward's per-token plan expanded by
+    the device planner (here its CPU stand-in) instead of the host: the oracle
+    comparisons of each scenario still hold."""
+    monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", 2)
+    FK.CALLS.clear()
+    {"prefill_then_decode": test_prefill_then_decode_matches_oracle,
+     "cow_order": test_copy_on_write_order_rule,
+     "radix_random": test_radix_random_workload_matches_oracle,
+     "positions": test_positions_shapes,
+     "csr": test_csr_plan_closed_form,
+     "attend_rope": lambda: test_attend_rope_equals_attend_on_rotated_inputs("paged")}[scenario]()
+    if scenario in ("prefill_then_decode", "radix_random", "attend_rope"):  # these have multi-token forwards
+        assert any(name == "forward_plan" for name, _ in FK.CALLS)
