@@ -241,13 +241,14 @@ class _PlanStaging:
             n = a.size
             host[off:off + n] = a.reshape(-1)
             off += n
-        main = torch.cuda.current_stream(self.device)
         self.pending[k] = True
         if 4 * total <= self.SIDE_STREAM_BYTES:
             dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
-            dev[:total].copy_(buf[:total], non_blocking=True)
-            self.copied[k].record(main)
+            if total:
+                (dev if total == dev.numel() else dev[:total]).copy_(buf[:total], non_blocking=True)
+            self.copied[k].record()  # on the current (compute) stream
             return dev
+        main = torch.cuda.current_stream(self.device)
         with torch.cuda.stream(self.side):
             dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
             dev[:total].copy_(buf[:total], non_blocking=True)
@@ -279,11 +280,10 @@ def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Ten
     else:
         dev = torch.from_numpy(np.concatenate([np.asarray(a, dtype=np.int32).reshape(-1) for a in parts])
                                if parts else np.zeros(0, np.int32)).clone()
-    out, off = [], 0
-    for n in sizes:
-        out.append(dev[off:off + n])
-        off += n
-    return out
+    if dev.numel() > total:
+        sizes = sizes + [dev.numel() - total]
+        return list(dev.split(sizes))[:-1]
+    return list(dev.split(sizes))
 
 
 def _ragged_layout(start_positions, new_token_counts, input_offsets, iw):
@@ -769,24 +769,34 @@ class PagedCacheContext(CacheContext):
             ncnt = np.fromiter(self.new_token_counts, np.int64, B)
             start = np.fromiter(self.start_positions, np.int64, B)
             have = np.fromiter((st.n_pages for st in states), np.int64, B)
-            # copy-on-write first, in batch order: a sequence writes its pages
-            # start//ps .. (start+n-1)//ps (those it has); shared ones are copied
-            for b, st in enumerate(states):
-                n = int(ncnt[b])
-                if n <= 0:
-                    continue
-                p0 = int(start[b]) // ps
-                p1 = min((int(start[b]) + n - 1) // ps + 1, st.n_pages)
-                if p1 > p0 and bool((pool.ref_count[st.bt[p0:p1]] > 1).any()):
-                    for p in range(p0, p1):
-                        if pool.is_shared(int(st.bt[p])):
-                            _cow(st, p)
-            # CSR block table (kv_cache.py:598-615)
+            # CSR block table (kv_cache.py:598-615), before copy-on-write
             lens = start + ncnt
             npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
             indptr = np.zeros(B + 1, np.int64)
             np.cumsum(npg, out=indptr[1:])
             indices = self._csr_indices(states, npg)
+            # copy-on-write, in batch order: a sequence writes its pages
+            # start//ps .. (start+n-1)//ps (those it has); shared ones are copied. Only a
+            # sequence writing a page that is shared before any copy can need one (copies
+            # only lower refcounts), so those are found at once on the CSR and the rule is
+            # then applied to them in batch order; their copies are patched into the CSR.
+            n = np.maximum(ncnt, 0)
+            p0 = start // ps
+            cnt = np.where(n > 0, np.maximum(np.minimum((start + n - 1) // ps + 1, have) - p0, 0), 0)
+            tot = int(cnt.sum())
+            if tot:
+                rep = np.repeat(np.arange(B), cnt)
+                first = np.zeros(B, np.int64)
+                np.cumsum(cnt[:-1], out=first[1:])
+                at = indptr[rep] + p0[rep] + (np.arange(tot, dtype=np.int64) - first[rep])
+                hit = pool.ref_count[indices[at]] > 1
+                if bool(hit.any()):
+                    for b in np.unique(rep[hit]).tolist():
+                        st = states[b]
+                        for p in range(int(p0[b]), int(p0[b] + cnt[b])):
+                            if pool.is_shared(int(st.bt[p])):
+                                _cow(st, p)
+                                indices[indptr[b] + p] = st.bt[p]
             T = int(ncnt.sum())
             device_plan = T >= self.DEVICE_PLAN_TOKENS and hasattr(cache.kernels, "_forward_plan")
             if device_plan:
@@ -1134,11 +1144,25 @@ class PagedKVCache(KVCacheManager):
         ps = self.cfg.page_size
         if any(n != 1 for n in ntoks):
             self._dev_plan = None
-        for s, n in zip(seq_ids, ntoks):  # extend_sequence, inlined
+        # extend_sequence for every sequence (kv_cache.py:724-728, 760-768), in batch
+        # order: one pool allocation for all of them when the free pages suffice (the
+        # same pages, in the same order, as one allocation per sequence), else per
+        # sequence, with eviction and the OOM error at the sequence that runs out
+        grow = []
+        for s, n in zip(seq_ids, ntoks):
             st = self.seqs[s]
-            need = -(-(st.num_tokens + n) // ps)
-            if need > st.n_pages:
-                st.extend(self._alloc(need - st.n_pages, defer_zero=True))
+            need = -(-(st.num_tokens + n) // ps) - st.n_pages
+            if need > 0:
+                grow.append((st, need))
+        if len(grow) > 1 and self.pool.num_free >= sum(k for _, k in grow):
+            pages = self._alloc(sum(k for _, k in grow), defer_zero=True)
+            o = 0
+            for st, k in grow:
+                st.extend(pages[o:o + k])
+                o += k
+        else:
+            for st, k in grow:
+                st.extend(self._alloc(k, defer_zero=True))
         zero, self._pending_zero = self._pending_zero, []
         return PagedCacheContext(self, seq_ids, ntoks, offsets, zero_pages=zero)
 
