@@ -49,6 +49,8 @@ def _parse():
                     choices=["kv_pressure", "small_batch", "radix", "prefill", "rope", "copy_calibration"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="decode workloads: replay each step from captured HIP graphs (DecodeGraph)")
     return ap.parse_args()
 
 
@@ -357,6 +359,7 @@ def run_decode(args):
         cfg = {"workload": "small_batch_decode_append", "batch": 4, "ctx": "uniform[1024,4096]",
                "pool_pages": 65536, "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D,
                "layers": 1, "seed": args.seed}
+    cfg["step"] = "graph replay (DecodeGraph)" if args.graph else "eager (begin_forward / attend / end_forward)"
     _log(f"workload {w.name}: B={w.B} pages={w.mgr.cfg.max_pages} sum(L)={sum(lens)}")
     from nanoslg_amd import kernels
     timed = EventTimedKernels(kernels)
@@ -364,6 +367,18 @@ def run_decode(args):
     for _ in range(args.warmup):
         w.step()
     torch.cuda.synchronize()
+    step = w.step
+    if args.graph:
+        from nanoslg_amd.kv_cache import DecodeGraph
+
+        def make_graph(warm):
+            g = DecodeGraph(w.mgr, w.ids, lambda ctx: ctx.attend(0, w.q[0], w.kn[0], w.vn[0], HQ, HKV))
+            for _ in range(warm):
+                g.step()
+            torch.cuda.synchronize()
+            return g
+        graph = make_graph(4)
+        step = graph.step
     lens_before = w.seq_lens()
     churn_at = args.steps // 2 if w.churn_frac > 0 else -1
     # Every sequence gains one token per step and the churn re-admits sequences at
@@ -384,9 +399,12 @@ def run_decode(args):
             torch.cuda.synchronize()
             c0 = time.perf_counter()
             w.churn()
+            if args.graph:  # the batch changed: capture the step again
+                graph = make_graph(0)
+                step = graph.step
             torch.cuda.synchronize()
             churn_s = time.perf_counter() - c0
-        w.step()
+        step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0 - churn_s
     assert w.seq_lens() == [L + args.steps for L in lens_before]

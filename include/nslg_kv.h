@@ -246,6 +246,23 @@ int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
                           int32_t head_dim, int32_t dtype, nslg_stream_t stream);
 
 /*
+ * nslg_decode_plan_step with the opened-page list read from memory at run time
+ * (int32[batch], same meaning as new_page above): device memory or pinned host
+ * memory (hipHostMalloc; read through its device mapping). For a step captured in
+ * a HIP graph: the launch's arguments stay the same from step to step and the host
+ * writes the list before each replay. The zeroing grid has a slot per sequence;
+ * slots of sequences that open no page exit. new_pages_out needs batch entries.
+ */
+int nslg_decode_plan_step_device(const int32_t* kv_indptr, const int32_t* kv_indices,
+                                 const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                                 const int32_t* new_page, int32_t* kv_indptr_out,
+                                 int32_t* kv_indices_out, int32_t* kv_last_page_len_out,
+                                 int32_t* slot_mapping_out, int32_t* positions_out, int32_t* new_pages_out,
+                                 void* k_pool, void* v_pool, int32_t num_layers, int64_t num_pages,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                 nslg_stream_t stream);
+
+/*
  * Device-side write plan of a multi-token forward: expands the forward's
  * per-sequence tables into the per-token arrays the append and the prefill take.
  * Replaces the per-token loop of FlashInferCacheContext.__init__ (slot of every new

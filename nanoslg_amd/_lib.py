@@ -47,6 +47,10 @@ SIGNATURES = {
     "nslg_decode_plan_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p]),
+    "nslg_decode_plan_step_device": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_void_p, c_int32, c_int64, c_int32, c_int32, c_int32,
+                                               c_void_p]),
     "nslg_forward_plan": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                     c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "nslg_rope_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,

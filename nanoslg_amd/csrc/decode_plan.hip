@@ -40,10 +40,17 @@ struct PlanStepArgs {
   int64_t page_bytes;  // bytes of one page in one layer (a multiple of 16)
   int32_t num_layers;
   int32_t zero_parts;  // ceil(page_bytes / kZeroBytes)
+  const int32_t* new_page_dev;  // nullptr: the list below; else the same list in device memory
   int32_t new_page[kMaxPlanBatch];  // page opened by sequence b this step, or -1
 };
 
-// Workgroup z of the zeroing part: opened page j, layer, K or V, 16 KiB part.
+__device__ inline int opened_page(const PlanStepArgs& a, int b) {
+  return a.new_page_dev ? a.new_page_dev[b] : a.new_page[b];
+}
+
+// Workgroup z of the zeroing part: (page, layer, K or V, 16 KiB part), where the
+// page is the j-th opened one of the list in the kernel arguments, or, with the
+// list in memory, the one sequence j opened (if any: one read of the list each).
 __device__ void zero_part(const PlanStepArgs& a, int z) {
   const int part = z % a.zero_parts;
   z /= a.zero_parts;
@@ -51,14 +58,19 @@ __device__ void zero_part(const PlanStepArgs& a, int z) {
   z >>= 1;
   const int layer = z % a.num_layers;
   const int j = z / a.num_layers;
-  int page = -1, seen = 0;
-  for (int b = 0; b < a.batch; ++b) {  // the j-th opened page, from the kernel arguments
-    if (a.new_page[b] >= 0) {
-      if (seen == j) {
-        page = a.new_page[b];
-        break;
+  int page = -1;
+  if (a.new_page_dev) {
+    page = j < a.batch ? a.new_page_dev[j] : -1;
+  } else {
+    int seen = 0;
+    for (int b = 0; b < a.batch; ++b) {  // the j-th opened page
+      if (a.new_page[b] >= 0) {
+        if (seen == j) {
+          page = a.new_page[b];
+          break;
+        }
+        ++seen;
       }
-      ++seen;
     }
   }
   if (page < 0 || (int64_t)page >= a.num_pages) return;
@@ -120,7 +132,7 @@ __global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs a) {
     int page;  // the page the new token goes to
     int lpl;
     if (opens) {
-      page = a.new_page[b];
+      page = opened_page(a, b);
       if (page < 0) page = 0;  // no page given: the null page (the sink of writes past a table)
       a.indices_out[seg_out + np_in] = page;
       a.new_pages_out[new_before_sh] = page;
@@ -143,20 +155,23 @@ __global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs a) {
 
 using namespace nslg;
 
-extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
-                                     const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
-                                     const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
-                                     int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
-                                     int32_t* positions_out, int32_t* new_pages_out, void* k_pool,
-                                     void* v_pool, int32_t num_layers, int64_t num_pages,
-                                     int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
-                                     nslg_stream_t stream) {
+namespace {
+
+// Shared set-up of both entry points; new_page_host xor new_page_dev is given. With
+// the list in memory the number of opened pages is not known here: the zeroing grid
+// has a slot per sequence and the slots of sequences that open no page exit.
+int plan_step_impl(const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                   int32_t batch, int32_t page_size, const int32_t* new_page_host, const int32_t* new_page_dev,
+                   int32_t* kv_indptr_out, int32_t* kv_indices_out,
+                   int32_t* kv_last_page_len_out, int32_t* slot_mapping_out, int32_t* positions_out,
+                   int32_t* new_pages_out, void* k_pool, void* v_pool, int32_t num_layers, int64_t num_pages,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t dtype, nslg_stream_t stream) {
   if (batch < 0 || page_size <= 0) return fail(NSLG_EINVAL, "decode_plan_step: bad sizes");
   if (batch == 0) return NSLG_OK;
   if (batch > kMaxPlanBatch)
     return fail(NSLG_EUNSUPPORTED, "decode_plan_step: batch %d > %d", batch, kMaxPlanBatch);
-  if (!kv_indptr || !kv_indices || !kv_last_page_len || !new_page || !kv_indptr_out || !kv_indices_out ||
-      !kv_last_page_len_out || !slot_mapping_out || !positions_out || !new_pages_out)
+  if (!kv_indptr || !kv_indices || !kv_last_page_len || !(new_page_host || new_page_dev) || !kv_indptr_out ||
+      !kv_indices_out || !kv_last_page_len_out || !slot_mapping_out || !positions_out || !new_pages_out)
     return fail(NSLG_EINVAL, "decode_plan_step: null pointer");
   if (kv_indices_out == kv_indices || kv_indptr_out == kv_indptr || kv_last_page_len_out == kv_last_page_len)
     return fail(NSLG_EINVAL, "decode_plan_step: output tables must not alias the input ones");
@@ -172,10 +187,15 @@ extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv
   a.new_pages_out = new_pages_out;
   a.batch = batch;
   a.page_size = page_size;
+  a.new_page_dev = new_page_dev;
   int opened = 0;
-  for (int b = 0; b < batch; ++b) {
-    a.new_page[b] = new_page[b];
-    opened += new_page[b] >= 0 ? 1 : 0;
+  if (new_page_host) {
+    for (int b = 0; b < batch; ++b) {
+      a.new_page[b] = new_page_host[b];
+      opened += new_page_host[b] >= 0 ? 1 : 0;
+    }
+  } else {
+    opened = batch;  // one zeroing slot per sequence: sequence j's page, if it opens one
   }
   a.k_pool = (char*)k_pool;
   a.v_pool = (char*)v_pool;
@@ -201,4 +221,46 @@ extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv
   }
   decode_plan_step_kernel<<<(unsigned)(batch + zero_groups), 256, 0, as_stream(stream)>>>(a);
   return check_launch("decode_plan_step");
+}
+
+}  // namespace
+
+extern "C" int nslg_decode_plan_step(const int32_t* kv_indptr, const int32_t* kv_indices,
+                                     const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                                     const int32_t* new_page, int32_t* kv_indptr_out, int32_t* kv_indices_out,
+                                     int32_t* kv_last_page_len_out, int32_t* slot_mapping_out,
+                                     int32_t* positions_out, int32_t* new_pages_out, void* k_pool,
+                                     void* v_pool, int32_t num_layers, int64_t num_pages,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                     nslg_stream_t stream) {
+  return plan_step_impl(kv_indptr, kv_indices, kv_last_page_len, batch, page_size, new_page, nullptr,
+                        kv_indptr_out, kv_indices_out, kv_last_page_len_out, slot_mapping_out, positions_out,
+                        new_pages_out, k_pool, v_pool, num_layers, num_pages, num_kv_heads, head_dim, dtype,
+                        stream);
+}
+
+extern "C" int nslg_decode_plan_step_device(const int32_t* kv_indptr, const int32_t* kv_indices,
+                                            const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                                            const int32_t* new_page, int32_t* kv_indptr_out,
+                                            int32_t* kv_indices_out, int32_t* kv_last_page_len_out,
+                                            int32_t* slot_mapping_out, int32_t* positions_out,
+                                            int32_t* new_pages_out, void* k_pool, void* v_pool,
+                                            int32_t num_layers, int64_t num_pages, int32_t num_kv_heads,
+                                            int32_t head_dim, int32_t dtype, nslg_stream_t stream) {
+  if (!new_page) return fail(NSLG_EINVAL, "decode_plan_step_device: null pointer");
+  // pinned host memory is read through its device mapping
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, new_page) == hipSuccess && attr.type == hipMemoryTypeHost) {
+    void* dptr = nullptr;
+    if (hipHostGetDevicePointer(&dptr, const_cast<int32_t*>(new_page), 0) != hipSuccess || !dptr) {
+      (void)hipGetLastError();
+      return fail(NSLG_EINVAL, "decode_plan_step_device: host list is not pinned, mapped memory");
+    }
+    new_page = static_cast<const int32_t*>(dptr);
+  }
+  (void)hipGetLastError();
+  return plan_step_impl(kv_indptr, kv_indices, kv_last_page_len, batch, page_size, nullptr, new_page,
+                        kv_indptr_out, kv_indices_out, kv_last_page_len_out, slot_mapping_out, positions_out,
+                        new_pages_out, k_pool, v_pool, num_layers, num_pages, num_kv_heads, head_dim, dtype,
+                        stream);
 }

@@ -315,7 +315,22 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
   if constexpr (kGrouped) units += ga.num_groups;
   const LaneLens<kGrouped> lens(p, ga, units);
   int ct = p.chunk_tokens;
-  if (p.chunk_budget > 0) ct = fit_chunk_tokens<kGrouped>(p, ga, lens, 64, ct, p.chunk_budget);
+  if (p.chunk_budget > 0) {
+    // An upper bound that fits, from the lengths themselves: with T tokens over U
+    // units, length ceil(T / (budget - U)) gives at most T / len + U <= budget
+    // chunks. (It is at most the host's bound, which came from an upper bound of T,
+    // so the search finds the same length; and a launch captured once stays right
+    // while the lengths grow.)
+    int tot = 0;
+    const int groups = (lens.units + 63) >> 6;
+    for (int i = 0; i < groups; ++i) tot += lens.at(p, ga, i);
+    const int64_t t_all = (int64_t)__builtin_amdgcn_readfirstlane(wave_sum_i32(tot));
+    const int64_t usable = (int64_t)p.chunk_budget - lens.units;
+    int64_t hi = (t_all + usable - 1) / usable;
+    hi = ((hi + 15) / 16) * 16;
+    hi = hi < 64 ? 64 : (hi > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : hi);
+    ct = fit_chunk_tokens<kGrouped>(p, ga, lens, 64, (int)hi, p.chunk_budget);
+  }
   int u = 0, cstart = 0, nchunks = 0;
   if (!locate_chunk<kGrouped>(p, ga, lens, ct, chunk, u, cstart, nchunks)) return;
   u = __builtin_amdgcn_readfirstlane(u);

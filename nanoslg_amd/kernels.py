@@ -387,6 +387,17 @@ def forward_plan(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, start: torch
                          int(input_width), int(page_size), int(total_tokens))
 
 
+def _decode_plan_step_device(kv_indptr, kv_indices, kv_last_page_len, new_page, B, page_size, dst, pool_args):
+    """The device planner reading the opened-page list from memory at run time (a
+    device tensor or a pinned host tensor), for a step captured in a graph: writes the
+    next plan into dst's static tensors."""
+    rc = _lib.load().nslg_decode_plan_step_device(
+        kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, int(page_size),
+        new_page.data_ptr(), dst.indptr.data_ptr(), dst.indices.data_ptr(), dst.lpl.data_ptr(),
+        dst.slot.data_ptr(), dst.pos.data_ptr(), dst.new_pages.data_ptr(), *pool_args, _stream(kv_indptr))
+    _lib.check(rc, "nslg_decode_plan_step_device")
+
+
 def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
     """forward_plan without the argument checks (the cache manager's own tables)."""
     sizes = [B * iw, B * iw, T, B + 1]

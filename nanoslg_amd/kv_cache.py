@@ -28,7 +28,7 @@ import math
 import threading
 from abc import ABC, abstractmethod
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -1423,3 +1423,176 @@ def attention_forward(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
     model's cos/sin tables, the cache write and attention, with the rotation and the
     write in one kernel launch (the context's attend_rope)."""
     return cache_ctx.attend_rope(layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads)
+
+
+# --------------------------------------------------------------------------------------
+# decode step replayed from HIP graphs
+# --------------------------------------------------------------------------------------
+
+
+class _GraphPlan:
+    """One static set of decode-plan tensors (indices with room for growth)."""
+
+    def __init__(self, device, batch, capacity):
+        sizes = [batch + 1, capacity, batch, batch, batch, batch]
+        self.buf = torch.zeros(sum(sizes), dtype=torch.int32, device=device)
+        (self.indptr, self.indices, self.lpl, self.slot, self.pos, self.new_pages) = self.buf.split(sizes)
+        self.batch, self.iw = batch, 1
+        self.groups = None
+
+
+class _GraphDecodeContext(CacheContext):
+    """The context a captured decode step's attend calls run on: its plan tensors
+    are static (the graph's), its host attributes are refreshed every step."""
+
+    def __init__(self, graph: "DecodeGraph", plan: _GraphPlan, launch):
+        self._graph, self._plan_t, self._launch = graph, plan, launch
+        self.seq_ids = list(graph.seq_ids)
+        self.batch_size = len(self.seq_ids)
+        self.new_token_counts = [1] * self.batch_size
+        self.input_offsets = [0] * self.batch_size
+        self.seq_lens: List[int] = []
+        self.start_positions: List[int] = []
+
+    def get_position_ids(self, S: int) -> torch.Tensor:
+        pos = self._plan_t.pos.view(self.batch_size, 1).long()
+        return pos if S == 1 else torch.cat([pos, pos.new_zeros(self.batch_size, S - 1)], 1)
+
+    def get_start_pos(self, idx: int = 0) -> int:
+        return self.start_positions[idx]
+
+    def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
+        B = q.shape[0]
+        return self._launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
+
+    def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
+        B = q.shape[0]
+        return self._launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, self._plan_t.pos)).reshape(B, 1, -1)
+
+
+class DecodeGraph:
+    """Steady decode steps of a fixed batch replayed from HIP graphs.
+
+    A step is: a copy of this step's opened-page list in (from pinned host memory),
+    the device planner (the next block tables, slots and positions from the previous
+    step's, zeroing the opened pages), then `forward(ctx)`, the caller's attend
+    calls for every layer (a model forward) on its static input tensors. Two graphs
+    alternate between two static plan buffers. Host work per step: the cache
+    bookkeeping of the step (pages opened, tokens_used), the page list, one replay.
+
+    forward(ctx) is called once per graph at capture; its return value (static
+    tensors) is what step() returns after each replay. The batch must not write a
+    shared page (copy-on-write goes through the eager path) and its chunking must
+    fit one resident round (the decode's launch is captured once); capacity bounds
+    the block-table growth: after max_steps steps, build a new DecodeGraph."""
+
+    def __init__(self, cache: "PagedKVCache", seq_ids: Sequence[str], forward, max_steps: int = 4096):
+        kern = cache.kernels
+        if not hasattr(kern, "_decode_plan_step_device"):
+            raise RuntimeError("DecodeGraph needs the HIP kernels")
+        self.cache, self.seq_ids, self.forward = cache, list(seq_ids), forward
+        B, ps, pool, cfg = len(self.seq_ids), cache.cfg.page_size, cache.pool, cache.cfg
+        if not 1 <= B <= 512:
+            raise ValueError("DecodeGraph: 1..512 sequences")
+        self.states = [cache.seqs[s] for s in self.seq_ids]
+        lens = np.fromiter((st.num_tokens for st in self.states), np.int64, B)
+        if (lens < 1).any():
+            raise ValueError("DecodeGraph: every sequence needs at least one cached token")
+        npg = (lens + ps - 1) // ps
+        have = np.fromiter((st.n_pages for st in self.states), np.int64, B)
+        if (have < npg).any():
+            raise ValueError("DecodeGraph: a sequence has fewer pages than tokens")
+        indptr = np.zeros(B + 1, np.int64)
+        np.cumsum(npg, out=indptr[1:])
+        indices = np.concatenate([st.bt[:k] for st, k in zip(self.states, npg.tolist())])
+        lpl = lens - (npg - 1) * ps
+        self.max_steps = int(max_steps)
+        cap = int(indptr[-1]) + B * ((self.max_steps + ps - 1) // ps + 1)
+        dev = pool.device
+        self.plans = [_GraphPlan(dev, B, cap), _GraphPlan(dev, B, cap)]
+        (d_ip, d_ix, d_lpl) = _upload_i32([indptr, indices, lpl], dev)
+        p0 = self.plans[0]
+        p0.indptr.copy_(d_ip)
+        p0.indices[:indices.size].copy_(d_ix)
+        p0.lpl.copy_(d_lpl)
+        groups = cache._prefix_groups(self.states, npg + 1)
+        if groups is not None:
+            g = kern.DecodeGroups(B, groups[0], groups[1], dev)
+            for p in self.plans:
+                p.groups = g
+        self.new_host = [torch.zeros(B, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.new_np = [t.numpy() for t in self.new_host]
+        self.new_dev = [torch.zeros(B, dtype=torch.int32, device=dev) for _ in range(2)]
+        self.done = [torch.cuda.Event() for _ in range(2)]
+        self.used = [False, False]
+        L, P = cfg.num_layers, cfg.max_pages
+        self.pool_args = (pool.k.data_ptr(), pool.v.data_ptr(), L, P, cfg.num_kv_heads, cfg.head_dim,
+                          kern.dtype_code(pool.k.dtype))
+        # The launch is captured once, so it is sized for the pool (P pages) rather than
+        # this step's page count; the kernel derives its chunk length from the lengths.
+        launches = [kern.DecodeLaunch(pool.k, pool.v, p.slot, p.indptr, p.indices, p.lpl, P, cfg.num_qo_heads,
+                                      workspace=cache.workspace, groups=p.groups) for p in self.plans]
+        self.ctxs = [_GraphDecodeContext(self, self.plans[(i + 1) % 2], launches[(i + 1) % 2]) for i in range(2)]
+        self.graphs, self.outputs = [], []
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        torch.cuda.synchronize(dev)
+        with torch.cuda.stream(side):
+            for i in range(2):  # graph i: plan i -> plan 1-i, then the forward on plan 1-i
+                src, dst = self.plans[i], self.plans[1 - i]
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=side):
+                    # this step's page list: pinned host memory -> device (a copy node of
+                    # the graph; measured faster than the planner reading host memory)
+                    self.new_dev[i].copy_(self.new_host[i], non_blocking=True)
+                    kern._decode_plan_step_device(src.indptr, src.indices, src.lpl, self.new_dev[i], B, ps, dst,
+                                                  self.pool_args)
+                    out = forward(self.ctxs[i])
+                self.graphs.append(g)
+                self.outputs.append(out)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.parity = 0
+        self.steps = 0
+        cache._dev_plan = None
+
+    def step(self):
+        """One decode step of the batch: bookkeeping, then the graph replay."""
+        cache, pool, ps = self.cache, self.cache.pool, self.cache.cfg.page_size
+        if self.steps >= self.max_steps:
+            raise RuntimeError("DecodeGraph: block-table capacity used up; build a new DecodeGraph")
+        i = self.parity
+        if self.used[i]:
+            self.done[i].synchronize()  # the page list of two steps ago has been copied in
+        B = len(self.states)
+        start = np.fromiter((st.num_tokens for st in self.states), np.int64, B)
+        opens = start % ps == 0
+        new_np = self.new_np[i]
+        new_np[:] = -1
+        pids = np.empty(B, np.int64)
+        for b in np.flatnonzero(opens).tolist():
+            st = self.states[b]
+            need = int(start[b]) // ps + 1
+            if st.n_pages < need:  # zeroed by the graph's planner, not by a launch of its own
+                k = need - st.n_pages
+                st.extend(cache._alloc(k, defer_zero=True))
+                del cache._pending_zero[-k:]
+            # (a page the sequence already had was zeroed when it was allocated)
+            new_np[b] = st.bt[need - 1]
+        npg = start // ps + 1
+        for b, st in enumerate(self.states):
+            pids[b] = st.bt[npg[b] - 1]
+        if bool((pool.ref_count[pids] > 1).any()):
+            raise RuntimeError("DecodeGraph: a shared page would be written; use the eager path")
+        sl = start % ps
+        pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
+        ctx = self.ctxs[i]
+        ctx.start_positions = start.tolist()
+        ctx.seq_lens = (start + 1).tolist()
+        self.graphs[i].replay()
+        self.done[i].record()
+        self.used[i] = True
+        for st in self.states:
+            st.num_tokens += 1
+        self.parity ^= 1
+        self.steps += 1
+        return self.outputs[i]

@@ -247,3 +247,50 @@ def test_forward_plan_on_device_equals_host_plan(monkeypatch):
             assert torch.equal(oa, ob)
         assert np.array_equal(host.pool.tokens_used, dev.pool.tokens_used)
     assert torch.equal(host.pool.k, dev.pool.k) and torch.equal(host.pool.v, dev.pool.v)
+
+
+def test_decode_graph_replays_match_eager_steps():
+    """Decode steps replayed from the captured graphs (planner + per-layer append and
+    decode) against the same steps run eagerly on a second cache with the same
+    history: every replay's outputs, the pool bytes, tokens_used and block tables
+    are identical, over steps that open pages (in-graph zeroing)."""
+    _log("decode graph vs eager")
+    from nanoslg_amd import kv_cache as KC
+    g = torch.Generator().manual_seed(23)
+    lens = [15, 16, 100, 257]
+    ids = ["a", "b", "c", "d"]
+    caches = [make(ps=16, pages=400, prefix=False)[0] for _ in range(2)]
+    S = max(lens)
+    q0 = torch.randn(4, S, HQ, D, generator=g).half().to(DEV)
+    k0 = torch.randn(4, S, HKV, D, generator=g).half().to(DEV)
+    for m in caches:
+        for s, n in zip(ids, lens):
+            m.allocate_sequence(s, num_tokens=n)
+        c = m.begin_forward(ids, lens)
+        for layer in range(L):
+            c.attend(layer, q0, k0, k0, HQ, HKV)
+        m.end_forward(c)
+    gm, em = caches
+    qs = torch.zeros(4, 1, HQ, D, dtype=torch.float16, device=DEV)
+    ks = torch.zeros(4, 1, HKV, D, dtype=torch.float16, device=DEV)
+    vs = torch.zeros(4, 1, HKV, D, dtype=torch.float16, device=DEV)
+    graph = KC.DecodeGraph(gm, ids, lambda ctx: [ctx.attend(layer, qs, ks, vs, HQ, HKV) for layer in range(L)])
+    for step in range(40):
+        q = torch.randn(4, 1, HQ, D, generator=g).half().to(DEV)
+        k = torch.randn(4, 1, HKV, D, generator=g).half().to(DEV)
+        v = torch.randn(4, 1, HKV, D, generator=g).half().to(DEV)
+        qs.copy_(q)
+        ks.copy_(k)
+        vs.copy_(v)
+        outs = graph.step()
+        c = em.begin_forward(ids, [1] * 4)
+        ref = [c.attend(layer, q, k, v, HQ, HKV) for layer in range(L)]
+        em.end_forward(c)
+        torch.cuda.synchronize()
+        for a, b in zip(outs, ref):
+            assert torch.equal(a, b), step
+    assert torch.equal(gm.pool.k, em.pool.k) and torch.equal(gm.pool.v, em.pool.v)
+    assert np.array_equal(gm.pool.tokens_used, em.pool.tokens_used)
+    for s in ids:
+        assert gm.seqs[s].num_tokens == em.seqs[s].num_tokens
+        assert gm.seqs[s].block_table == em.seqs[s].block_table
