@@ -35,6 +35,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Extra flags for single sources. The prefill kernel's softmax takes running maxima
+# of scores that are never NaN for finite inputs; without NaN semantics the
+# compiler drops the quieting copy it otherwise puts in front of every max.
+FILE_FLAGS = {
+    "paged_prefill.hip": ["-fno-honor-nans"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -48,7 +56,7 @@ def sources() -> list[Path]:
 
 def _compile_one(hipcc: str, src: Path, extra: list[str]) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

@@ -3,22 +3,31 @@
 //
 // Query rows are packed GQA-style: for KV head h of sequence b the row space is
 // the b's n_b new tokens x the G query heads of h, row = token*G + g. A
-// workgroup (4 waves) owns 128 consecutive rows of one (sequence, KV head);
-// each wave owns 32 rows as two 16-row column blocks of the MFMA.
+// workgroup (8 waves, 2 per SIMD) owns 256 consecutive rows of one (sequence, KV
+// head); each wave owns 32 rows as two 16-row column blocks of the MFMA.
 //
-// Per 64-key tile (staged in LDS, double buffered, shared by the 4 waves):
+// Keys are staged in LDS in 128-key tiles (double buffered, shared by the 8 waves)
+// and consumed in 32-key blocks. Per block:
 //   S^T[16 key x 16 row] = K[16 key x D] * Q^T[D x 16 row]   v_mfma 16x16x32, D/32 steps
-//   online softmax per row (column) in fp32, running max rescaled lazily
+//   online softmax per row (column) in fp32, running max raised lazily
 //   O^T[D x 16 row] += V^T[D x 32 key] * P^T[32 key x 16 row]  v_mfma 16x16x32,
 //     V^T operands read from the row-major V tile with transposing LDS reads
-//   (P.V runs over 32-key blocks so it uses the full-rate 16x16x32 instruction; the
-//   16x16x16 one issues at half the rate on gfx950)
-// which is the decode kernel's formulation with all 16 MFMA columns live.
+//   the row sums of P come from one more MFMA with an all-ones A operand
+// (P.V runs over 32-key blocks so it uses the full-rate 16x16x32 instruction; the
+// 16x16x16 one issues at half the rate on gfx950). Within a tile the blocks are
+// software pipelined: the scores of block i+1 are computed before the
+// probabilities of block i, and the K operands of block i+2 are read from LDS
+// during P.V of block i. The next tile is fetched from HBM and stashed into the
+// other LDS stage in two 64-key halves at two points of the current tile, so
+// only one half's staging registers are live at a time.
 //
 // Causality is bottom-right aligned: sequence b holds L_b tokens of which the
 // last n_b are the new ones, so row token t sees keys j <= L_b - n_b + t.
 // The sequence's page ids for the workgroup's key range sit in LDS (windows of
 // 2048 pages), so tile loads never wait on index loads.
+//
+// Built with -fno-honor-nans (nanoslg_amd/_build.py): the running maxima are
+// taken with plain v_max/v_max3 instead of NaN-quieting ones.
 #include "nslg_common.h"
 
 #include <math.h>
@@ -30,9 +39,10 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerWG = kWaves * kRowsPerWave;  // 256
-constexpr int kKeys = 64;                          // keys per LDS tile
+constexpr int kKeys = 128;
 constexpr int kPageWin = 2048;                     // page ids per LDS window
 constexpr float kRescaleSlack = 8.0f;
+constexpr int kBlocks = kKeys / 32;                // 32-key blocks per tile
 
 struct PrefillParams {
   const uint16_t* q;
@@ -104,11 +114,12 @@ template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p) {
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
-  constexpr int kPitch = D + 8;  // LDS row pitch in elements (16 B pad vs bank conflicts)
+  constexpr int kPitch = D + 8;   // K tile row pitch in elements: 16 B reads of 16 lanes span all banks
+  constexpr int kVPitch = D + 16; // V tile row pitch: transposing 8 B reads of 8 rows x 4 lanes span all banks
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKeys * kPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kVPitch];
   __shared__ int32_t page_lds[kPageWin];
 
   const int tid = threadIdx.x;
@@ -167,22 +178,36 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   }
   // highest key any row of this wave may see (rows are token-major, so the wave's last row)
   const int wave_last_row = min(row0_wg + wave * kRowsPerWave + kRowsPerWave, nrows) - 1;
-  const int wave_kv_end = wave_last_row >= row0_wg + wave * kRowsPerWave ? start + wave_last_row / G + 1 : 0;
+  const int wave_kv_end = __builtin_amdgcn_readfirstlane(
+      wave_last_row >= row0_wg + wave * kRowsPerWave ? start + wave_last_row / G + 1 : 0);
   // lowest position among the wave's rows: keys below start + first_tok + 1 are visible to all
-  const int wave_first_tok = start + (row0_wg + wave * kRowsPerWave) / G;
+  const int wave_first_tok = __builtin_amdgcn_readfirstlane(start + (row0_wg + wave * kRowsPerWave) / G);
 
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+  // row sums of P on the MFMA: an all-ones A operand makes every row of the 16x16
+  // output tile the column's sum over the block's keys
+  f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  const unsigned short one16 = T::from_f32(1.f);
+  const u16x8 ones = u16x8{one16, one16, one16, one16, one16, one16, one16, one16};
+  // per column block: raw-score threshold above which the running max must be raised,
+  // and the exponent offset -m (0 while m = -inf); both change only with m
+  float thr[2] = {-INFINITY, -INFINITY};
+  float neg_m[2] = {0.f, 0.f};
+  const float inv_scale_log2 = 1.f / p.scale_log2;
   f32x4 o[2][NT];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[cb][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- cooperative tile loads: 64 keys x D for K and V, 16 B per thread-chunk ------
-  constexpr int kChunks = D / 8;                       // 16 B chunks per row
-  constexpr int kPerThread = kKeys * kChunks / kThreads;  // 2 (D=128) or 1 (D=64)
-  u32x4 kreg[kPerThread], vreg[kPerThread];
+  // ---- cooperative tile loads: kKeys keys x D for K and V in two halves ------------
+  // Each half (kKeys / 2 keys) is fetched into registers and stashed into the next LDS
+  // stage at its own point of the current tile, so only one half's staging registers
+  // are live at a time.
+  constexpr int kChunks = D / 8;                             // 16 B chunks per row
+  constexpr int kHalf = kKeys / 2;
+  constexpr int kPerThreadH = kHalf * kChunks / kThreads;    // 2 (D=128) or 1 (D=64)
+  u32x4 kreg[kPerThreadH], vreg[kPerThreadH];
   int win_base = -1;
 
   auto load_pages = [&](int first_key) {
@@ -204,10 +229,10 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   const bool ps_pow2 = (ps & (ps - 1)) == 0;
   const int ps_shift = __builtin_ctz((unsigned)ps);
   const int64_t page_bytes = (int64_t)ps * row_bytes;
-  auto fetch = [&](int kt) {
-    const int key0 = kt * kKeys;
+  auto fetch_half = [&](int kt, int half) {
+    const int key0 = kt * kKeys + half * kHalf;
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
+    for (int i = 0; i < kPerThreadH; ++i) {
       int kabs = key0 + f_key + (kThreads / kChunks) * i;
       kabs = kabs < kv_end ? kabs : kv_end - 1;
       int pg, slot;
@@ -224,12 +249,12 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
       vreg[i] = *reinterpret_cast<const u32x4*>(vpool + off);
     }
   };
-  auto stash = [&](int stage) {
+  auto stash_half = [&](int stage, int half) {
 #pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      const int e = (f_key + (kThreads / kChunks) * i) * kPitch + f_ch16 / 2;
-      *reinterpret_cast<u32x4*>(&k_lds[stage][e]) = kreg[i];
-      *reinterpret_cast<u32x4*>(&v_lds[stage][e]) = vreg[i];
+    for (int i = 0; i < kPerThreadH; ++i) {
+      const int key = half * kHalf + f_key + (kThreads / kChunks) * i;
+      *reinterpret_cast<u32x4*>(&k_lds[stage][key * kPitch + f_ch16 / 2]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&v_lds[stage][key * kVPitch + f_ch16 / 2]) = vreg[i];
     }
   };
   // first key of the window holding tile kt must cover the whole tile
@@ -239,132 +264,174 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
     return win_base >= 0 && k_first / ps >= win_base && k_last / ps < win_base + kPageWin;
   };
 
+  // ---- per-block pieces ------------------------------------------------------------
+  // K operands of a 32-key block: keys kbase + 16t + r, columns 32s + 8gq .. +7
+  auto load_k = [&](int stage, int kb, u16x8 (&ka)[2][kSteps]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint16_t* krow = &k_lds[stage][(32 * kb + 16 * t + r) * kPitch + 8 * gq];
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) ka[t][s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
+    }
+  };
+  // S^T of both column blocks: keys kbase + 16t + 4gq + j in lane (r, gq), element j
+  auto qk = [&](const u16x8 (&ka)[2][kSteps], f32x4 (&sacc)[2][2]) {
+
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        sacc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) sacc[cb][t] = T::mma_k32(ka[t][s], qb[cb][s], sacc[cb][t]);
+      }
+
+  };
+  // A operand of output tile n, V^T[d = 16n + r][keys of k = 8gq + j], read from the
+  // row-major tile with gfx950's transposing LDS read: in each 16-lane group, lane
+  // i = 4a + c receives element c of the 8-byte blocks addressed by lanes a, 4 + a,
+  // 8 + a and 12 + a. Lane r addresses keys kbase + 4gq + r/4 (then + 16), columns
+  // 16n + 4(r%4) .. +3, so it receives keys kbase + 4gq + 0..3 (+ 16) at d = 16n + r.
+  auto load_v = [&](int stage, int kb, u16x8 (&va)[NT]) {
+    const uint16_t* vsrc = &v_lds[stage][(32 * kb + 4 * gq + (r >> 2)) * kVPitch + 4 * (r & 3)];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      typedef short i16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) i16x4* lds_i16x4;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n + 16 * kVPitch));
+      va[n] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+  // masking (blocks touching the causal diagonal or the end of the keys) and the lazy
+  // rescale: the row's running max m is raised only when some score of the block
+  // exceeds it by more than the slack, which each lane checks on its own 8 scores;
+  // the cross-lane row max is needed only then
+  auto mask_and_rescale = [&](int kbase, f32x4 (&sacc)[2][2]) {
+    const bool full = kbase + 32 <= wave_first_tok + 1 && kbase + 32 <= kv_end;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      if (!full) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = kbase + 16 * (j >> 2) + 4 * gq + (j & 3);
+          if (!(key < kv_end && key <= row_tok[cb])) sacc[cb][j >> 2][j & 3] = -INFINITY;
+        }
+      }
+      const f32x4 a = sacc[cb][0], b = sacc[cb][1];
+      const float lmax = fmaxf(fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])),
+                               fmaxf(fmaxf(b[0], b[1]), fmaxf(b[2], b[3])));
+      if (__ballot(lmax > thr[cb])) {
+        const float m_new = fmaxf(m_run[cb], rows_max(lmax * p.scale_log2));
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[cb] - m_new);
+        lsum[cb] *= alpha;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) o[cb][n] *= alpha;
+        m_run[cb] = m_new;
+        thr[cb] = (m_new + kRescaleSlack) * inv_scale_log2;
+        neg_m[cb] = m_new == -INFINITY ? 0.f : -m_new;
+      }
+    }
+  };
+  // probabilities of both column blocks as 16-bit MFMA B operands (k index 8gq + j
+  // stands for the lane's keys: j < 4 the first 16-key tile, j >= 4 the second)
+  auto probs = [&](const f32x4 (&sacc)[2][2], u16x8 (&pb)[2], u16x8 (&pb_lo)[2]) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pj = fast_exp2(fmaf(sacc[cb][j >> 2][j & 3], p.scale_log2, neg_m[cb]));
+        pb[cb][j] = T::from_f32(pj);
+        if constexpr (kSplitP) pb_lo[cb][j] = T::from_f32(pj - T::to_f32(pb[cb][j]));
+      }
+  };
+  auto pv = [&](const u16x8 (&va)[NT], const u16x8 (&pb)[2], const u16x8 (&pb_lo)[2]) {
+
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        o[cb][n] = T::mma_k32(va[n], pb[cb], o[cb][n]);
+        if constexpr (kSplitP) o[cb][n] = T::mma_k32(va[n], pb_lo[cb], o[cb][n]);
+      }
+      lsum[cb] = T::mma_k32(ones, pb[cb], lsum[cb]);
+      if constexpr (kSplitP) lsum[cb] = T::mma_k32(ones, pb_lo[cb], lsum[cb]);
+    }
+
+  };
+
   if (n_kt > 0) {
     load_pages(0);
     __syncthreads();
-    fetch(0);
-    stash(0);
+    fetch_half(0, 0);
+    stash_half(0, 0);
+    fetch_half(0, 1);
+    stash_half(0, 1);
   }
   __syncthreads();
 
   for (int kt = 0; kt < n_kt; ++kt) {
     const int stage = kt & 1;
     const bool more = kt + 1 < n_kt;
-    bool need_win = false;
-    if (more) {
-      need_win = !window_ok(kt + 1);
-      if (!need_win) fetch(kt + 1);
-    }
+    const bool staged = more && window_ok(kt + 1);  // next tile fetched in halves during this one
+    if (staged) fetch_half(kt + 1, 0);
     const int key0 = kt * kKeys;
-    if (key0 < wave_kv_end) {
-      // 32-key blocks. S^T comes from two 16-key MFMA tiles (keys kbase + 4gq + j and
-      // kbase + 16 + 4gq + j in a lane); P^T feeds one 16x16x32 MFMA per output tile
-      // whose k index 8gq + j stands for exactly those keys (j < 4: first tile,
-      // j >= 4: second), and the V operand is loaded for the same keys, so the
-      // key order inside the block is consistent and P.V is exact.
+    // 32-key blocks of this tile that the wave's rows can see (wave-uniform)
+    int nb = (min(wave_kv_end, key0 + kKeys) - key0 + 31) / 32;
+    nb = nb < 0 ? 0 : (nb > kBlocks ? kBlocks : nb);
+    bool half1_done = false;
+    if (nb > 0) {
+      // Software pipeline over the tile's blocks: the scores of block kb + 1 are
+      // computed (MFMA) while the probabilities of block kb are (VALU), and P.V of
+      // block kb runs while the K operands of block kb + 2 are read from LDS.
+      u16x8 ka[2][kSteps];
+      f32x4 sacc[2][2][2];
+      load_k(stage, 0, ka);
+      qk(ka, sacc[0]);
+      if (nb > 1) load_k(stage, 1, ka);
 #pragma unroll
-      for (int kb = 0; kb < kKeys / 32; ++kb) {
+      for (int kb = 0; kb < kBlocks; ++kb) {
+        if (kb >= nb) break;
+        const int cur = kb & 1;
         const int kbase = key0 + 32 * kb;
-        if (kbase >= wave_kv_end) break;
-        const bool full = kbase + 32 <= wave_first_tok + 1 && kbase + 32 <= kv_end;
-        u16x8 ka[2][kSteps];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint16_t* krow = &k_lds[stage][(32 * kb + 16 * t + r) * kPitch + 8 * gq];
-#pragma unroll
-          for (int s = 0; s < kSteps; ++s) ka[t][s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
-        }
-        f32x4 sacc[2][2];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            sacc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) sacc[cb][t] = T::mma_k32(ka[t][s], qb[cb][s], sacc[cb][t]);
-          }
-        // A operand of output tile n, V^T[d = 16n + r][keys of k = 8gq + j], read from the
-        // row-major tile with gfx950's transposing LDS read: in each 16-lane group, lane
-        // i = 4a + c receives element c of the 8-byte blocks addressed by lanes a, 4 + a,
-        // 8 + a and 12 + a. Lane r addresses keys kbase + 4gq + r/4 (then + 16), columns
-        // 16n + 4(r%4) .. +3, so it receives keys kbase + 4gq + 0..3 (+ 16) at d = 16n + r.
+        mask_and_rescale(kbase, sacc[cur]);
         u16x8 va[NT];
-        {
-          const uint16_t* vsrc = &v_lds[stage][(32 * kb + 4 * gq + (r >> 2)) * kPitch + 4 * (r & 3)];
-#pragma unroll
-          for (int n = 0; n < NT; ++n) {
-            typedef short i16x4 __attribute__((ext_vector_type(4)));
-            typedef __attribute__((address_space(3))) i16x4* lds_i16x4;
-            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vsrc + 16 * n + 16 * kPitch));
-            va[n] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          }
-        }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          // raw scores; the softmax scale is applied inside the exponent's FMA. Only a
-          // block that touches the causal diagonal (or the end of the keys) is masked.
-          float sv[8];
-          if (full) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sv[j] = sacc[cb][j >> 2][j & 3];
-          } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int key = kbase + 16 * (j >> 2) + 4 * gq + (j & 3);
-              sv[j] = (key < kv_end && key <= row_tok[cb]) ? sacc[cb][j >> 2][j & 3] : -INFINITY;
-            }
-          }
-          // Lazy rescale: the row's running max m is raised only when some score of the
-          // block exceeds it by more than the slack, which each lane checks on its own
-          // 8 scores; the cross-lane row max is needed only then.
-          const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]))) * p.scale_log2;
-          if (__ballot(lmax > m_run[cb] + kRescaleSlack)) {
-            const float m_new = fmaxf(m_run[cb], rows_max(lmax));
-            const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[cb] - m_new);
-            l_run[cb] *= alpha;
-#pragma unroll
-            for (int n = 0; n < NT; ++n) o[cb][n] *= alpha;
-            m_run[cb] = m_new;
-          }
-          const float neg_m = m_run[cb] == -INFINITY ? 0.f : -m_run[cb];
-          u16x8 pb, pb_lo;
-          float pj[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            pj[j] = fast_exp2(fmaf(sv[j], p.scale_log2, neg_m));
-            pb[j] = T::from_f32(pj[j]);
-            if constexpr (kSplitP) pb_lo[j] = T::from_f32(pj[j] - T::to_f32(pb[j]));
-          }
-          l_run[cb] += ((pj[0] + pj[1]) + (pj[2] + pj[3])) + ((pj[4] + pj[5]) + (pj[6] + pj[7]));
-#pragma unroll
-          for (int n = 0; n < NT; ++n) {
-            o[cb][n] = T::mma_k32(va[n], pb, o[cb][n]);
-            if constexpr (kSplitP) o[cb][n] = T::mma_k32(va[n], pb_lo, o[cb][n]);
-          }
+        u16x8 pb[2], pb_lo[2];
+        load_v(stage, kb, va);
+        if (kb + 1 < nb) qk(ka, sacc[cur ^ 1]);
+        probs(sacc[cur], pb, pb_lo);
+        if (kb + 2 < nb) load_k(stage, kb + 2, ka);
+        pv(va, pb, pb_lo);
+        if (kb == 1 && staged) {
+          stash_half(stage ^ 1, 0);
+          fetch_half(kt + 1, 1);
+          half1_done = true;
         }
       }
     }
-    if (more) {
-      if (need_win) {
-        // the next tile crosses the page-id window: reload it (all threads finished
-        // reading the current stage's page ids in the fetch above, so only the new
-        // window must be visible before fetching)
-        __syncthreads();
-        load_pages((kt + 1) * kKeys);
-        __syncthreads();
-        fetch(kt + 1);
+    if (staged) {
+      if (!half1_done) {
+        stash_half(stage ^ 1, 0);
+        fetch_half(kt + 1, 1);
       }
-      stash(stage ^ 1);
+      stash_half(stage ^ 1, 1);
+    } else if (more) {
+      // the next tile crosses the page-id window: reload it (every thread is done
+      // reading page ids of the current window once all reach the barrier)
+      __syncthreads();
+      load_pages((kt + 1) * kKeys);
+      __syncthreads();
+      fetch_half(kt + 1, 0);
+      stash_half(stage ^ 1, 0);
+      fetch_half(kt + 1, 1);
+      stash_half(stage ^ 1, 1);
     }
     __syncthreads();
   }
-
   // ---- epilogue: normalise and store rows ----------------------------------------
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    const float l_tot = rows_sum(l_run[cb]);
+    const float l_tot = lsum[cb][0];
     if (!row_ok[cb]) continue;
     const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
     const int t = row / G;
@@ -424,6 +491,8 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_q < 0)
     return fail(NSLG_EINVAL, "paged_prefill: bad sizes");
+  if (!(sm_scale > 0.f) || !(sm_scale < INFINITY))
+    return fail(NSLG_EINVAL, "paged_prefill: sm_scale must be positive and finite");
   if (batch == 0 || total_q == 0) return NSLG_OK;
   if (!q || !qo_indptr || !k_pool || !v_pool || !kv_indptr || !kv_indices || !kv_last_page_len || !out)
     return fail(NSLG_EINVAL, "paged_prefill: null pointer");

@@ -53,6 +53,12 @@ def test_host_side_argument_checks():
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 34, 8, 128, 0.1, 0, 256, 4096,
                                None, 0, None)
     assert rc == -1  # Hq not a multiple of Hkv
+    # prefill: the softmax scale must be positive and finite (the lazy running max
+    # compares raw scores against a threshold divided by the scale)
+    for bad in (0.0, -0.1, float("inf"), float("nan")):
+        rc = lib.nslg_paged_prefill(256, 4096, 256, 8, 8, 256, 256, 100, 16, 256, 256, 256, 1, 32, 8, 128,
+                                    bad, 0, 256, 4096, 256, 256, None)
+        assert rc == -1 and "sm_scale" in _lib.last_error(), bad
     # device decode planner: too large a batch, null pointers, aliased outputs
     z = (None, None, 0, 0, 0, 0, 0)
     assert lib.nslg_decode_plan_step(1, 1, 1, 513, 16, 1, 2, 2, 2, 2, 2, 2, *z, None) == -2
