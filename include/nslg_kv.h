@@ -128,8 +128,11 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
  *   workspace         caller-owned device scratch of at least
  *                     nslg_paged_decode_workspace_size(...) bytes, 256-byte aligned;
  *                     one call at a time per workspace
- * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16;
- * D in {64, 128, 256}; 1 <= Hq/Hkv <= 16. A sequence with no tokens gets zeros.
+ * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16 (MFMA, split-K as
+ * above) and f32 (a VALU kernel, one workgroup per 16 query rows of a sequence and
+ * KV head, for caches kept in fp32 such as the contiguous backend of an fp32
+ * model, kv_cache.py:227-322); D in {64, 128, 256}; 1 <= Hq/Hkv <= 16. A sequence
+ * with no tokens gets zeros.
  */
 size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
                                         int32_t num_kv_heads, int32_t head_dim,
@@ -165,7 +168,8 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
  *                       [16 g, 16 g + n_g), -1 after them; 1 <= n_g <= 16 / G;
  *                       a sequence is in at most one group
  * The workspace holds 16 / G partial slots per chunk:
- * nslg_paged_decode_grouped_workspace_size(...) bytes.
+ * nslg_paged_decode_grouped_workspace_size(...) bytes. f16/bf16 only (the size
+ * query returns 0 for f32; decode f32 batches with nslg_paged_decode).
  */
 size_t nslg_paged_decode_grouped_workspace_size(int32_t batch, int32_t num_qo_heads,
                                                 int32_t num_kv_heads, int32_t head_dim,
@@ -198,7 +202,9 @@ int nslg_paged_decode_grouped(const void* q, int64_t q_stride,
  *               row t of b attends to keys j <= L_b - n_b + t.
  *   total_q     host copy of qo_indptr[batch]; max_q: host max of n_b
  *   out         [T] rows of Hq*D elements at stride out_stride
- * Supported: f16, bf16; D in {64, 128}; 1 <= Hq/Hkv <= 16.
+ *   sm_scale    positive and finite (EINVAL otherwise)
+ * Supported: f16, bf16 with D in {64, 128} (MFMA); f32 with D in {64, 128, 256}
+ * (the VALU kernel of nslg_paged_decode's f32 path); 1 <= Hq/Hkv <= 16.
  */
 size_t nslg_paged_prefill_workspace_size(int32_t batch, int32_t num_qo_heads,
                                          int32_t head_dim, int64_t total_q,
@@ -304,9 +310,10 @@ int nslg_forward_plan(const int32_t* kv_indptr, const int32_t* kv_indices, const
  *   cos_table, sin_table   fp32 [table_rows] rows of >= D floats at table_stride
  *                   (the model's precomputed tables, models.py:37-66)
  *   k_pool, v_pool  one layer, pool_slots rows of Hkv*D elements
- * q_out and the pool's K rows = rnd(rnd(x*c) + rnd(rot(x)*s)) in the 16-bit type
+ * q_out and the pool's K rows = rnd(rnd(x*c) + rnd(rot(x)*s)) in the storage type
  * with c, s the table values rounded to it, rot(x) = cat(-x[D/2:], x[:D/2]):
- * bit-exact with the eager expression. V rows are copied. f16/bf16, D in {64,128,256}.
+ * bit-exact with the eager expression. V rows are copied. f16/bf16/f32,
+ * D in {64,128,256}.
  */
 int nslg_rope_append(const void* q, int64_t q_stride, void* q_out, int64_t q_out_stride,
                      const void* k_new, int64_t k_stride, const void* v_new, int64_t v_stride,

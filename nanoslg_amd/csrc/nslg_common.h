@@ -106,4 +106,28 @@ __device__ inline float rows_sum(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- fp32 attention (attn_f32.hip), shared by the decode and prefill entries ----
+struct AttnF32Args {
+  const float* q;
+  int64_t q_stride;            // elements between query tokens
+  const int32_t* qo_indptr;    // [B+1] new-token offsets; null: one token per sequence
+  const float* k_pool;         // one layer, [P, ps, Hkv, D]
+  const float* v_pool;
+  int64_t num_pages;
+  int32_t page_size;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* last_len;
+  int32_t batch;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int32_t group;
+  float scale;                 // softmax scale, natural-exponent units
+  float* out;
+  int64_t out_stride;
+  int32_t row_tiles;           // set by attention_f32
+};
+// Launch on stream s; total_q = number of query tokens (B for decode).
+int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipStream_t s);
+
 }  // namespace nslg

@@ -827,8 +827,39 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     return fail(NSLG_EINVAL, "paged_decode: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_decode: GQA group %d > 16", group);
+  if (dtype == NSLG_F32) {
+    // fp32 pools: one query row per sequence through the fp32 attention kernel
+    if constexpr (kGrouped) {
+      return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: f16/bf16 only");
+    } else {
+      if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(NSLG_EUNSUPPORTED, "paged_decode: head_dim %d", head_dim);
+      if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
+        return fail(NSLG_EINVAL, "paged_decode: row stride smaller than Hq*D");
+      AttnF32Args a;
+      a.q = (const float*)q;
+      a.q_stride = q_stride;
+      a.qo_indptr = nullptr;
+      a.k_pool = (const float*)k_pool;
+      a.v_pool = (const float*)v_pool;
+      a.num_pages = num_pages;
+      a.page_size = page_size;
+      a.indptr = kv_indptr;
+      a.indices = kv_indices;
+      a.last_len = kv_last_page_len;
+      a.batch = batch;
+      a.num_qo_heads = num_qo_heads;
+      a.num_kv_heads = num_kv_heads;
+      a.group = group;
+      a.scale = sm_scale;
+      a.out = (float*)out;
+      a.out_stride = out_stride;
+      a.row_tiles = 0;
+      return attention_f32(a, batch, head_dim, as_stream(stream));
+    }
+  }
   if (dtype != NSLG_F16 && dtype != NSLG_BF16)
-    return fail(NSLG_EUNSUPPORTED, "paged_decode: dtype %d (f16/bf16 only)", dtype);
+    return fail(NSLG_EUNSUPPORTED, "paged_decode: dtype %d", dtype);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(NSLG_EUNSUPPORTED, "paged_decode: head_dim %d", head_dim);
   if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
@@ -914,6 +945,7 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
                                                    int64_t total_pages, int32_t page_size,
                                                    int32_t dtype) {
   if (!shape_ok(batch, num_qo_heads, num_kv_heads, head_dim, total_pages, page_size)) return 0;
+  if (dtype == NSLG_F32) return 256;  // the fp32 path keeps its state on chip
   const DecodeShape sh = shape_of<false>(dtype, head_dim, batch, num_kv_heads, total_pages * page_size, page_size);
   return workspace_bytes_for(sh, batch, num_qo_heads, head_dim, 1, 0);
 }
@@ -924,6 +956,7 @@ extern "C" size_t nslg_paged_decode_grouped_workspace_size(int32_t batch, int32_
                                                            int32_t dtype, int32_t num_groups) {
   if (!shape_ok(batch, num_qo_heads, num_kv_heads, head_dim, total_pages, page_size)) return 0;
   if (num_groups < 1 || num_groups > kMaxGroups) return 0;
+  if (dtype == NSLG_F32) return 0;  // grouped decode runs on the 16-bit MFMA path only
   const int group = num_qo_heads / num_kv_heads;
   if (group > kGroupCols) return 0;
   const DecodeShape sh =

@@ -500,8 +500,33 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
     return fail(NSLG_EINVAL, "paged_prefill: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_prefill: GQA group %d > 16", group);
+  if (dtype == NSLG_F32) {
+    // fp32 pools: the fp32 attention kernel, ragged rows, bottom-right causal
+    if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
+      return fail(NSLG_EINVAL, "paged_prefill: row stride smaller than Hq*D");
+    AttnF32Args a;
+    a.q = (const float*)q;
+    a.q_stride = q_stride;
+    a.qo_indptr = qo_indptr;
+    a.k_pool = (const float*)k_pool;
+    a.v_pool = (const float*)v_pool;
+    a.num_pages = num_pages;
+    a.page_size = page_size;
+    a.indptr = kv_indptr;
+    a.indices = kv_indices;
+    a.last_len = kv_last_page_len;
+    a.batch = batch;
+    a.num_qo_heads = num_qo_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.group = group;
+    a.scale = sm_scale;
+    a.out = (float*)out;
+    a.out_stride = out_stride;
+    a.row_tiles = 0;
+    return attention_f32(a, total_q, head_dim, as_stream(stream));
+  }
   if (dtype != NSLG_F16 && dtype != NSLG_BF16)
-    return fail(NSLG_EUNSUPPORTED, "paged_prefill: dtype %d (f16/bf16 only)", dtype);
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: dtype %d", dtype);
   if (head_dim != 64 && head_dim != 128)
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: head_dim %d (64 or 128)", head_dim);
   if (num_kv_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many KV heads");

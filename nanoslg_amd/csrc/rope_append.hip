@@ -7,7 +7,8 @@
 // q_out == q); k_new and v_new are only read.
 //
 // Arithmetic is that of the eager tensor expression it replaces, element by
-// element in the 16-bit storage type (each product and the sum rounded to it):
+// element in the storage type (each product and the sum rounded to it; fp16, bf16
+// or fp32):
 //   c = rnd(cos[pos][d]), s = rnd(sin[pos][d])
 //   out[d] = rnd(rnd(x[d] * c) + rnd(rot[d] * s)),  rot = cat(-x[H:], x[:H])
 // A 16-bit times 16-bit product is exact in fp32 and the sum is done in fp32, as
@@ -128,6 +129,90 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeArgs a) {
   }
 }
 
+// fp32 storage: the same items, 8 floats (two 16 B vectors) per half; the products
+// are kept apart from the add so each is rounded on its own, as in the eager ops.
+__device__ inline float rope_elem_f32(float x, float c, float r, float s) {
+  float a = x * c;
+  float b = r * s;
+  asm volatile("" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) rope_append_f32_kernel(RopeArgs a) {
+  constexpr int H = D / 2;
+  constexpr int W = 8;
+  constexpr int kRotPerHead = H / W;
+  constexpr int kCopyPerHead = D / W;
+  const int64_t t = blockIdx.x;
+  int pos = a.positions[t];
+  pos = pos < 0 ? 0 : (pos >= a.table_rows ? (int)(a.table_rows - 1) : pos);
+  const int32_t slot = a.slots[t];
+  const bool write = slot >= 0 && (int64_t)slot < a.pool_slots;
+  const int64_t row_elems = (int64_t)a.num_kv_heads * D;
+  const float* crow = a.cos + (int64_t)pos * a.table_stride;
+  const float* srow = a.sin + (int64_t)pos * a.table_stride;
+  const float* q = reinterpret_cast<const float*>(a.q);
+  float* q_out = reinterpret_cast<float*>(a.q_out);
+  const float* k = reinterpret_cast<const float*>(a.k);
+  const float* v = reinterpret_cast<const float*>(a.v);
+  float* k_pool = reinterpret_cast<float*>(a.k_pool);
+  float* v_pool = reinterpret_cast<float*>(a.v_pool);
+  const int rot_items = (a.num_qo_heads + (write ? a.num_kv_heads : 0)) * kRotPerHead;
+  const int items = rot_items + (write ? a.num_kv_heads * kCopyPerHead : 0);
+  for (int i = threadIdx.x; i < items; i += blockDim.x) {
+    if (i < rot_items) {
+      const int head = i / kRotPerHead;
+      const int j = (i % kRotPerHead) * W;
+      const float* src;
+      float* dst;
+      if (head < a.num_qo_heads) {
+        src = q + t * a.q_stride + (int64_t)head * D;
+        dst = q_out + t * a.q_out_stride + (int64_t)head * D;
+      } else {
+        const int kh = head - a.num_qo_heads;
+        src = k + t * a.k_stride + (int64_t)kh * D;
+        dst = k_pool + (int64_t)slot * row_elems + (int64_t)kh * D;
+      }
+      float lo[8], hi[8], c_lo[8], c_hi[8], s_lo[8], s_hi[8];
+      load8f(src + j, lo);
+      load8f(src + H + j, hi);
+      load8f(crow + j, c_lo);
+      load8f(crow + H + j, c_hi);
+      load8f(srow + j, s_lo);
+      load8f(srow + H + j, s_hi);
+      float o_lo[8], o_hi[8];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        o_lo[e] = rope_elem_f32(lo[e], c_lo[e], -hi[e], s_lo[e]);  // d < H: rot = -x[d + H]
+        o_hi[e] = rope_elem_f32(hi[e], c_hi[e], lo[e], s_hi[e]);   // d >= H: rot = x[d - H]
+      }
+      *reinterpret_cast<f32x4*>(dst + j) = f32x4{o_lo[0], o_lo[1], o_lo[2], o_lo[3]};
+      *reinterpret_cast<f32x4*>(dst + j + 4) = f32x4{o_lo[4], o_lo[5], o_lo[6], o_lo[7]};
+      *reinterpret_cast<f32x4*>(dst + H + j) = f32x4{o_hi[0], o_hi[1], o_hi[2], o_hi[3]};
+      *reinterpret_cast<f32x4*>(dst + H + j + 4) = f32x4{o_hi[4], o_hi[5], o_hi[6], o_hi[7]};
+    } else {
+      const int kk = i - rot_items;
+      const int vh = kk / kCopyPerHead;
+      const int j = (kk % kCopyPerHead) * W;
+      const float* vs = v + t * a.v_stride + (int64_t)vh * D + j;
+      float* vd = v_pool + (int64_t)slot * row_elems + (int64_t)vh * D + j;
+      *reinterpret_cast<f32x4*>(vd) = *reinterpret_cast<const f32x4*>(vs);
+      *reinterpret_cast<f32x4*>(vd + 4) = *reinterpret_cast<const f32x4*>(vs + 4);
+    }
+  }
+}
+
+int launch_rope_f32(const RopeArgs& a, int64_t rows, int head_dim, hipStream_t s) {
+  const dim3 grid((unsigned)rows);
+  switch (head_dim) {
+    case 64: rope_append_f32_kernel<64><<<grid, 256, 0, s>>>(a); break;
+    case 128: rope_append_f32_kernel<128><<<grid, 256, 0, s>>>(a); break;
+    default: rope_append_f32_kernel<256><<<grid, 256, 0, s>>>(a); break;
+  }
+  return check_launch("rope_append");
+}
+
 template <typename T>
 int launch_rope(const RopeArgs& a, int64_t rows, int head_dim, hipStream_t s) {
   const dim3 grid((unsigned)rows);
@@ -164,8 +249,9 @@ extern "C" int nslg_rope_append(const void* q, int64_t q_stride, void* q_out, in
   if (!q || !q_out || !k_new || !v_new || !positions || !slot_mapping || !cos_table || !sin_table || !k_pool ||
       !v_pool)
     return fail(NSLG_EINVAL, "rope_append: null pointer");
-  if (dtype != NSLG_F16 && dtype != NSLG_BF16)
-    return fail(NSLG_EUNSUPPORTED, "rope_append: dtype %d (f16/bf16 only)", dtype);
+  if (dtype != NSLG_F16 && dtype != NSLG_BF16 && dtype != NSLG_F32)
+    return fail(NSLG_EUNSUPPORTED, "rope_append: dtype %d", dtype);
+  const int64_t es = elem_bytes(dtype);
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(NSLG_EUNSUPPORTED, "rope_append: head_dim %d", head_dim);
   const int64_t q_row = (int64_t)num_qo_heads * head_dim;
@@ -175,10 +261,10 @@ extern "C" int nslg_rope_append(const void* q, int64_t q_stride, void* q_out, in
     return fail(NSLG_EINVAL, "rope_append: row stride smaller than the row");
   if (((uintptr_t)q | (uintptr_t)q_out | (uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)k_pool |
        (uintptr_t)v_pool | (uintptr_t)cos_table | (uintptr_t)sin_table) & 15 ||
-      (q_stride | q_out_stride | k_stride | v_stride) % 8 || table_stride % 4)
+      ((q_stride | q_out_stride | k_stride | v_stride) * es) % 16 || table_stride % 4)
     return fail(NSLG_EINVAL, "rope_append: pointers and row strides must be 16-byte aligned");
-  const int64_t q_bytes = ((num_rows - 1) * q_stride + q_row) * 2;
-  const int64_t qo_bytes = ((num_rows - 1) * q_out_stride + q_row) * 2;
+  const int64_t q_bytes = ((num_rows - 1) * q_stride + q_row) * es;
+  const int64_t qo_bytes = ((num_rows - 1) * q_out_stride + q_row) * es;
   if (q_out != q || q_out_stride != q_stride) {
     if (overlaps(q, q_bytes, q_out, qo_bytes))
       return fail(NSLG_EINVAL, "rope_append: q_out overlaps q without being q itself");
@@ -204,5 +290,6 @@ extern "C" int nslg_rope_append(const void* q, int64_t q_stride, void* q_out, in
   a.num_qo_heads = num_qo_heads;
   a.num_kv_heads = num_kv_heads;
   hipStream_t s = as_stream(stream);
+  if (dtype == NSLG_F32) return launch_rope_f32(a, num_rows, head_dim, s);
   return dtype == NSLG_F16 ? launch_rope<F16>(a, num_rows, head_dim, s) : launch_rope<BF16>(a, num_rows, head_dim, s);
 }

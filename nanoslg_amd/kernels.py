@@ -15,6 +15,10 @@ from . import _lib
 
 _DTYPE_CODE = {torch.float16: _lib.NSLG_F16, torch.bfloat16: _lib.NSLG_BF16, torch.float32: _lib.NSLG_F32}
 
+# Pool dtypes nslg_paged_decode_grouped serves (its work units are 16-bit MFMA tiles);
+# decode batches of other pools are decoded per sequence.
+GROUPED_DECODE_DTYPES = (torch.float16, torch.bfloat16)
+
 
 def dtype_code(dt: torch.dtype) -> int:
     try:

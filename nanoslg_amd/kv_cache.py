@@ -1029,6 +1029,8 @@ class PagedKVCache(KVCacheManager):
         B = len(states)
         if B < 2 or getattr(self.kernels, "DecodeGroups", None) is None:
             return None
+        if self.cfg.dtype not in getattr(self.kernels, "GROUPED_DECODE_DTYPES", ()):
+            return None
         cfg = self.cfg
         M = 16 // max(1, cfg.num_qo_heads // cfg.num_kv_heads)
         if M < 2:

@@ -164,6 +164,10 @@ def decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_siz
     return t(out_ip), t(out_idx), t(out_lpl), t(slots), t(pos), t(new)
 
 
+# the stand-in groups decode rows of any pool dtype (grouping does not change results)
+GROUPED_DECODE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
 class DecodeGroups:
     """As nanoslg_amd.kernels.DecodeGroups (the grouping does not change results)."""
 

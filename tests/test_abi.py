@@ -85,7 +85,7 @@ def test_rope_append_argument_checks():
                                     a["slot"], a["n"], a["cos"], a["sin"], a["ts"], a["tr"], a["hq"], a["hkv"],
                                     a["d"], a["kp"], a["vp"], a["slots"], a["dt"], None)
     assert rope(d=96, ts=96) == -2
-    assert rope(dt=2) == -2
+    assert rope(dt=7) == -2  # no such dtype (f16, bf16 and f32 are supported)
     assert rope(pos=None) == -1
     assert rope(qs=4092) == -1  # row stride smaller than Hq*D
     assert rope(ks=1028) == -1  # not a multiple of 8 elements

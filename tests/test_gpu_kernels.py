@@ -287,6 +287,39 @@ def test_prefill_sequence_without_new_tokens():
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
 
 
+# ------------------------------------------------------------------ fp32 pools
+
+F32_TOL = dict(atol=2e-5, rtol=1e-4)  # fp32 kernel against fp32 SDPA: summation-order differences only
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_f32_decode_and_prefill(D):
+    """fp32 pools (the contiguous backend of an fp32 model) go through the fp32
+    attention kernel: decode rows and ragged causal prefill rows."""
+    _log(f"f32 decode/prefill D={D}")
+    out, ref = _decode_case([1, 17, 300, 1024, 0], 32, 8, D, 16, torch.float32, seed=60 + D)
+    torch.testing.assert_close(out, ref, **F32_TOL)
+    assert torch.count_nonzero(out[4]) == 0
+    out, ref = _prefill_case([37, 300, 1, 50], [37, 64, 1, 0], 32, 8, D, 16, torch.float32, seed=61 + D)
+    torch.testing.assert_close(out, ref, **F32_TOL)
+
+
+@pytest.mark.parametrize("Hq,Hkv,ps", [(48, 3, 16), (16, 1, 1), (8, 8, 48), (64, 8, 32)])
+def test_f32_groups_and_page_sizes(Hq, Hkv, ps):
+    _log(f"f32 Hq={Hq} Hkv={Hkv} ps={ps}")
+    out, ref = _decode_case([5, ps + 1, 700], Hq, Hkv, 128, ps, torch.float32, seed=Hq + ps, scale=0.07)
+    torch.testing.assert_close(out, ref, **F32_TOL)
+    out, ref = _prefill_case([130, 77, 400], [130, 20, 129], Hq, Hkv, 128, ps, torch.float32, seed=Hq * ps)
+    torch.testing.assert_close(out, ref, **F32_TOL)
+
+
+def test_f32_grouped_decode_is_rejected():
+    """Grouped (shared-prefix) decode runs on the 16-bit MFMA path only."""
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    assert lib.nslg_paged_decode_grouped_workspace_size(4, 32, 8, 128, 100, 16, _lib.NSLG_F32, 1) == 0
+
+
 def test_decode_workspace_reuse_across_calls():
     """One workspace serves a sequence of different batches (split-K partials of a
     call never leak into the next)."""

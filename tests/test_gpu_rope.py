@@ -33,7 +33,7 @@ def _oracle_rows(q, k, cos, sin, pos):
     return qr.reshape(q.shape), kr.reshape(k.shape)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (8, 8, 64), (16, 2, 256), (4, 1, 128)])
 def test_rope_append_bit_exact(dtype, Hq, Hkv, D):
     _log(f"rope_append dtype={dtype} Hq={Hq} Hkv={Hkv} D={D}")

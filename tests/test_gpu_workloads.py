@@ -20,6 +20,9 @@ pages are compared bit for bit.
                 suffixes U[128, 1024] prefilled in one ragged forward (15 copies),
                 then decode
   chunked prefill  8 prompts of 4096 tokens in 512-token chunks
+  contiguous fp32  the reference's own CPU case on the GPU: one sequence, a
+                512-token prompt, then 64 decode steps, fp32, against the oracle's
+                restatement of the contiguous path (kv_cache.py:227-379)
 """
 import math
 import sys
@@ -275,3 +278,33 @@ def test_chunked_prefill_full_size():
             _check_rows_written(mgr, sid, c * CH, k[b], v[b])
             torch.testing.assert_close(out[b].view(CH, HQ, D).float(), _reference(mgr, sid, q[b]),
                                        atol=ATOL, rtol=RTOL, msg=lambda m, c=c, sid=sid: f"chunk {c} {sid}: {m}")
+
+
+def test_contiguous_fp32_prompt_and_decode():
+    """Contiguous backend in fp32: a 512-token prompt of N(0,1) K/V, then 64 decode
+    steps (q ~ N(0,1) / sqrt(128)), each against the oracle's contiguous path run on
+    the same inputs; pool bytes equal to the oracle's after every step."""
+    _log("workload: contiguous fp32 (1 x 512 prompt + 64 decode steps)")
+    from nanoslg_amd import kv_cache as KC
+    Smax = 640
+    cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, max_batch_size=1,
+                           max_seq_len=Smax, dtype=torch.float32, device=DEV, backend="contiguous")
+    mgr = KC.ContiguousKVCache(cfg)
+    ref = O.ContiguousRef(1, 1, Smax, HKV, D)
+    for m in (mgr, ref):
+        m.allocate_sequence("s")
+    g = torch.Generator().manual_seed(7)
+    steps = [512] + [1] * 64
+    for n in steps:
+        q = torch.randn(1, n, HQ, D, generator=g) / math.sqrt(D)
+        k = torch.randn(1, n, HKV, D, generator=g)
+        v = torch.randn(1, n, HKV, D, generator=g)
+        c1, c2 = mgr.begin_forward(["s"], [n]), ref.begin_forward(["s"], [n])
+        o1 = c1.attend(0, q.to(DEV), k.to(DEV), v.to(DEV), HQ, HKV).cpu()
+        o2 = c2.attend(0, q, k, v, HQ, HKV)
+        assert o1.dtype == torch.float32
+        torch.testing.assert_close(o1, o2, atol=2e-5, rtol=1e-4)
+        mgr.end_forward(c1)
+        ref.end_forward(c2)
+    torch.cuda.synchronize()
+    assert torch.equal(mgr.k.cpu(), ref.k) and torch.equal(mgr.v.cpu(), ref.v)
