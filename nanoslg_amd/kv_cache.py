@@ -198,6 +198,20 @@ class KVCacheManager(ABC):
 # --------------------------------------------------------------------------------------
 
 
+_STREAMS: Dict[int, torch.cuda.Stream] = {}
+
+
+def _current_stream(index: int) -> torch.cuda.Stream:
+    """Device `index`'s current stream as a torch Stream (one object per stream id),
+    without the device lookup torch.cuda.current_stream() and Event.record() do on
+    every call (about 15 us each)."""
+    sid, di, dt = torch._C._cuda_getCurrentStream(index)
+    st = _STREAMS.get(sid)
+    if st is None:
+        st = _STREAMS[sid] = torch.cuda.Stream(stream_id=sid, device_index=di, device_type=dt)
+    return st
+
+
 class _PlanStaging:
     """Host-to-device staging of per-forward int32 plans on one device.
 
@@ -219,6 +233,7 @@ class _PlanStaging:
 
     def __init__(self, device: torch.device):
         self.device = device
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
         self.side = torch.cuda.Stream(device=device)  # default priority
         self.host: List[Optional[torch.Tensor]] = [None] * self.RING
         self.host_np: List[Optional[np.ndarray]] = [None] * self.RING
@@ -246,9 +261,9 @@ class _PlanStaging:
             dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
             if total:
                 (dev if total == dev.numel() else dev[:total]).copy_(buf[:total], non_blocking=True)
-            self.copied[k].record()  # on the current (compute) stream
+            self.copied[k].record(_current_stream(self.index))  # on the compute stream
             return dev
-        main = torch.cuda.current_stream(self.device)
+        main = _current_stream(self.index)
         with torch.cuda.stream(self.side):
             dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
             dev[:total].copy_(buf[:total], non_blocking=True)
@@ -443,7 +458,9 @@ class PagePool:
         with self._lock:
             if len(self._free) < n:
                 return None
-            out = [self._free.pop() for _ in range(n)]
+            # the same pages, in the same order, as n pops from the end of the stack
+            out = self._free[:-n - 1:-1] if n else []
+            del self._free[len(self._free) - n:]
             idx = np.asarray(out, np.int64)
             self.ref_count[idx] = 1
             self.tokens_used[idx] = 0
@@ -1526,6 +1543,7 @@ class DecodeGraph:
         self.new_np = [t.numpy() for t in self.new_host]
         self.new_dev = [torch.zeros(B, dtype=torch.int32, device=dev) for _ in range(2)]
         self.done = [torch.cuda.Event() for _ in range(2)]
+        self.dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
         self.used = [False, False]
         L, P = cfg.num_layers, cfg.max_pages
         self.pool_args = (pool.k.data_ptr(), pool.v.data_ptr(), L, P, cfg.num_kv_heads, cfg.head_dim,
@@ -1591,7 +1609,7 @@ class DecodeGraph:
         ctx.start_positions = start.tolist()
         ctx.seq_lens = (start + 1).tolist()
         self.graphs[i].replay()
-        self.done[i].record()
+        self.done[i].record(_current_stream(self.dev_index))
         self.used[i] = True
         for st in self.states:
             st.num_tokens += 1
