@@ -320,6 +320,33 @@ def test_f32_grouped_decode_is_rejected():
     assert lib.nslg_paged_decode_grouped_workspace_size(4, 32, 8, 128, 100, 16, _lib.NSLG_F32, 1) == 0
 
 
+def test_decode_large_batches():
+    """Batches larger than half the device's resident chunk slots take the
+    several-rounds launch; more than 256 sequences go past the lengths a wave
+    keeps in registers. Mixed lengths (empty ones included) and many short ones."""
+    rng = np.random.default_rng(70)
+    lens = rng.integers(0, 3000, size=400).tolist()
+    lens[:3] = [0, 1, 16]
+    _log(f"decode large batch B={len(lens)}")
+    out, ref = _decode_case(lens, 32, 8, 128, 16, torch.float16, seed=70)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    lens = rng.integers(1, 65, size=2000).tolist()
+    _log(f"decode large batch B={len(lens)}")
+    out, ref = _decode_case(lens, 32, 8, 128, 16, torch.bfloat16, seed=71)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_large_ragged_batch():
+    """100 sequences with 0..64 new tokens over cached contexts of up to 2000 tokens."""
+    rng = np.random.default_rng(72)
+    news = rng.integers(0, 65, size=100).tolist()
+    lens = [n + int(c) for n, c in zip(news, rng.integers(0, 2000, size=100))]
+    lens[0], news[0] = 0, 0
+    _log(f"prefill large ragged batch B={len(lens)} T={sum(news)}")
+    out, ref = _prefill_case(lens, news, 32, 8, 128, 16, torch.float16, seed=72)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
 def test_decode_workspace_reuse_across_calls():
     """One workspace serves a sequence of different batches (split-K partials of a
     call never leak into the next)."""
