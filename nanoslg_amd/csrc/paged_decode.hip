@@ -584,22 +584,35 @@ struct MergeParams {
   int64_t out_stride;
 };
 
-// Merge of the split-K partials: one wave per (sequence, query head). Sequences
-// with several partials (chunks of their own tokens, and of their group's prefix)
-// are merged; empty sequences get zero rows; sequences with a single chunk and no
-// group were finished by the decode kernel. The wave reads its sequence's chunk
-// ranges (one round of loads), then the partials' (m, l) with lanes over partials
-// and the first rows of O with lanes over (partial, d) in one more round: O row c
-// is D floats, D/4 lanes read it as float4s, 64/(D/4) rows per load.
-template <typename T, int D, bool kGrouped>
+// Merge of the split-K partials: one wave per (sequence, query head), or, when the
+// sequences average more than kSplitMergeChunks partials, one workgroup of 4 waves
+// per (sequence, query head), each wave over a quarter of the partials. Sequences with several partials
+// (chunks of their own tokens, and of their group's prefix) are merged; empty
+// sequences get zero rows; sequences with a single chunk and no group were finished
+// by the decode kernel. A wave reads the sequence's chunk range (one round of
+// loads), then its partials' (m, l) with lanes over partials and the first rows of
+// O with lanes over (partial, d) in one more round: O row c is D floats, D/4 lanes
+// read it as float4s, 64/(D/4) rows per load. The four waves' (m, l, O), each
+// relative to its own max, are combined through LDS by the first wave. Splitting a
+// sequence's partials over 4 waves shortens the chain of dependent load rounds for
+// sequences with many chunks (small batches: ~100 chunks each; measured 6.5 -> 4.2
+// us at 4 sequences), and costs more than it saves at a few chunks each (5.3 ->
+// 8.8 us at 64 sequences of ~6 chunks).
+constexpr int kSplitMergeChunks = 32;
+template <typename T, int D, bool kGrouped, bool kSplit>
 __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupArgs<kGrouped> ga) {
   constexpr int LPC = D / 4;     // lanes per O row
   constexpr int CPI = 64 / LPC;  // O rows per load instruction
   constexpr int kBatch = 8;      // load instructions per lane in flight
+  constexpr int kParts = 4;      // kSplit: waves per (sequence, query head), a quarter of the chunks each
+  __shared__ float s_m[kParts], s_l[kParts];
+  __shared__ __attribute__((aligned(16))) float s_o[kParts][D];
   const int b = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int hq = blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (hq >= p.num_qo_heads) return;
+  // kSplit: the workgroup's 4 waves share one query head; else each wave has its own
+  const int hq = kSplit ? blockIdx.y : blockIdx.y * 4 + wave;
+  if (!kSplit && hq >= p.num_qo_heads) return;
   const int len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
   const int2 mt = p.meta[b];
   const int sub = lane / LPC;
@@ -607,7 +620,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupA
   uint16_t* orow = p.out + (int64_t)b * p.out_stride + (int64_t)hq * D + d0;
   if (len == 0) {
     // A sequence with no tokens attends to nothing: its output rows are zero.
-    if (sub == 0) *reinterpret_cast<u16x4*>(orow) = u16x4{0, 0, 0, 0};
+    if ((!kSplit || wave == 0) && sub == 0) *reinterpret_cast<u16x4*>(orow) = u16x4{0, 0, 0, 0};
     return;
   }
   // own chunks [cstart, cstart + nown) at member slot 0; the group prefix's chunks
@@ -630,7 +643,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupA
   int nown = own > 0 ? mt.y : 0;
   if (nown > 0 && (cstart < 0 || cstart >= p.max_chunks)) nown = 0;
   if (cstart + nown > p.max_chunks) nown = p.max_chunks - cstart;
-  if (ngrp == 0 && nown <= 1) return;
+  if (ngrp == 0 && nown <= 1) return;  // uniform over the workgroup
   const int nchunks = nown + ngrp;
 
   // partial k of the sequence -> its slot
@@ -639,56 +652,92 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupA
                                 : (int64_t)(gstart + k - nown) * p.slot_members + member;
     return ck * p.num_qo_heads + hq;
   };
-  f32x4 oc[kBatch];
-  float mc[kBatch];
-  auto load_rows = [&](int c0) {
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int64_t sl = slot_of(min(c0 + CPI * k + sub, nchunks - 1));
-      oc[k] = *reinterpret_cast<const f32x4*>(p.part_o + sl * D + d0);
-      mc[k] = p.part_ml[sl * 2];
-    }
-  };
-  load_rows(0);  // in flight with the (m, l) pass below
+  // this wave's chunks [k0, k0 + cnt)
+  const int per = kSplit ? (nchunks + kParts - 1) / kParts : nchunks;
+  const int k0 = kSplit ? wave * per : 0;
+  const int cnt = min(nchunks, k0 + per) - k0;
 
-  // the running max M and the denominator sum_c 2^(m_c - M) l_c, lanes over chunks
   float mmax = -INFINITY, lsum = 0.f;
-  for (int c = lane; c < nchunks; c += 64) {
-    const float2 v = *reinterpret_cast<const float2*>(p.part_ml + slot_of(c) * 2);
-    const float m_new = fmaxf(mmax, v.x);
-    lsum = lsum * fast_exp2(mmax - m_new) + v.y * fast_exp2(v.x - m_new);
-    mmax = m_new;
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float om = __shfl_xor(mmax, off, 64);
-    const float ol = __shfl_xor(lsum, off, 64);
-    const float m_new = fmaxf(mmax, om);
-    lsum = (mmax == -INFINITY ? 0.f : lsum * fast_exp2(mmax - m_new)) +
-           (om == -INFINITY ? 0.f : ol * fast_exp2(om - m_new));
-    mmax = m_new;
-  }
-
-  // sum_c 2^(m_c - M) O_c over the lane's rows, then over the CPI rows of a load
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < nchunks; c0 += CPI * kBatch) {
-    if (c0 > 0) load_rows(c0);
+  if (cnt > 0) {
+    f32x4 oc[kBatch];
+    float mc[kBatch];
+    auto load_rows = [&](int c0) {
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const float w = c0 + CPI * k + sub < nchunks ? fast_exp2(mc[k] - mmax) : 0.f;
-      acc += w * oc[k];
+      for (int k = 0; k < kBatch; ++k) {
+        const int64_t sl = slot_of(k0 + min(c0 + CPI * k + sub, cnt - 1));
+        oc[k] = *reinterpret_cast<const f32x4*>(p.part_o + sl * D + d0);
+        mc[k] = p.part_ml[sl * 2];
+      }
+    };
+    load_rows(0);  // in flight with the (m, l) pass below
+
+    // the running max M and the denominator sum_c 2^(m_c - M) l_c, lanes over chunks
+    for (int c = lane; c < cnt; c += 64) {
+      const float2 v = *reinterpret_cast<const float2*>(p.part_ml + slot_of(k0 + c) * 2);
+      const float m_new = fmaxf(mmax, v.x);
+      lsum = lsum * fast_exp2(mmax - m_new) + v.y * fast_exp2(v.x - m_new);
+      mmax = m_new;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float om = __shfl_xor(mmax, off, 64);
+      const float ol = __shfl_xor(lsum, off, 64);
+      const float m_new = fmaxf(mmax, om);
+      lsum = (mmax == -INFINITY ? 0.f : lsum * fast_exp2(mmax - m_new)) +
+             (om == -INFINITY ? 0.f : ol * fast_exp2(om - m_new));
+      mmax = m_new;
+    }
+
+    // sum_c 2^(m_c - M) O_c over the lane's rows, then over the CPI rows of a load
+    for (int c0 = 0; c0 < cnt; c0 += CPI * kBatch) {
+      if (c0 > 0) load_rows(c0);
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const float w = c0 + CPI * k + sub < cnt ? fast_exp2(mc[k] - mmax) : 0.f;
+        acc += w * oc[k];
+      }
+    }
+#pragma unroll
+    for (int off = LPC; off < 64; off <<= 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], off, 64);
     }
   }
+  if constexpr (!kSplit) {
+    if (sub == 0) {
+      const float inv = 1.f / lsum;
+      u16x4 w16;
 #pragma unroll
-  for (int off = LPC; off < 64; off <<= 1) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], off, 64);
+      for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(acc[j] * inv);
+      *reinterpret_cast<u16x4*>(orow) = w16;
+    }
+    return;
   }
-  if (sub == 0) {
-    const float inv = 1.f / lsum;
+  if (lane == 0) {
+    s_m[wave] = mmax;
+    s_l[wave] = lsum;
+  }
+  if (sub == 0) *reinterpret_cast<f32x4*>(&s_o[wave][d0]) = acc;
+  __syncthreads();
+  if (wave == 0 && sub == 0) {
+    // the waves' parts, each relative to its own max: rescale to the common one
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kParts; ++w) M = fmaxf(M, s_m[w]);
+    float L = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kParts; ++w) {
+      if (s_m[w] == -INFINITY) continue;
+      const float f = fast_exp2(s_m[w] - M);
+      L += f * s_l[w];
+      o += f * *reinterpret_cast<const f32x4*>(&s_o[w][d0]);
+    }
+    const float inv = 1.f / L;
     u16x4 w16;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(acc[j] * inv);
+    for (int j = 0; j < 4; ++j) w16[j] = T::from_f32(o[j] * inv);
     *reinterpret_cast<u16x4*>(orow) = w16;
   }
 }
@@ -789,7 +838,11 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, const GroupArgs<
     paged_decode_kernel<T, D, false, 2, kGrouped><<<grid, 64 * waves, 0, s>>>(p, ga);
   int rc = check_launch("paged_decode");
   if (rc) return rc;
-  decode_merge_kernel<T, D, kGrouped><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp, ga);
+  // sequences of many chunks (small batches) split their partials over 4 waves
+  if (p.max_chunks > kSplitMergeChunks * p.batch)
+    decode_merge_kernel<T, D, kGrouped, true><<<dim3(p.batch, p.num_qo_heads), 256, 0, s>>>(mp, ga);
+  else
+    decode_merge_kernel<T, D, kGrouped, false><<<dim3(p.batch, (p.num_qo_heads + 3) / 4), 256, 0, s>>>(mp, ga);
   return check_launch("paged_decode_merge");
 }
 
@@ -827,6 +880,7 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     return fail(NSLG_EINVAL, "paged_decode: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_decode: GQA group %d > 16", group);
+  if (num_qo_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_decode: %d query heads", num_qo_heads);
   if (dtype == NSLG_F32) {
     // fp32 pools: one query row per sequence through the fp32 attention kernel
     if constexpr (kGrouped) {
