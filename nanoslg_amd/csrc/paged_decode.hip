@@ -328,8 +328,14 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
     const int64_t usable = (int64_t)p.chunk_budget - lens.units;
     int64_t hi = (t_all + usable - 1) / usable;
     hi = ((hi + 15) / 16) * 16;
-    hi = hi < 64 ? 64 : (hi > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : hi);
-    ct = fit_chunk_tokens<kGrouped>(p, ga, lens, 64, (int)hi, p.chunk_budget);
+    // Shortest chunk: a chunk costs a fixed set-up and a partial to merge, so small
+    // batches (where the slots are not the limit) take fewer, longer chunks: about
+    // t_all / 96 tokens, between 64 and 256 (measured best at 4 sequences of 1k-4k
+    // tokens and at 16-64 sequences of 1k-2k; large batches are bounded by `hi`).
+    int64_t lo = ((t_all / 96 + 15) / 16) * 16;
+    lo = lo < 64 ? 64 : (lo > 256 ? 256 : lo);
+    hi = hi < lo ? lo : (hi > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : hi);
+    ct = fit_chunk_tokens<kGrouped>(p, ga, lens, (int)lo, (int)hi, p.chunk_budget);
   }
   int u = 0, cstart = 0, nchunks = 0;
   if (!locate_chunk<kGrouped>(p, ga, lens, ct, chunk, u, cstart, nchunks)) return;
