@@ -200,7 +200,9 @@ int nslg_paged_decode_grouped(const void* q, int64_t q_stride,
  *               [qo_indptr[b], qo_indptr[b+1]) and sit at the LAST positions of
  *               that sequence's L_b tokens (bottom-right causal alignment):
  *               row t of b attends to keys j <= L_b - n_b + t.
- *   total_q     host copy of qo_indptr[batch]; max_q: host max of n_b
+ *   total_q     host copy of qo_indptr[batch]; max_q: host max of n_b (sizes the
+ *               longest-first tile order of near-uniform batches; a value below
+ *               the true max only costs that order, never correctness)
  *   out         [T] rows of Hq*D elements at stride out_stride
  *   sm_scale    positive and finite (EINVAL otherwise)
  * Supported: f16, bf16 with D in {64, 128} (MFMA); f32 with D in {64, 128, 256}

@@ -65,6 +65,7 @@ struct PrefillParams {
   int32_t row_tiles;  // row-tile slots per KV head (an upper bound over the batch)
   int32_t num_work;   // row_tiles * num_kv_heads
   int32_t per_xcd;    // ceil(num_work / 8)
+  int32_t by_round;   // > 0: longest-first rounds of this many tiles per sequence (see below)
 };
 
 template <int N>
@@ -78,6 +79,38 @@ __device__ inline int kv_len_of(const PrefillParams& p, int s) {
   int lpl = p.last_len[s];
   lpl = lpl < 1 ? 1 : (lpl > p.page_size ? p.page_size : lpl);
   return (np - 1) * p.page_size + lpl;
+}
+
+// Longest first: slot g is round r = g / batch of sequence g % batch, and round r
+// takes each sequence's r-th tile from the end. A later row tile sees more keys
+// (causal), so the first slots dispatched carry the most work and the short tiles
+// fill in behind them. Slots past a sequence's tiles are empty.
+__device__ inline bool locate_tile_by_round(const PrefillParams& p, int g, int& b, int& tile) {
+  b = g % p.batch;
+  const int r = g / p.batch;
+  const int n = p.qo_indptr[b + 1] - p.qo_indptr[b];
+  const int nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+  if (r >= nt) return false;
+  tile = nt - 1 - r;
+  return true;
+}
+
+// Most row tiles of any sequence of the batch (wave-wide, uniform).
+__device__ inline int most_tiles(const PrefillParams& p) {
+  const int lane = threadIdx.x & 63;
+  int most = 0;
+  for (int s0 = 0; s0 < p.batch; s0 += 64) {
+    const int s = s0 + lane;
+    int nt = 0;
+    if (s < p.batch) {
+      const int n = p.qo_indptr[s + 1] - p.qo_indptr[s];
+      nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) nt = max(nt, __shfl_xor(nt, off, 64));
+    most = max(most, nt);
+  }
+  return __builtin_amdgcn_readfirstlane(most);
 }
 
 // Wave-wide search for the (sequence, row tile) of workgroup x.
@@ -132,7 +165,12 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   if (w >= p.num_work) return;
   const int h = w / p.row_tiles;
   int b = 0, tile = 0;
-  if (!locate_tile(p, w - h * p.row_tiles, b, tile)) return;  // uniform across the workgroup
+  const int g = w - h * p.row_tiles;
+  // longest-first rounds when the host's round count covers every sequence (it came
+  // from the caller's max_q); otherwise the packed order, which the grid also fits
+  const bool rounds = p.by_round > 0 && most_tiles(p) <= p.by_round;
+  if (!(rounds ? locate_tile_by_round(p, g, b, tile) : locate_tile(p, g, b, tile)))
+    return;  // uniform across the workgroup
   b = __builtin_amdgcn_readfirstlane(b);
   tile = __builtin_amdgcn_readfirstlane(tile);
 
@@ -485,7 +523,6 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
                                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                                   float sm_scale, int32_t dtype, void* out, int64_t out_stride,
                                   void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
-  (void)max_q;
   (void)workspace;
   (void)workspace_bytes;
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
@@ -559,8 +596,18 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
   p.out = (uint16_t*)out;
   p.out_stride = out_stride;
   if (tiles * num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
-  p.row_tiles = (int32_t)tiles;
-  p.num_work = (int32_t)(tiles * num_kv_heads);
+  // Longest-first rounds need batch x (most tiles of a sequence) slots; taken when
+  // that is at most 5/4 of the slots of the packed order (near-uniform batches,
+  // such as the chunks of a batch of prompts), so few slots are empty.
+  // The grid fits both orders; the kernel checks the rounds against the batch.
+  const int64_t most = max_q > 0 ? ((int64_t)max_q * group + kRowsPerWG - 1) / kRowsPerWG : 0;
+  const int64_t round_slots = (int64_t)batch * most;
+  const bool by_round = most > 0 && most <= 0x7fffffff && 4 * round_slots <= 5 * tiles;
+  p.by_round = by_round ? (int32_t)most : 0;
+  const int64_t slots = by_round && round_slots > tiles ? round_slots : tiles;
+  if (slots * num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
+  p.row_tiles = (int32_t)slots;
+  p.num_work = (int32_t)(slots * num_kv_heads);
   p.per_xcd = (p.num_work + 7) / 8;
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) return head_dim == 64 ? launch_prefill<F16, 64>(p, tiles, s) : launch_prefill<F16, 128>(p, tiles, s);

@@ -228,7 +228,7 @@ def test_decode_rejects_bad_arguments():
 # ------------------------------------------------------------------ prefill attention
 
 
-def _prefill_case(lens, news, Hq, Hkv, D, ps, dtype, seed, scale=None):
+def _prefill_case(lens, news, Hq, Hkv, D, ps, dtype, seed, scale=None, max_q=None):
     g = torch.Generator().manual_seed(seed)
     npg = sum(math.ceil(L / ps) for L in lens)
     P = npg + 4
@@ -239,7 +239,8 @@ def _prefill_case(lens, news, Hq, Hkv, D, ps, dtype, seed, scale=None):
     tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, seed)
     qo = np.zeros(len(lens) + 1, np.int32)
     qo[1:] = np.cumsum(news)
-    out = _k().paged_prefill(q.to(DEV), torch.from_numpy(qo).to(DEV), T, max(news), k.to(DEV), v.to(DEV),
+    out = _k().paged_prefill(q.to(DEV), torch.from_numpy(qo).to(DEV), T, max(news) if max_q is None else max_q,
+                             k.to(DEV), v.to(DEV),
                              torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV),
                              torch.from_numpy(lpl).to(DEV), sm_scale=scale)
     torch.cuda.synchronize()
@@ -279,6 +280,19 @@ def test_prefill_long_chunk_and_page_window():
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
     out, ref = _prefill_case([4500], [70], 32, 8, 128, 1, torch.float16, seed=51)
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
+def test_prefill_row_tile_orders():
+    """Near-uniform batches run their row tiles longest first (rounds sized by the
+    host's max_q); a max_q below a sequence's new tokens, or a ragged batch, takes the
+    packed order. Same results either way."""
+    _log("prefill tile orders")
+    lens, news = [1500, 1400, 1300, 1200], [512, 512, 500, 480]
+    # exact: rounds; understated: the kernel finds a sequence with more tiles than the
+    # rounds cover and packs; far overstated: too many empty slots, packed by the host
+    for max_q in (None, 1, 4096):
+        out, ref = _prefill_case(lens, news, 32, 8, 128, 16, torch.float16, seed=53, max_q=max_q)
+        torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
 
 
 def test_prefill_sequence_without_new_tokens():
