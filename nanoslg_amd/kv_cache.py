@@ -731,6 +731,10 @@ class PagedCacheContext(CacheContext):
             pid = int(st.bt[p])
             new = pool.cow_alloc(pid)
             if new is None:
+                # The copies made so far stand (the reference copies each page as it
+                # goes, kv_cache.py:429-436, and does not undo them on the error).
+                if cow_src:
+                    pool.copy(cow_src, cow_dst)
                 raise RuntimeError("KV OOM during CoW")
             cow_src.append(pid)
             cow_dst.append(new)
@@ -1183,7 +1187,14 @@ class PagedKVCache(KVCacheManager):
             for st, k in grow:
                 st.extend(self._alloc(k, defer_zero=True))
         zero, self._pending_zero = self._pending_zero, []
-        return PagedCacheContext(self, seq_ids, ntoks, offsets, zero_pages=zero)
+        try:
+            return PagedCacheContext(self, seq_ids, ntoks, offsets, zero_pages=zero)
+        except RuntimeError:
+            # the pages this call took stay with their sequences and are zeroed, as
+            # allocation zeroes them (kv_cache.py:411), whatever stopped the forward
+            if zero:
+                self.pool.zero(zero)
+            raise
 
     def end_forward(self, ctx):
         for b in range(ctx.batch_size):

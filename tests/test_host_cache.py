@@ -182,6 +182,43 @@ def test_cow_oom_raises():
         mgr.begin_forward(["x"], [1])
 
 
+def test_cow_oom_keeps_the_copies_already_made():
+    """Three sequences share a partial page; the pool holds one more page. A decode
+    forward of all three copies the page for the first writer, then runs out at the
+    second: RuntimeError, as in the reference, whose first copy already happened
+    (kv_cache.py:429-436, 586-591). The first sequence reads the same K/V as before,
+    through its new page, on both sides."""
+    g = torch.Generator().manual_seed(11)
+    mgr, ref = make(ps=4, pages=6, prefix=False)
+    for impl in (mgr, ref):
+        impl.allocate_sequence("a")
+    forward_both(mgr, ref, ["a"], [6], [0], g)          # pages: 4 tokens + 2 in a partial page
+    for impl in (mgr, ref):
+        st = impl.seqs["a"]
+        pages = list(st.block_table)
+        for sid in ("b", "c"):
+            impl.allocate_sequence(sid)
+            for p in pages:
+                impl.pool.add_ref(p)
+            nst = impl.seqs[sid]
+            if hasattr(nst, "bt"):
+                nst.extend(pages)
+            else:
+                nst.block_table = list(pages)
+            nst.num_tokens = 6
+        impl.allocate_sequence("filler", num_tokens=8)  # two of the three free pages
+    assert mgr.pool.num_free == ref.pool.num_free == 1
+    before = logical(mgr, "a", 0)
+    with pytest.raises(RuntimeError, match="KV OOM during CoW"):
+        mgr.begin_forward(["a", "b", "c"], [1, 1, 1])
+    with pytest.raises(RuntimeError, match="KV OOM during CoW"):
+        ref.begin_forward(["a", "b", "c"], [1, 1, 1])
+    assert mgr.seqs["a"].block_table[-1] != mgr.seqs["b"].block_table[-1]  # a moved to its copy
+    after = logical(mgr, "a", 0)
+    assert torch.equal(before[0], after[0]) and torch.equal(before[1], after[1])
+    check_state(mgr, ref, ["a", "b", "c"])
+
+
 def test_kv_oom_message_and_eviction():
     mgr, ref = make(pages=6, prefix=True)
     with pytest.raises(RuntimeError, match=r"KV OOM: need 6, free 5"):

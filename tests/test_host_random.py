@@ -1,0 +1,183 @@
+"""Randomised serving traffic through the host layer against the oracle.
+
+Each seed drives one PagedKVCache (CPU stand-in kernels, tests/fake_kernels.py) and
+the oracle's PagedRef with the same stream of calls, the way nanoslg's worker
+drives its manager (worker.py:169-213, 398-426; kv_cache.py:707-777):
+
+  * admissions with token ids from a 3-symbol vocabulary, so prompts share
+    prefixes and the radix tree matches, inserts and evicts pages;
+  * ragged prefill forwards of several admitted sequences with left padding
+    (input offsets), decode forwards of every running sequence (steady decode
+    batches are planned on the device after the first);
+  * partial pages shared by reference (add_ref, as kv_cache.py:713 does for full
+    pages) so that the next write copies them (copy-on-write order rule);
+  * releases (which cache the full pages in the tree) and OOM on both sides.
+
+After every forward: outputs (rows with new tokens), positions, the number of
+copy-on-writes, free pages, cached pages and every sequence's K/V read through
+its block table are compared; pad rows must be zero."""
+import random
+
+import pytest
+import torch
+
+import fake_kernels as FK
+from nanoslg_amd import kv_cache as KC
+from oracle import kv_oracle as O
+
+L, HQ, HKV, D = 2, 4, 2, 8
+
+
+def _make(ps, pages):
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
+                           max_pages=pages, dtype=torch.float32, device=None, enable_prefix_caching=True,
+                           backend="paged")
+    return KC.PagedKVCache(cfg, kernels=FK), O.PagedRef(L, pages, ps, HKV, D, torch.float32,
+                                                        enable_prefix_caching=True)
+
+
+def _logical(cache, sid, layer, ps):
+    st = cache.seqs[sid]
+    bt = st.block_table
+    n = st.num_tokens
+    if n == 0:
+        return None, None
+    k = torch.stack([cache.pool.k[layer, bt[t // ps], t % ps] for t in range(n)])
+    v = torch.stack([cache.pool.v[layer, bt[t // ps], t % ps] for t in range(n)])
+    return k, v
+
+
+def _forward(mgr, ref, ids, ntok, offs, g):
+    S = max(o + n for o, n in zip(offs, ntok))
+    B = len(ids)
+    q = torch.randn(B, S, HQ, D, generator=g)
+    k = torch.randn(B, S, HKV, D, generator=g)
+    v = torch.randn(B, S, HKV, D, generator=g)
+    try:
+        c1 = mgr.begin_forward(ids, ntok, offs)
+    except RuntimeError as e:
+        with pytest.raises(RuntimeError):
+            ref.begin_forward(ids, ntok, offs)
+        return str(e)
+    c2 = ref.begin_forward(ids, ntok, offs)
+    assert c1.start_positions == c2.start_positions and c1.seq_lens == c2.seq_lens
+    assert torch.equal(c1.get_position_ids(S), c2.get_position_ids(S))
+    assert len(c1.cow_pairs) == len(c2.cow_events)
+    for layer in range(L):
+        o1 = c1.attend(layer, q, k, v, HQ, HKV)
+        o2 = c2.attend(layer, q, k, v, HQ, HKV)
+        for b in range(B):
+            rows = slice(offs[b], offs[b] + ntok[b])
+            torch.testing.assert_close(o1[b, rows].float(), o2[b, rows], atol=1e-5, rtol=1e-5)
+            pad = torch.ones(S, dtype=torch.bool)
+            pad[rows] = False
+            assert not o1[b, pad].any()
+    mgr.end_forward(c1)
+    ref.end_forward(c2)
+    return None
+
+
+def _check(mgr, ref, live, ps):
+    assert mgr.pool.num_free == ref.pool.num_free
+    assert mgr.tree.cached_pages == ref.tree.cached_pages
+    for sid in live:
+        assert mgr.seqs[sid].num_tokens == ref.seqs[sid].num_tokens
+        for layer in range(L):
+            k1, v1 = _logical(mgr, sid, layer, ps)
+            k2, v2 = ref.logical_kv(sid, layer)
+            if k1 is None:
+                assert k2.shape[0] == 0
+            else:
+                assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+@pytest.mark.parametrize("seed,ps,pages", [(1, 4, 48), (2, 2, 40), (3, 4, 24), (4, 3, 64), (5, 1, 60)])
+def test_random_serving_traffic_matches_oracle(seed, ps, pages):
+    rnd = random.Random(seed)
+    g = torch.Generator().manual_seed(seed)
+    mgr, ref = _make(ps, pages)
+    pending = {}   # admitted, prompt not yet prefilled: sid -> new tokens to feed
+    running = []   # prefilled, decoding
+    tokens = {}
+    counts = {"prefill": 0, "decode": 0, "cow": 0, "oom": 0, "release": 0, "shared": 0}
+    for it in range(120):
+        r = rnd.random()
+        if r < 0.25 and len(pending) + len(running) < 6:
+            sid = f"s{it}"
+            toks = [rnd.randint(0, 2) for _ in range(rnd.randint(1, 3 * ps + 4))]
+            try:
+                p1 = mgr.allocate_sequence(sid, token_ids=toks)
+            except RuntimeError:
+                with pytest.raises(RuntimeError):
+                    ref.allocate_sequence(sid, token_ids=toks)
+                counts["oom"] += 1
+                continue
+            p2 = ref.allocate_sequence(sid, token_ids=toks)
+            assert p1 == p2
+            tokens[sid] = list(toks)
+            if len(toks) - p1 > 0:
+                pending[sid] = len(toks) - p1
+            else:
+                running.append(sid)  # a full prefix hit: straight to decode
+        elif r < 0.45 and pending:
+            ids = sorted(pending)[: rnd.randint(1, len(pending))]
+            ntok = [pending[s] for s in ids]
+            offs = [rnd.randint(0, 2) for _ in ids]
+            err = _forward(mgr, ref, ids, ntok, offs, g)
+            if err:
+                counts["oom"] += 1
+                continue
+            counts["prefill"] += 1
+            for s in ids:
+                del pending[s]
+                running.append(s)
+        elif r < 0.8 and running:
+            err = _forward(mgr, ref, list(running), [1] * len(running), [0] * len(running), g)
+            if err:
+                counts["oom"] += 1
+                continue
+            counts["decode"] += 1
+            for s in running:
+                tok = rnd.randint(0, 2)
+                tokens[s].append(tok)
+                mgr.append_token_ids(s, [tok])
+                ref.append_token_ids(s, [tok])
+        elif r < 0.88 and len(running) >= 2:
+            # share the last (partial) page of one running sequence with another one
+            # admitted on it: the next write of either copies it, in batch order
+            src = rnd.choice(running)
+            st1, st2 = mgr.seqs[src], ref.seqs[src]
+            n = st1.num_tokens
+            if n == 0 or n % ps == 0:
+                continue
+            sid = f"c{it}"
+            for impl, st in ((mgr, st1), (ref, st2)):
+                impl.allocate_sequence(sid)
+                pages_ = list(st.block_table[: (n + ps - 1) // ps])
+                for p in pages_:
+                    impl.pool.add_ref(p)
+                nst = impl.seqs[sid]
+                if hasattr(nst, "bt"):
+                    nst.extend(pages_)
+                else:
+                    nst.block_table = list(pages_)
+                nst.num_tokens = n
+            tokens[sid] = list(tokens[src][:n])
+            running.append(sid)
+            counts["shared"] += 1
+        elif running or pending:
+            sid = rnd.choice(running + sorted(pending))
+            mgr.release_sequence(sid)
+            ref.release_sequence(sid)
+            if sid in pending:
+                del pending[sid]
+            else:
+                running.remove(sid)
+            counts["release"] += 1
+        _check(mgr, ref, running + sorted(pending), ps)
+    # the traffic reached the paths it is meant to cover
+    assert counts["prefill"] >= 5 and counts["decode"] >= 10 and counts["release"] >= 3
+    for s in running + sorted(pending):
+        mgr.release_sequence(s)
+        ref.release_sequence(s)
+    assert mgr.pool.num_free == ref.pool.num_free
