@@ -55,7 +55,11 @@ tests live in tests/test_oracle.py):
                                                 sequences recorded from the
                                                 reference's own RadixTree and
                                                 PagePool (tests/golden/
-                                                radix_vectors.json)
+                                                radix_vectors.json); its
+                                                stop_at_gap mode (the build's
+                                                match, ending at an evicted
+                                                page) by a known-answer case
+                                                against the default mode
   PagedRef               kv_cache.py:534-777    write plan + CoW order rule,
                                                 CSR, attend = SDPA over the
                                                 gathered pages; pinned against
@@ -496,13 +500,19 @@ class _RNodeRef:
 
 class RadixTreeRef:
     """Per-token trie of kv_cache.py:453-531, with the reference's behaviour kept: match does not
-    stop at an evicted interior page (:467), and LRU ties keep DFS pre-order (:507)."""
+    stop at an evicted interior page (:467), and LRU ties keep DFS pre-order (:507).
 
-    def __init__(self, ps, pool):
+    stop_at_gap=True restates the build's decision instead: match returns pages only up to the
+    first evicted page (a gap-free prefix); the walk, its access stamps and its invalidations are
+    unchanged. The golden vectors pin the default; tests that compare the product's cache over
+    whole serving runs use this mode."""
+
+    def __init__(self, ps, pool, stop_at_gap=False):
         self.root = _RNodeRef()
         self.ps = ps
         self.pool = pool
         self._clock = 0
+        self.stop_at_gap = stop_at_gap
 
     def _now(self):
         self._clock += 1
@@ -510,6 +520,7 @@ class RadixTreeRef:
 
     def match(self, tokens):
         node, pages, now = self.root, [], self._now()
+        gap = False
         for i, tok in enumerate(tokens):
             ch = node.children.get(tok)
             if ch is None:
@@ -517,9 +528,12 @@ class RadixTreeRef:
             node = ch
             node.last_access = now
             d = i + 1
+            if d % self.ps == 0 and node.page_id < 0:
+                gap = True
             if d % self.ps == 0 and node.page_id >= 0:
                 if self.pool.ref_count[node.page_id] > 0:
-                    pages.append(node.page_id)
+                    if not (self.stop_at_gap and gap):
+                        pages.append(node.page_id)
                 else:
                     node.page_id = -1
                     break
@@ -610,10 +624,10 @@ class PagedRef:
     FlashInfer replaced by fp32 SDPA over the gathered pages."""
 
     def __init__(self, num_layers, max_pages, page_size, num_kv_heads, head_dim,
-                 dtype=torch.float32, enable_prefix_caching=True):
+                 dtype=torch.float32, enable_prefix_caching=True, stop_at_gap=False):
         self.ps = page_size
         self.pool = PagePoolRef(num_layers, max_pages, page_size, num_kv_heads, head_dim, dtype)
-        self.tree = RadixTreeRef(page_size, self.pool) if enable_prefix_caching else None
+        self.tree = RadixTreeRef(page_size, self.pool, stop_at_gap) if enable_prefix_caching else None
         self.seqs: Dict[str, _SeqRef] = {}
         self.max_pages = max_pages
 

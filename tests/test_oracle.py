@@ -230,6 +230,28 @@ def test_radix_eviction_lru_and_pins():
     assert tree.evict_lru(5) == 2 and pool.num_free == 9 and tree.cached_pages == 0
 
 
+def test_radix_match_over_an_evicted_interior_page():
+    """Three cached pages on one path, the middle one evicted (its node keeps its
+    children, kv_cache.py:512-516). The reference's match walks on and returns the
+    first and third pages, a prefix with a gap (:459-472); with stop_at_gap the
+    match ends at the evicted page."""
+    ps = 2
+    toks = [1, 1, 2, 2, 3, 3]
+    for stop, want_pages in ((False, [0, 2]), (True, [0])):
+        pool = O.PagePoolRef(1, 10, ps, 1, 2)
+        tree = O.RadixTreeRef(ps, pool, stop_at_gap=stop)
+        pages = _insert_seq(tree, pool, toks)
+        node = tree.root
+        for t in toks[:4]:
+            node = node.children[t]
+        assert node.page_id == pages[1]
+        node.page_id = -1           # the eviction of the middle page
+        pool.release(pages[1])
+        plen, got = tree.match(toks)
+        assert got == [pages[i] for i in want_pages]
+        assert plen == len(got) * ps
+
+
 # ---------------------------------------------------------------- backend pins
 
 
