@@ -1,0 +1,27 @@
+"""Randomised serving traffic on the GPU: the same seeded runs as
+tests/test_host_random.py (admissions with prefix hits, ragged prefill, decode of
+whole batches, subsets and mixed with prefill rows, partial pages shared by
+reference, releases, evictions, OOM), through the real kernels: the host and
+device planners, append, zero and copy pages, the decode (grouped when requests
+share their first pages) and prefill kernels. fp16 pools, head_dim 64, 8 query /
+2 KV heads. After every forward: outputs within 2e-3 abs + 1e-2 rel of the
+oracle's fp32 SDPA on the same (fp16-rounded) inputs, positions, copy-on-writes,
+free and cached pages, and every sequence's K/V read through its block table
+bit-exact."""
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+GPU = dict(device="cuda:0", dtype=torch.float16, HQ=8, HKV=2, D=64, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("seed,ps,pages", [(s, [1, 2, 3, 4, 8, 16][s % 6], [12, 20, 24, 30, 40, 64][(s // 6) % 6])
+                                           for s in range(1, 21)])
+def test_random_serving_traffic_on_gpu(seed, ps, pages):
+    import test_host_random as R
+    print(f"random traffic seed={seed} ps={ps} pages={pages}", flush=True)
+    sys.stdout.flush()
+    R.run_traffic(seed, ps, pages, GPU)

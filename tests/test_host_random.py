@@ -25,17 +25,20 @@ import fake_kernels as FK
 from nanoslg_amd import kv_cache as KC
 from oracle import kv_oracle as O
 
-L, HQ, HKV, D = 2, 4, 2, 8
+L = 2
+CPU = dict(device=None, dtype=torch.float32, HQ=4, HKV=2, D=8, atol=1e-5, rtol=1e-5)
 
 
-def _make(ps, pages):
-    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
-                           max_pages=pages, dtype=torch.float32, device=None, enable_prefix_caching=True,
-                           backend="paged")
+def _make(ps, pages, env):
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=env["HKV"], num_qo_heads=env["HQ"], head_dim=env["D"],
+                           page_size=ps, max_pages=pages, dtype=env["dtype"], device=env["device"],
+                           enable_prefix_caching=True, backend="paged")
+    kernels = FK if env["device"] is None else None
     # the oracle's match stops at an evicted page, as the product's does (the
     # reference's match returns the pages past it, a block table with a gap)
-    return KC.PagedKVCache(cfg, kernels=FK), O.PagedRef(L, pages, ps, HKV, D, torch.float32,
-                                                        enable_prefix_caching=True, stop_at_gap=True)
+    return (KC.PagedKVCache(cfg, kernels=kernels),
+            O.PagedRef(L, pages, ps, env["HKV"], env["D"], torch.float32, enable_prefix_caching=True,
+                       stop_at_gap=True))
 
 
 def _logical(cache, sid, layer, ps):
@@ -44,17 +47,22 @@ def _logical(cache, sid, layer, ps):
     n = st.num_tokens
     if n == 0:
         return None, None
-    k = torch.stack([cache.pool.k[layer, bt[t // ps], t % ps] for t in range(n)])
-    v = torch.stack([cache.pool.v[layer, bt[t // ps], t % ps] for t in range(n)])
-    return k, v
+    rows = torch.tensor([bt[t // ps] * ps + t % ps for t in range(n)], device=cache.pool.k.device)
+    k = cache.pool.k[layer].reshape(-1, *cache.pool.k.shape[-2:])[rows]
+    v = cache.pool.v[layer].reshape(-1, *cache.pool.v.shape[-2:])[rows]
+    return k.cpu().float(), v.cpu().float()
 
 
-def _forward(mgr, ref, ids, ntok, offs, g):
+def _forward(mgr, ref, ids, ntok, offs, g, env):
     S = max(o + n for o, n in zip(offs, ntok))
     B = len(ids)
-    q = torch.randn(B, S, HQ, D, generator=g)
-    k = torch.randn(B, S, HKV, D, generator=g)
-    v = torch.randn(B, S, HKV, D, generator=g)
+    HQ, HKV, D, dt = env["HQ"], env["HKV"], env["D"], env["dtype"]
+    # inputs in the pool's dtype; the oracle gets the same values in fp32
+    q = torch.randn(B, S, HQ, D, generator=g).to(dt)
+    k = torch.randn(B, S, HKV, D, generator=g).to(dt)
+    v = torch.randn(B, S, HKV, D, generator=g).to(dt)
+    dev = env["device"]
+    qd, kd, vd = (q, k, v) if dev is None else (q.to(dev), k.to(dev), v.to(dev))
     try:
         c1 = mgr.begin_forward(ids, ntok, offs)
     except RuntimeError as e:
@@ -63,14 +71,14 @@ def _forward(mgr, ref, ids, ntok, offs, g):
         return str(e)
     c2 = ref.begin_forward(ids, ntok, offs)
     assert c1.start_positions == c2.start_positions and c1.seq_lens == c2.seq_lens
-    assert torch.equal(c1.get_position_ids(S), c2.get_position_ids(S))
+    assert torch.equal(c1.get_position_ids(S).cpu(), c2.get_position_ids(S))
     assert len(c1.cow_pairs) == len(c2.cow_events)
     for layer in range(L):
-        o1 = c1.attend(layer, q, k, v, HQ, HKV)
-        o2 = c2.attend(layer, q, k, v, HQ, HKV)
+        o1 = c1.attend(layer, qd, kd, vd, HQ, HKV).cpu().float()
+        o2 = c2.attend(layer, q.float(), k.float(), v.float(), HQ, HKV)
         for b in range(B):
             rows = slice(offs[b], offs[b] + ntok[b])
-            torch.testing.assert_close(o1[b, rows].float(), o2[b, rows], atol=1e-5, rtol=1e-5)
+            torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=env["atol"], rtol=env["rtol"])
             pad = torch.ones(S, dtype=torch.bool)
             pad[rows] = False
             assert not o1[b, pad].any()
@@ -96,9 +104,15 @@ def _check(mgr, ref, live, ps):
 @pytest.mark.parametrize("seed,ps,pages", [(1, 4, 48), (2, 2, 40), (3, 4, 24), (4, 3, 64), (5, 1, 60),
                                            (6, 4, 20), (7, 2, 24), (8, 8, 40), (9, 3, 30), (10, 16, 12)])
 def test_random_serving_traffic_matches_oracle(seed, ps, pages):
+    run_traffic(seed, ps, pages, CPU)
+
+
+def run_traffic(seed, ps, pages, env):
+    """One seeded serving run (see the module docstring); env: device (None = the
+    CPU stand-in kernels), pool dtype, head shape, output tolerance."""
     rnd = random.Random(seed)
     g = torch.Generator().manual_seed(seed)
-    mgr, ref = _make(ps, pages)
+    mgr, ref = _make(ps, pages, env)
     pending = {}   # admitted, prompt not yet prefilled: sid -> new tokens to feed
     running = []   # prefilled, decoding
     tokens = {}
@@ -126,7 +140,7 @@ def test_random_serving_traffic_matches_oracle(seed, ps, pages):
             ids = sorted(pending)[: rnd.randint(1, len(pending))]
             ntok = [pending[s] for s in ids]
             offs = [rnd.randint(0, 2) for _ in ids]
-            err = _forward(mgr, ref, ids, ntok, offs, g)
+            err = _forward(mgr, ref, ids, ntok, offs, g, env)
             if err:
                 counts["oom"] += 1
                 continue
@@ -148,7 +162,7 @@ def test_random_serving_traffic_matches_oracle(seed, ps, pages):
                 ids += extra
                 ntok += [pending[s] for s in extra]
             offs = [rnd.randint(0, 1) if n > 1 else 0 for n in ntok]
-            err = _forward(mgr, ref, ids, ntok, offs, g)
+            err = _forward(mgr, ref, ids, ntok, offs, g, env)
             if err:
                 counts["oom"] += 1
                 continue
