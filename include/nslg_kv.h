@@ -130,9 +130,9 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
  *                     one call at a time per workspace
  * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16 (MFMA, split-K as
  * above) and f32 (a VALU kernel, one workgroup per 16 query rows of a sequence and
- * KV head, for caches kept in fp32 such as the contiguous backend of an fp32
- * model, kv_cache.py:227-322); D in {64, 128, 256}; 1 <= Hq/Hkv <= 16. A sequence
- * with no tokens gets zeros.
+ * KV head and key split, then an fp32 merge, for caches kept in fp32 such as the
+ * contiguous backend of an fp32 model, kv_cache.py:227-322); D in {64, 128, 256};
+ * 1 <= Hq/Hkv <= 16. A sequence with no tokens gets zeros.
  */
 size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
                                         int32_t num_kv_heads, int32_t head_dim,

@@ -91,7 +91,12 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
   const int nrows = n_new * G;
   const int row0 = tile * kRowsF;
   const int last_row = min(row0 + kRowsF, nrows) - 1;
-  const int kv_end = min(L, start + last_row / G + 1);
+  const int kv_all = min(L, start + last_row / G + 1);
+  // split y of p.splits takes keys [kv_begin, kv_end) (32-key aligned pieces)
+  const int split = blockIdx.y;
+  const int piece = ((kv_all + p.splits - 1) / p.splits + kKeysF - 1) / kKeysF * kKeysF;
+  const int kv_begin = min(kv_all, split * piece);
+  const int kv_end = min(kv_all, kv_begin + piece);
   const int32_t* idx = p.indices + p.indptr[b];
   const int ps = p.page_size;
   const int64_t row_elems = (int64_t)p.num_kv_heads * D;
@@ -119,7 +124,7 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
 #pragma unroll
   for (int c = 0; c < kCols; ++c) o[c] = 0.f;
 
-  for (int key0 = 0; key0 < kv_end; key0 += kKeysF) {
+  for (int key0 = kv_begin; key0 < kv_end; key0 += kKeysF) {
     __syncthreads();  // previous tile's K/V/P reads are done (and q_lds is written)
     for (int e = tid; e < kKeysF * (D / 4); e += kThreadsF) {
       const int j = e / (D / 4), c = e % (D / 4);
@@ -183,15 +188,72 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
   }
 
   if (!row_ok) return;
-  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   const int t = my_row / G, g = my_row % G;
+  if (p.splits > 1) {
+    // partial of this split: unnormalised O, running max and sum (merged later)
+    const int64_t slot = ((int64_t)(q0 + t) * p.num_qo_heads + h * G + g) * p.splits + split;
+    float* po = p.part_o + slot * D + rj * kCols;
+#pragma unroll
+    for (int c = 0; c < kCols; c += 4) *reinterpret_cast<f32x4*>(po + c) = f32x4{o[c], o[c + 1], o[c + 2], o[c + 3]};
+    if (rj == 0) {
+      p.part_ml[slot * 2] = m_run;
+      p.part_ml[slot * 2 + 1] = l_run;
+    }
+    return;
+  }
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   float* orow = p.out + (int64_t)(q0 + t) * p.out_stride + (int64_t)(h * G + g) * D + rj * kCols;
 #pragma unroll
   for (int c = 0; c < kCols; c += 4)
     *reinterpret_cast<f32x4*>(orow + c) = f32x4{o[c] * inv, o[c + 1] * inv, o[c + 2] * inv, o[c + 3] * inv};
 }
 
+// Merge of the splits of one (query token, query head) row: one wave, lanes over D.
+template <int D>
+__global__ void __launch_bounds__(64) attention_f32_merge_kernel(AttnF32Args p, int64_t rows) {
+  const int64_t row = blockIdx.x;  // (token, head) in [0, total_q * Hq)
+  if (row >= rows) return;
+  const int lane = threadIdx.x;
+  const float* ml = p.part_ml + row * p.splits * 2;
+  float M = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, ml[2 * s]);
+  float lsum = 0.f;
+  float acc[D / 64];
+#pragma unroll
+  for (int c = 0; c < D / 64; ++c) acc[c] = 0.f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float m = ml[2 * s];
+    if (m == -INFINITY) continue;
+    const float f = expf(m - M);
+    lsum += f * ml[2 * s + 1];
+    const float* po = p.part_o + (row * p.splits + s) * D;
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c) acc[c] = fmaf(f, po[c * 64 + lane], acc[c]);
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const int64_t t = row / p.num_qo_heads, hq = row % p.num_qo_heads;
+  float* orow = p.out + t * p.out_stride + hq * D;
+#pragma unroll
+  for (int c = 0; c < D / 64; ++c) orow[c * 64 + lane] = acc[c] * inv;
+}
+
 }  // namespace
+
+int attention_f32_splits(int64_t batch, int64_t total_tokens) {
+  // a split per ~512 keys of the average sequence, up to 64, for one query token
+  // per sequence (decode); the prefill rows fill the GPU on their own
+  if (batch <= 0) return 1;
+  const int64_t per_seq = total_tokens / batch;
+  int64_t sp = per_seq / 512;
+  const int64_t cap = 4096 / batch;  // keep splits x sequences near a few thousand workgroups
+  sp = sp > cap ? cap : sp;
+  return (int)(sp < 1 ? 1 : (sp > 64 ? 64 : sp));
+}
+
+size_t attention_f32_workspace(int64_t total_q, int32_t num_qo_heads, int32_t head_dim, int splits) {
+  if (splits <= 1) return 256;
+  return (size_t)total_q * num_qo_heads * splits * (head_dim + 2) * sizeof(float) + 256;
+}
 
 int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipStream_t s) {
   if (a.group > kRowsF * 64) return fail(NSLG_EUNSUPPORTED, "attention_f32: GQA group %d", a.group);
@@ -204,16 +266,28 @@ int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipSt
   // end in a partial tile)
   const int64_t tiles = (total_q * a.group + kRowsF - 1) / kRowsF + a.batch;
   if (tiles * a.num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "attention_f32: too many rows");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(NSLG_EUNSUPPORTED, "attention_f32: head_dim %d (64, 128 or 256)", head_dim);
+  if (a.splits < 1 || a.splits > 64) return fail(NSLG_EINVAL, "attention_f32: %d splits", a.splits);
+  if (a.splits > 1 && (!a.part_o || !a.part_ml)) return fail(NSLG_EWORKSPACE, "attention_f32: no workspace");
   AttnF32Args p = a;
   p.row_tiles = (int32_t)tiles;
-  const dim3 grid((unsigned)(tiles * a.num_kv_heads));
+  const dim3 grid((unsigned)(tiles * a.num_kv_heads), (unsigned)a.splits);
   switch (head_dim) {
     case 64: attention_f32_kernel<64><<<grid, kThreadsF, 0, s>>>(p); break;
     case 128: attention_f32_kernel<128><<<grid, kThreadsF, 0, s>>>(p); break;
-    case 256: attention_f32_kernel<256><<<grid, kThreadsF, 0, s>>>(p); break;
-    default: return fail(NSLG_EUNSUPPORTED, "attention_f32: head_dim %d (64, 128 or 256)", head_dim);
+    default: attention_f32_kernel<256><<<grid, kThreadsF, 0, s>>>(p); break;
   }
-  return check_launch("attention_f32");
+  int rc = check_launch("attention_f32");
+  if (rc || a.splits == 1) return rc;
+  const int64_t rows = total_q * a.num_qo_heads;
+  if (rows > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "attention_f32: too many rows");
+  switch (head_dim) {
+    case 64: attention_f32_merge_kernel<64><<<dim3((unsigned)rows), 64, 0, s>>>(p, rows); break;
+    case 128: attention_f32_merge_kernel<128><<<dim3((unsigned)rows), 64, 0, s>>>(p, rows); break;
+    default: attention_f32_merge_kernel<256><<<dim3((unsigned)rows), 64, 0, s>>>(p, rows); break;
+  }
+  return check_launch("attention_f32_merge");
 }
 
 }  // namespace nslg

@@ -126,8 +126,14 @@ struct AttnF32Args {
   float* out;
   int64_t out_stride;
   int32_t row_tiles;           // set by attention_f32
+  int32_t splits;              // key ranges per row tile (1: no partials)
+  float* part_o;               // splits > 1: [total_q, Hq, splits, D] partial outputs
+  float* part_ml;              // splits > 1: [total_q, Hq, splits, 2] running max and sum
 };
 // Launch on stream s; total_q = number of query tokens (B for decode).
 int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipStream_t s);
+// Key splits for a decode batch, and the workspace they need.
+int attention_f32_splits(int64_t batch, int64_t total_tokens);
+size_t attention_f32_workspace(int64_t total_q, int32_t num_qo_heads, int32_t head_dim, int splits);
 
 }  // namespace nslg

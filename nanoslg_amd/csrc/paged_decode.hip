@@ -915,6 +915,18 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
       a.out = (float*)out;
       a.out_stride = out_stride;
       a.row_tiles = 0;
+      // long sequences are split over keys; the partials go to the workspace
+      a.splits = attention_f32_splits(batch, total_pages * (int64_t)page_size);
+      a.part_o = nullptr;
+      a.part_ml = nullptr;
+      if (a.splits > 1) {
+        const size_t need = attention_f32_workspace(batch, num_qo_heads, head_dim, a.splits);
+        if (!workspace || workspace_bytes < need)
+          return fail(NSLG_EWORKSPACE, "paged_decode: workspace %zu < %zu bytes", workspace_bytes, need);
+        if (((uintptr_t)workspace) & 255) return fail(NSLG_EINVAL, "paged_decode: workspace must be 256-byte aligned");
+        a.part_o = (float*)workspace;
+        a.part_ml = a.part_o + (int64_t)batch * num_qo_heads * a.splits * head_dim;
+      }
       return attention_f32(a, batch, head_dim, as_stream(stream));
     }
   }
@@ -1005,7 +1017,9 @@ extern "C" size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo
                                                    int64_t total_pages, int32_t page_size,
                                                    int32_t dtype) {
   if (!shape_ok(batch, num_qo_heads, num_kv_heads, head_dim, total_pages, page_size)) return 0;
-  if (dtype == NSLG_F32) return 256;  // the fp32 path keeps its state on chip
+  if (dtype == NSLG_F32)  // partials of the key splits of the fp32 path
+    return attention_f32_workspace(batch, num_qo_heads, head_dim,
+                                   attention_f32_splits(batch, total_pages * (int64_t)page_size));
   const DecodeShape sh = shape_of<false>(dtype, head_dim, batch, num_kv_heads, total_pages * page_size, page_size);
   return workspace_bytes_for(sh, batch, num_qo_heads, head_dim, 1, 0);
 }

@@ -560,6 +560,9 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
     a.out = (float*)out;
     a.out_stride = out_stride;
     a.row_tiles = 0;
+    a.splits = 1;  // the query rows fill the GPU
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
     return attention_f32(a, total_q, head_dim, as_stream(stream));
   }
   if (dtype != NSLG_F16 && dtype != NSLG_BF16)

@@ -53,6 +53,11 @@ def test_host_side_argument_checks():
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 34, 8, 128, 0.1, 0, 256, 4096,
                                None, 0, None)
     assert rc == -1  # Hq not a multiple of Hkv
+    # an fp32 decode long enough to be split over keys needs its workspace
+    assert lib.nslg_paged_decode_workspace_size(1, 32, 8, 128, 2048, 16, 2) > (1 << 20)
+    rc = lib.nslg_paged_decode(256, 4096, 256, 256, 4096, 16, 256, 256, 256, 2048, 1, 32, 8, 128, 0.1, 2, 256,
+                               4096, None, 0, None)
+    assert rc == -4 and "workspace" in _lib.last_error()
     # prefill: the softmax scale must be positive and finite (the lazy running max
     # compares raw scores against a threshold divided by the scale)
     for bad in (0.0, -0.1, float("inf"), float("nan")):

@@ -327,6 +327,18 @@ def test_f32_groups_and_page_sizes(Hq, Hkv, ps):
     torch.testing.assert_close(out, ref, **F32_TOL)
 
 
+@pytest.mark.parametrize("lens", [[32768], [9000, 3000, 1, 0], [20000] * 8])
+def test_f32_decode_split_over_keys(lens):
+    """Long fp32 decodes are split over keys (partials in the workspace, then an fp32
+    merge): 64, 7 and 8 splits here."""
+    _log(f"f32 decode splits lens={lens[:4]}")
+    out, ref = _decode_case(lens, 32, 8, 128, 16, torch.float32, seed=len(lens) + lens[0] % 97)
+    torch.testing.assert_close(out, ref, **F32_TOL)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert torch.count_nonzero(out[b]) == 0
+
+
 def test_f32_grouped_decode_is_rejected():
     """Grouped (shared-prefix) decode runs on the 16-bit MFMA path only."""
     from nanoslg_amd import _lib
