@@ -25,3 +25,10 @@ def test_random_serving_traffic_on_gpu(seed, ps, pages):
     print(f"random traffic seed={seed} ps={ps} pages={pages}", flush=True)
     sys.stdout.flush()
     R.run_traffic(seed, ps, pages, GPU)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5])
+def test_random_contiguous_traffic_on_gpu(seed):
+    import test_host_random as R
+    print(f"random contiguous traffic seed={seed}", flush=True)
+    R.run_contiguous_traffic(seed, GPU)

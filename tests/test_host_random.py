@@ -216,3 +216,69 @@ def run_traffic(seed, ps, pages, env):
         mgr.release_sequence(s)
         ref.release_sequence(s)
     assert mgr.pool.num_free == ref.pool.num_free
+
+
+def run_contiguous_traffic(seed, env, max_batch=4, max_seq=64):
+    """The contiguous backend (kv_cache.py:227-379) over random forwards: every
+    forward carries all live sequences in allocation order (the reference indexes
+    its pool by batch row, which equals the slot only then), each with a random
+    number of new tokens (prefill and decode rows in one forward) and a random left
+    pad; sequences are released all together (the reference resets its slot counter
+    only then). Outputs and the pool bytes against the oracle after every forward."""
+    rnd = random.Random(seed)
+    g = torch.Generator().manual_seed(seed)
+    HQ, HKV, D, dt = env["HQ"], env["HKV"], env["D"], env["dtype"]
+    cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, max_batch_size=max_batch,
+                           max_seq_len=max_seq, dtype=dt, device=env["device"], backend="contiguous")
+    mgr = KC.ContiguousKVCache(cfg, kernels=FK if env["device"] is None else None)
+    ref = O.ContiguousRef(L, max_batch, max_seq, HKV, D)
+    live, lens, forwards = [], {}, 0
+    for it in range(60):
+        r = rnd.random()
+        if (r < 0.2 or not live) and len(live) < max_batch:
+            sid = f"s{it}"
+            mgr.allocate_sequence(sid)
+            ref.allocate_sequence(sid)
+            live.append(sid)
+            lens[sid] = 0
+        elif r < 0.9:
+            room = [max_seq - lens[s] for s in live]
+            if min(room) < 1:
+                continue
+            ntok = [rnd.choice([1, 1, 1, rnd.randint(1, min(12, rm))]) for rm in room]
+            offs = [rnd.randint(0, 2) for _ in live]
+            if all(n == 1 for n in ntok):
+                # a decode forward is one token wide, unpadded (worker.py:398-426): the
+                # reference's decode write takes input column 0 (kv_cache.py:301-303)
+                offs = [0] * len(live)
+            S = max(o + n for o, n in zip(offs, ntok))
+            q = torch.randn(len(live), S, HQ, D, generator=g).to(dt)
+            k = torch.randn(len(live), S, HKV, D, generator=g).to(dt)
+            v = torch.randn(len(live), S, HKV, D, generator=g).to(dt)
+            dev = env["device"]
+            qd, kd, vd = (q, k, v) if dev is None else (q.to(dev), k.to(dev), v.to(dev))
+            c1, c2 = mgr.begin_forward(live, ntok, offs), ref.begin_forward(live, ntok, offs)
+            assert torch.equal(c1.get_position_ids(S).cpu(), c2.get_position_ids(S))
+            for layer in range(L):
+                o1 = c1.attend(layer, qd, kd, vd, HQ, HKV).cpu().float()
+                o2 = c2.attend(layer, q.float(), k.float(), v.float(), HQ, HKV)
+                for b in range(len(live)):
+                    rows = slice(offs[b], offs[b] + ntok[b])
+                    torch.testing.assert_close(o1[b, rows], o2[b, rows], atol=env["atol"], rtol=env["rtol"])
+            mgr.end_forward(c1)
+            ref.end_forward(c2)
+            for s, n in zip(live, ntok):
+                lens[s] += n
+            forwards += 1
+            assert torch.equal(mgr.k.cpu().float(), ref.k) and torch.equal(mgr.v.cpu().float(), ref.v)
+        else:
+            for s in live:
+                mgr.release_sequence(s)
+                ref.release_sequence(s)
+            live, lens = [], {}
+    assert forwards >= 20, forwards
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5])
+def test_random_contiguous_traffic_matches_oracle(seed):
+    run_contiguous_traffic(seed, CPU)
