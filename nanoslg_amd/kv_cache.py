@@ -353,7 +353,7 @@ class _ForwardPlan:
         self.group_slot = groups.seq_group_slot if groups is not None else None
         self.slot, self.pos_i32, self.indptr, self.indices, self.lpl = slot, pos, indptr, indices, lpl
         self.qo_indptr, self.q_rows = qo_indptr, q_rows
-        self.cow_src = self.cow_dst = slot[:0]
+        self.cow_src = self.cow_dst = None  # a decode step planned on the device copies no page
         self.zero_ids = zero_ids
         self.batch, self.iw = batch, 1
         self.total_pages = int(total_pages)
@@ -716,10 +716,13 @@ class PagedCacheContext(CacheContext):
         cfg, pool, ps = cache.cfg, cache.pool, cache.cfg.page_size
         states = [cache.seqs[s] for s in self.seq_ids]
         self.start_positions = [st.num_tokens for st in states]
-        self.seq_lens = [self.start_positions[i] + self.new_token_counts[i] for i in range(B)]
+        self.seq_lens = [a + n for a, n in zip(self.start_positions, self.new_token_counts)]
         self.max_kv_len = max(self.seq_lens) if self.seq_lens else 0
-        self._is_decode = B > 0 and all(n == 1 for n in self.new_token_counts)
-        self._iw = max(o + n for o, n in zip(self.input_offsets, self.new_token_counts)) if B else 1
+        self._is_decode = B > 0 and self.new_token_counts.count(1) == B
+        if self._is_decode and not input_offsets:
+            self._iw = 1  # one token per sequence, no padding
+        else:
+            self._iw = max(o + n for o, n in zip(self.input_offsets, self.new_token_counts)) if B else 1
         iw = self._iw
 
         # write plan + copy-on-write, in batch order (kv_cache.py:575-594): a shared page
@@ -1018,7 +1021,7 @@ class PagedKVCache(KVCacheManager):
 
     # ---- decode plans built on the device ---------------------------------------------
     def _record_decode_plan(self, seq_ids, plan, seq_lens) -> None:
-        self._dev_plan = (tuple(seq_ids), plan, np.asarray(seq_lens, np.int64))
+        self._dev_plan = (tuple(seq_ids), plan, list(seq_lens))
 
     def _decode_launcher(self, plan: "_ForwardPlan", num_qo_heads: int):
         """The decode launcher of a forward: the previous forward's, re-bound to this
@@ -1091,6 +1094,61 @@ class PagedKVCache(KVCacheManager):
                 slot[b] = 16 * g + m
         return groups, prefixes, slot
 
+    SCALAR_PLAN_BATCH = 16  # decode batches up to this size are checked in plain Python (cheaper than numpy)
+
+    def _decode_step_pages(self, states, prev_lens, zero_pages):
+        """The pages a decode step opens, for the device planner: (new_page [B] int32,
+        -1 where the sequence's new token goes into its current last page; count), after
+        checking that every sequence gained exactly the previous step's token, has the
+        pages the step needs, and writes no shared page, and that the pages opened are
+        the ones allocated for it. None when a check fails. Updates tokens_used."""
+        B, ps, pool = len(states), self.cfg.page_size, self.pool
+        start = np.fromiter((st.num_tokens for st in states), np.int64, B)
+        if not np.array_equal(start, prev_lens):
+            return None
+        npg = start // ps + 1
+        if not np.array_equal(np.fromiter((st.n_pages for st in states), np.int64, B), npg):
+            return None
+        opens = start % ps == 0
+        pids = np.fromiter((int(st.bt[k - 1]) for st, k in zip(states, npg.tolist())), np.int64, B)
+        if bool((pool.ref_count[pids] > 1).any()):
+            return None  # a shared page is written: copy-on-write goes through the host plan
+        new_page = np.where(opens, pids, -1).astype(np.int32)
+        if sorted(zero_pages or []) != sorted(pids[opens].tolist()):
+            return None
+        sl = start % ps
+        pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
+        return new_page, int(opens.sum())
+
+    def _decode_step_pages_scalar(self, states, prev_lens, zero_pages):
+        """_decode_step_pages for a small batch, one sequence at a time: the same
+        checks, result and tokens_used update."""
+        ps, rc = self.cfg.page_size, self.pool.ref_count
+        pids, new_page, opened = [], [], []
+        for st, n in zip(states, prev_lens):
+            if st.num_tokens != n:
+                return None
+            k = n // ps + 1
+            if st.n_pages != k:
+                return None
+            pid = int(st.bt[k - 1])
+            if rc[pid] > 1:
+                return None  # a shared page is written: copy-on-write goes through the host plan
+            pids.append(pid)
+            if n % ps == 0:
+                new_page.append(pid)
+                opened.append(pid)
+            else:
+                new_page.append(-1)
+        if sorted(zero_pages or []) != sorted(opened):
+            return None
+        tu = self.pool.tokens_used
+        for pid, n in zip(pids, prev_lens):
+            used = n % ps + 1
+            if tu[pid] < used:
+                tu[pid] = used
+        return np.array(new_page, np.int32), len(opened)
+
     def _advance_decode_plan(self, seq_ids, states, zero_pages) -> Optional[_ForwardPlan]:
         """This decode forward's plan built on the device from the previous one
         (kernels.decode_plan_step), when the batch is the one the previous decode
@@ -1104,22 +1162,13 @@ class PagedKVCache(KVCacheManager):
         B, ps, pool = len(states), self.cfg.page_size, self.pool
         if B == 0 or B > 512:
             return None
-        start = np.fromiter((st.num_tokens for st in states), np.int64, B)
-        if not np.array_equal(start, prev[2]):
+        if B <= self.SCALAR_PLAN_BATCH:
+            step = self._decode_step_pages_scalar(states, prev[2], zero_pages)
+        else:
+            step = self._decode_step_pages(states, prev[2], zero_pages)
+        if step is None:
             return None
-        npg = start // ps + 1
-        if not np.array_equal(np.fromiter((st.n_pages for st in states), np.int64, B), npg):
-            return None
-        opens = start % ps == 0
-        pids = np.fromiter((int(st.bt[k - 1]) for st, k in zip(states, npg.tolist())), np.int64, B)
-        if bool((pool.ref_count[pids] > 1).any()):
-            return None  # a shared page is written: copy-on-write goes through the host plan
-        new_page = np.where(opens, pids, -1).astype(np.int32)
-        n_new = int(opens.sum())
-        if sorted(zero_pages or []) != sorted(pids[opens].tolist()):
-            return None
-        sl = start % ps
-        pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
+        new_page, n_new = step
         plan = prev[1]
         fast = getattr(kern, "_decode_plan_step", None)
         if fast is not None:  # inputs are the previous plan's outputs: no argument checks

@@ -385,11 +385,14 @@ def test_stats_and_reset():
     assert mgr.stats["active_seqs"] == 0 and mgr.stats["radix"] == 2 and mgr.pool.num_free == 13
 
 
-def test_device_decode_plan_matches_host_plan():
+@pytest.mark.parametrize("scalar_batch", [16, 0])
+def test_device_decode_plan_matches_host_plan(scalar_batch, monkeypatch):
     """Steady decode steps build their plan from the previous one (decode_plan_step);
     each such plan equals, entry for entry, the plan the host builds for the same
     step, and pages, refcounts and tokens_used stay identical. Batch changes, prefill
-    and shared pages fall back to the host plan."""
+    and shared pages fall back to the host plan. Both host checks of a step run: the
+    per-sequence one of small batches and the vectorised one."""
+    monkeypatch.setattr(KC.PagedKVCache, "SCALAR_PLAN_BATCH", scalar_batch)
     g = torch.Generator().manual_seed(11)
     fast, _ = make(ps=4, pages=96, prefix=False)
     slow, _ = make(ps=4, pages=96, prefix=False)
