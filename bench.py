@@ -244,6 +244,8 @@ class _TimedLaunch:
 
     def __call__(self, layer, q, k_new, v_new, rope=None):
         timed = self.timed
+        if q.dim() == 4 and timed.recording and rope is None:  # a forward's [B, 1, Hq, D] grid
+            return self(layer, q[:, 0], k_new, v_new).reshape(q.shape[0], 1, -1)
         if not timed.recording or rope is not None:
             return self.real(layer, q, k_new, v_new, rope=rope)
         slots, indptr, indices, lpl, total_pages, groups = self.plan

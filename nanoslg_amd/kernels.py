@@ -499,7 +499,8 @@ class DecodeLaunch:
     def __call__(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                  rope: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
         """q [B, Hq, D] (rows may be strided), k_new/v_new [B, ..., Hkv, D] rows of one
-        token each; returns [B, Hq, D] for pool layer `layer`. With rope = (cos, sin,
+        token each; returns [B, Hq, D] for pool layer `layer` (q [B, 1, Hq, D]: returns
+        [B, 1, Hq * D], the layout of a forward's attention output). With rope = (cos, sin,
         positions int32 [B]) q and k_new are first rotated (nslg_rope_append replaces
         nslg_append_kv)."""
         if not 0 <= layer < self.L:
@@ -509,8 +510,14 @@ class DecodeLaunch:
                 or k_new.get_device() != di or v_new.get_device() != di):
             raise ValueError(f"DecodeLaunch: tensors must be {self.dtype} on {self.device}")
         B, Hq, D = self.B, self.Hq, self.D
-        if q.shape != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
+        if q.dim() == 4:  # [B, 1, Hq, D], a forward's input grid: the output is [B, 1, Hq * D]
+            if q.shape != (B, 1, Hq, D) or q.stride(3) != 1 or q.stride(2) != D:
+                raise ValueError(f"DecodeLaunch: q must be [{B}, 1, {Hq}, {D}] with a contiguous [Hq, D] block")
+            out_shape = (B, 1, Hq * D)
+        elif q.shape != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
             raise ValueError(f"DecodeLaunch: q must be [{B}, {Hq}, {D}] with a contiguous [Hq, D] block")
+        else:
+            out_shape = (B, Hq, D)
         ks = self._kv_rows(k_new, "k_new")
         vs = self._kv_rows(v_new, "v_new")
         stream = _RAW_STREAM(di) if _RAW_STREAM is not None else torch.cuda.current_stream(self.device).cuda_stream
@@ -536,7 +543,7 @@ class DecodeLaunch:
                                       self.P * self.ps, self.code, stream)
             _lib.check(rc, "nslg_rope_append")
             q_ptr, q_stride = q_rot.data_ptr(), Hq * D
-        out = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
+        out = torch.empty(out_shape, dtype=self.dtype, device=self.device)
         grp = self.groups
         if grp is None:
             rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,

@@ -952,7 +952,7 @@ class PagedCacheContext(CacheContext):
             launch = self._decode_launch
             if launch is None or launch.bound_plan is not plan:
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
-            return launch(layer_idx, q[:, 0], k_new, v_new).reshape(B, 1, -1)
+            return launch(layer_idx, q, k_new, v_new)
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         return self._prefill(q, k_layer, v_layer)
@@ -974,7 +974,7 @@ class PagedCacheContext(CacheContext):
             launch = self._decode_launch
             if launch is None or launch.bound_plan is not plan:
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
-            return launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, pos)).reshape(B, 1, -1)
+            return launch(layer_idx, q, k_new, v_new, rope=(cos, sin, pos))
         k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
         q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
         return self._prefill(q_rot, k_layer, v_layer)

@@ -107,6 +107,8 @@ class DecodeLaunch:
         self.sm_scale = sm_scale
 
     def __call__(self, layer, q, k_new, v_new, rope=None):
+        if q.dim() == 4:  # [B, 1, Hq, D] -> [B, 1, Hq * D]
+            return self(layer, q[:, 0], k_new, v_new, rope).reshape(q.shape[0], 1, -1)
         slots, indptr, indices, lpl, total = self.args
         k_layer, v_layer = self.k_pool[layer], self.v_pool[layer]
         if rope is None:
