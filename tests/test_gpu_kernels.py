@@ -475,7 +475,8 @@ def test_decode_chunks_longer_than_the_page_window():
 
 def test_decode_launch_matches_separate_calls():
     """The per-forward launcher (append + decode per layer) gives the same pool bytes
-    and the same outputs as append_kv followed by paged_decode on each layer."""
+    and the same outputs as append_kv followed by paged_decode on each layer, with q
+    as [B, Hq, D] rows or as a forward's [B, 1, Hq, D] grid (output [B, 1, Hq * D])."""
     _log("decode launcher vs separate calls")
     from nanoslg_amd import kernels as K
     g = torch.Generator().manual_seed(72)
@@ -493,14 +494,20 @@ def test_decode_launch_matches_separate_calls():
         q = torch.randn(len(lens), Hq, D, generator=g).half().to(DEV)
         kn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
         vn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
-        o1 = launch(layer, q, kn, vn)
+        grid = layer % 2 == 1  # odd layers: the forward's [B, 1, Hq, D] grid
+        o1 = launch(layer, q.unsqueeze(1) if grid else q, kn, vn)
         K.append_kv(kn, vn, slots, k2[layer], v2[layer])
         o2 = K.paged_decode(q, k2[layer], v2[layer], ip, ix, lp, int(indptr[-1]))
         torch.cuda.synchronize()
+        if grid:
+            assert o1.shape == (len(lens), 1, Hq * D)
+            o1 = o1.view(len(lens), Hq, D)
         assert torch.equal(o1, o2)
     assert torch.equal(k_pool, k2) and torch.equal(v_pool, v2)
     with pytest.raises(ValueError):
         launch(0, q[:2], kn, vn)
+    with pytest.raises(ValueError):  # two tokens per sequence: not a decode grid
+        launch(0, q.unsqueeze(1).expand(-1, 2, -1, -1), kn, vn)
     with pytest.raises(IndexError):
         launch(L, q, kn, vn)
 
