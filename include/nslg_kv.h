@@ -150,6 +150,34 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
                       nslg_stream_t stream);
 
 /*
+ * nslg_paged_decode without a caller workspace: the split-K partials live in a
+ * static device array of NSLG_NOALLOC_SCRATCH_BYTES (16 MiB) that the library
+ * holds on every GPU it runs on until the process ends. No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It allocates nothing and calls no allocating routine.
+ *
+ * Arguments and results as nslg_paged_decode (same kernels, bit-identical output),
+ * without workspace / workspace_bytes. The call's device is the current device
+ * (hipSetDevice), which must be the stream's. A call that would need more scratch
+ * than the static array (nslg_paged_decode_workspace_size(...) >
+ * NSLG_NOALLOC_SCRATCH_BYTES: e.g. batches of several hundred long sequences)
+ * returns NSLG_EWORKSPACE without launching. All calls on one GPU share the one
+ * array: calls that overlap on a GPU (different streams, or host threads, without
+ * ordering between them) race and give wrong results.
+ */
+#define NSLG_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+int nslg_paged_decode_noalloc(const void* q, int64_t q_stride,
+                              const void* k_pool, const void* v_pool, int64_t num_pages,
+                              int32_t page_size, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                              int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                              int32_t dtype, void* out, int64_t out_stride,
+                              nslg_stream_t stream);
+
+/*
  * Paged decode for a batch in which groups of sequences share their first pages
  * (a radix prefix: the same page ids, kv_cache.py:459-472, 707-716). Same result
  * as nslg_paged_decode (within the attention tolerance: the split differs); the

@@ -16,6 +16,8 @@ import torch  # noqa: F401  (loads torch's HIP runtime first, so the library bin
 LIB_PATH = Path(__file__).resolve().parent / "libnslg_kv.so"
 
 NSLG_F16, NSLG_BF16, NSLG_F32 = 0, 1, 2
+NSLG_EWORKSPACE = -4
+NSLG_NOALLOC_SCRATCH_BYTES = 16 << 20  # the static scratch of nslg_paged_decode_noalloc
 
 _I32P = POINTER(c_int32)
 
@@ -38,7 +40,10 @@ SIGNATURES = {
                                     c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,
                                     c_void_p]),
-    "nslg_paged_decode_grouped_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
+    "nslg_paged_decode_noalloc": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
+                                            c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
+                                            c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),
+    "nslg_paged_decode_grouped_workspace_size":(c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int64, c_int32,
                                                             c_int32, c_int32]),
     "nslg_paged_decode_grouped": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                             c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,

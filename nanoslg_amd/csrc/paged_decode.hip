@@ -34,6 +34,7 @@
 #include <math.h>
 
 #include <atomic>
+#include <mutex>
 
 namespace nslg {
 namespace {
@@ -1050,6 +1051,69 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
   return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
                             kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
                             dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream);
+}
+
+// ---- decode without a caller workspace ---------------------------------------------
+// The split-K partials and chunk ranges of nslg_paged_decode_noalloc live in this
+// fixed device array instead of a caller's workspace. Every GPU the library runs on
+// holds its own copy at its own address until the process ends. Host code never
+// passes the array's name to a kernel: its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and used from then on.
+static __device__ __align__(256) unsigned char scratch[NSLG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first call
+// made with that device current).
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return fail(NSLG_EINVAL, "paged_decode_noalloc: no current device (or device %d >= %d)", dev, kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(NSLG_ELAUNCH, "paged_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSLG_OK;
+}
+
+}  // namespace
+
+extern "C" int nslg_paged_decode_noalloc(const void* q, int64_t q_stride, const void* k_pool,
+                                         const void* v_pool, int64_t num_pages, int32_t page_size,
+                                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                                         const int32_t* kv_last_page_len, int64_t total_pages,
+                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                         int64_t out_stride, nslg_stream_t stream) {
+  // Same scratch layout and size as nslg_paged_decode's workspace; nothing in it has
+  // to start at zero (every chunk range and partial is written before it is read).
+  const size_t need = nslg_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, total_pages,
+                                                       page_size, dtype);
+  if (need > (size_t)NSLG_NOALLOC_SCRATCH_BYTES)
+    return fail(NSLG_EWORKSPACE,
+                "paged_decode_noalloc: this call needs %zu bytes of scratch, more than the %zu-byte static "
+                "scratch; call nslg_paged_decode with a workspace",
+                need, (size_t)NSLG_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  GroupArgs<false> ga;
+  return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
+                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                            dtype, out, out_stride, ga, 0, 1, ws, (size_t)NSLG_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const void* k_pool,

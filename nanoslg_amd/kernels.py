@@ -323,6 +323,36 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     return out
 
 
+def paged_decode_noalloc(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                         kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                         total_pages: int, out: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
+    """paged_decode through nslg_paged_decode_noalloc: no workspace, nothing allocated
+    (the library's static per-GPU scratch holds the split-K partials). The caller
+    passes `out` ([B, Hq, D], q's dtype). Calls on one GPU must not overlap. A batch
+    needing more than NSLG_NOALLOC_SCRATCH_BYTES of scratch raises KernelLibraryError
+    (status NSLG_EWORKSPACE) without launching."""
+    _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, out)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, n)
+    P, ps, Hkv, D = _layer_geom(k_layer, v_layer)
+    if q.dim() != 3 or q.shape[2] != D or q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError(f"paged_decode_noalloc: q must be [B, Hq, {D}] with a contiguous [Hq, D] block")
+    if q.dtype != k_layer.dtype:
+        raise TypeError("paged_decode_noalloc: q dtype must match the pool")
+    B, Hq, _ = q.shape
+    if kv_indptr.numel() != B + 1 or kv_last_page_len.numel() < B:
+        raise ValueError("paged_decode_noalloc: kv_indptr must have B+1 entries and kv_last_page_len B")
+    if out.shape != (B, Hq, D) or out.stride(2) != 1 or out.stride(1) != D or out.dtype != q.dtype:
+        raise ValueError("paged_decode_noalloc: bad out tensor")
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    rc = _lib.load().nslg_paged_decode_noalloc(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(),
+                                               P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                               kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
+                                               dtype_code(q.dtype), out.data_ptr(), out.stride(0), _stream(q))
+    _lib.check(rc, "nslg_paged_decode_noalloc")
+    return out
+
+
 def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                      new_page, page_size: int, num_new: int, k_pool: Optional[torch.Tensor] = None,
                      v_pool: Optional[torch.Tensor] = None):

@@ -99,6 +99,20 @@ def test_rope_append_argument_checks():
     assert rope(n=0) == 0
 
 
+def test_noalloc_decode_rejects_oversize_on_host():
+    """nslg_paged_decode_noalloc refuses a call whose scratch need exceeds its static
+    array before any device work (no device is touched here)."""
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    # 1000 sequences over 2^20 pages: several hundred chunks of partials, > 16 MiB
+    need = lib.nslg_paged_decode_workspace_size(1000, 32, 8, 128, 1 << 20, 16, 0)
+    assert need > _lib.NSLG_NOALLOC_SCRATCH_BYTES
+    A = 4096
+    rc = lib.nslg_paged_decode_noalloc(A, 4096, A, A, 1 << 20, 16, A, A, A, 1 << 20, 1000, 32, 8, 128, 0.1, 0,
+                                       A, 4096, None)
+    assert rc == _lib.NSLG_EWORKSPACE and "static scratch" in _lib.last_error()
+
+
 def test_decode_workspace_size_monotone():
     from nanoslg_amd import _lib
     lib = _lib.load()
