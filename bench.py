@@ -514,7 +514,7 @@ def run_radix(args):
         assert plen == full * PS, plen
         st = mgr.seqs[sid]
         own = int(st.bt[full])
-        st.bt[full] = owner_pages[full]  # share the partial page
+        st.set_page(full, owner_pages[full])  # share the partial page
         mgr.pool.add_ref(owner_pages[full])
         mgr.pool.release(own)
         st.num_tokens = PRE

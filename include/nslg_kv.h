@@ -299,6 +299,34 @@ int nslg_decode_plan_step_device(const int32_t* kv_indptr, const int32_t* kv_ind
                                  nslg_stream_t stream);
 
 /*
+ * CSR block table of a forward from device-resident block tables. Replaces the
+ * O(sum of pages) loop of FlashInferCacheContext._plan_flashinfer
+ * (nanoslg/kv_cache.py:598-615, missing entries -> page 0 at :606-607) that
+ * rebuilt the CSR from the Python block tables on every forward, and its upload
+ * (:611-615).
+ *
+ *   tables          int32 arena (device) of table_capacity entries holding one row
+ *                   per sequence: entry i of a row = page id of logical page i
+ *   row_offset      int32[batch]: first arena entry of sequence b's row (rows of
+ *                   the batch must not overlap)
+ *   pages_have      int32[batch]: entries of row b that are valid (pages allocated)
+ *   synced          int32[batch]: entries [0, synced_b) are already in the arena
+ *   patch_indptr    int32[batch+1], patch int32[patch_total]: the values of entries
+ *                   [synced_b, pages_have_b) of row b are patch[patch_indptr[b] ..];
+ *                   they are also written into the arena (rows stay current)
+ *   kv_indptr       int32[batch+1]: CSR pointers of the forward (npg_b pages of b)
+ *   kv_indices      int32[total_pages] out: entry i < npg_b of segment b = row entry
+ *                   i for i < pages_have_b, else 0 (the null page)
+ * All arrays are device memory. Indices outside the arena, the patch or the CSR
+ * are skipped (read as page 0). Bit-exact with the host CSR.
+ */
+int nslg_block_table_csr(int32_t* tables, int64_t table_capacity, const int32_t* row_offset,
+                         const int32_t* pages_have, const int32_t* synced,
+                         const int32_t* patch_indptr, const int32_t* patch, int64_t patch_total,
+                         const int32_t* kv_indptr, int32_t* kv_indices, int64_t total_pages,
+                         int32_t batch, nslg_stream_t stream);
+
+/*
  * Device-side write plan of a multi-token forward: expands the forward's
  * per-sequence tables into the per-token arrays the append and the prefill take.
  * Replaces the per-token loop of FlashInferCacheContext.__init__ (slot of every new

@@ -421,6 +421,40 @@ def forward_plan(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, start: torch
                          int(input_width), int(page_size), int(total_tokens))
 
 
+def block_table_csr(tables: torch.Tensor, row_offset: torch.Tensor, pages_have: torch.Tensor, synced: torch.Tensor,
+                    patch_indptr: torch.Tensor, patch: torch.Tensor, kv_indptr: torch.Tensor,
+                    kv_indices: torch.Tensor) -> torch.Tensor:
+    """CSR indices of a forward from device-resident block-table rows
+    (nslg_block_table_csr): kv_indices[kv_indptr[b] + i] = row entry i of sequence b
+    (entries [synced_b, pages_have_b) taken from `patch` and written into `tables`),
+    0 past pages_have_b. All int32 on the device; rows of the batch must not overlap
+    and must lie inside `tables`. Returns kv_indices."""
+    _require_gpu(tables, row_offset, pages_have, synced, patch_indptr, patch, kv_indptr, kv_indices)
+    for t, n in ((tables, "tables"), (row_offset, "row_offset"), (pages_have, "pages_have"), (synced, "synced"),
+                 (patch_indptr, "patch_indptr"), (patch, "patch"), (kv_indptr, "kv_indptr"),
+                 (kv_indices, "kv_indices")):
+        _i32(t, n)
+    B = kv_indptr.numel() - 1
+    for t in (row_offset, pages_have, synced):
+        if t.numel() != B:
+            raise ValueError(f"block_table_csr: per-sequence arrays must have {B} entries")
+    if patch_indptr.numel() != B + 1:
+        raise ValueError(f"block_table_csr: patch_indptr must have {B + 1} entries")
+    _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch.numel(), kv_indptr,
+                     kv_indices, kv_indices.numel(), B)
+    return kv_indices
+
+
+def _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr,
+                     kv_indices, total_pages, B):
+    """block_table_csr without the argument checks (the cache manager's own tables)."""
+    rc = _lib.load().nslg_block_table_csr(tables.data_ptr(), tables.numel(), row_offset.data_ptr(),
+                                          pages_have.data_ptr(), synced.data_ptr(), patch_indptr.data_ptr(),
+                                          patch.data_ptr(), int(patch_total), kv_indptr.data_ptr(),
+                                          kv_indices.data_ptr(), int(total_pages), int(B), _stream(tables))
+    _lib.check(rc, "nslg_block_table_csr")
+
+
 def _decode_plan_step_device(kv_indptr, kv_indices, kv_last_page_len, new_page, B, page_size, dst, pool_args):
     """The device planner reading the opened-page list from memory at run time (a
     device tensor or a pinned host tensor), for a step captured in a graph: writes the

@@ -241,7 +241,21 @@ class _PlanStaging:
         self.pending = [False] * self.RING
         self.next = 0
 
-    def upload(self, parts: List[np.ndarray], total: int) -> torch.Tensor:
+    def reserve(self, n: int) -> None:
+        """Pin ring buffers of at least n int32 each now, so that no forward whose plan
+        fits pays for a pinned allocation (which costs milliseconds)."""
+        for k in range(self.RING):
+            buf = self.host[k]
+            if buf is None or buf.numel() < n:
+                if self.pending[k]:
+                    self.copied[k].synchronize()
+                    self.pending[k] = False
+                buf = torch.empty(n, dtype=torch.int32, pin_memory=True)
+                self.host[k], self.host_np[k] = buf, buf.numpy()
+
+    def upload(self, parts: List[np.ndarray], total: int, extra: int = 0) -> torch.Tensor:
+        """The concatenated parts on the device, followed by `extra` entries left
+        uninitialised (device outputs of the same forward)."""
         k = self.next
         self.next = (k + 1) % self.RING
         if self.pending[k]:
@@ -257,15 +271,16 @@ class _PlanStaging:
             host[off:off + n] = a.reshape(-1)
             off += n
         self.pending[k] = True
+        size = max(total + extra, 1)
         if 4 * total <= self.SIDE_STREAM_BYTES:
-            dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
+            dev = torch.empty(size, dtype=torch.int32, device=self.device)
             if total:
-                (dev if total == dev.numel() else dev[:total]).copy_(buf[:total], non_blocking=True)
+                (dev if total == size else dev[:total]).copy_(buf[:total], non_blocking=True)
             self.copied[k].record(_current_stream(self.index))  # on the compute stream
             return dev
         main = _current_stream(self.index)
         with torch.cuda.stream(self.side):
-            dev = torch.empty(max(total, 1), dtype=torch.int32, device=self.device)
+            dev = torch.empty(size, dtype=torch.int32, device=self.device)
             dev[:total].copy_(buf[:total], non_blocking=True)
             self.copied[k].record(self.side)
         main.wait_event(self.copied[k])
@@ -285,18 +300,22 @@ def _staging(device: torch.device) -> _PlanStaging:
     return st
 
 
-def _upload_i32(parts: List[np.ndarray], device: torch.device) -> List[torch.Tensor]:
+def _upload_i32(parts: List[np.ndarray], device: torch.device, extra: int = 0) -> List[torch.Tensor]:
     """Concatenate int32 arrays, copy them to `device` at once, return the views (one
-    per part). On a GPU this goes through the device's _PlanStaging."""
+    per part; with extra > 0, one more view of `extra` uninitialised entries in the
+    same buffer, for a device output). On a GPU this goes through the device's
+    _PlanStaging."""
     sizes = [int(a.size) for a in parts]
     total = sum(sizes)
     if device.type == "cuda":
-        dev = _staging(device).upload([np.asarray(a) for a in parts], total)
+        dev = _staging(device).upload([np.asarray(a) for a in parts], total, extra)
     else:
-        dev = torch.from_numpy(np.concatenate([np.asarray(a, dtype=np.int32).reshape(-1) for a in parts])
-                               if parts else np.zeros(0, np.int32)).clone()
-    if dev.numel() > total:
-        sizes = sizes + [dev.numel() - total]
+        dev = torch.from_numpy(np.concatenate([np.asarray(a, dtype=np.int32).reshape(-1) for a in parts]
+                                              + [np.zeros(extra, np.int32)])).clone()
+    if extra:
+        sizes = sizes + [extra]
+    if dev.numel() > sum(sizes):
+        sizes = sizes + [dev.numel() - sum(sizes)]
         return list(dev.split(sizes))[:-1]
     return list(dev.split(sizes))
 
@@ -675,8 +694,14 @@ class RadixTree:
 
 
 class _PagedSeqState:
-    """Per-sequence state (kv_cache.py:534-542); the block table is an int32 array."""
-    __slots__ = ("seq_id", "bt", "n_pages", "num_tokens", "prefix_len", "token_ids")
+    """Per-sequence state (kv_cache.py:534-542); the block table is an int32 array.
+
+    The table also lives on the device, as a row of the cache's _BlockTableArena:
+    `row`/`row_cap` locate it there (-1 before the sequence's first forward) and
+    `synced` counts the leading entries the device row already holds. Entries are
+    only appended (extend) or replaced through set_page, which lowers `synced`, so
+    the device row never goes stale."""
+    __slots__ = ("seq_id", "bt", "n_pages", "num_tokens", "prefix_len", "token_ids", "row", "row_cap", "synced")
 
     def __init__(self, sid, prefix_pages=None, plen=0, tids=None):
         self.seq_id = sid
@@ -687,6 +712,7 @@ class _PagedSeqState:
         self.num_tokens = plen
         self.prefix_len = plen
         self.token_ids = list(tids or [])
+        self.row, self.row_cap, self.synced = -1, 0, 0
 
     @property
     def block_table(self) -> List[int]:
@@ -700,6 +726,66 @@ class _PagedSeqState:
             self.bt = nb
         self.bt[self.n_pages:need] = pages
         self.n_pages = need
+
+    def set_page(self, i: int, pid: int) -> None:
+        """Logical page i now lives in pool page pid (copy-on-write, shared pages)."""
+        self.bt[i] = pid
+        if i < self.synced:
+            self.synced = i
+
+
+class _BlockTableArena:
+    """The cache's block tables on the device: one int32 row per live sequence in a
+    persistent device array (row entry i = the pool page of logical page i).
+
+    A forward builds its CSR block table from these rows on the device
+    (nslg_block_table_csr), uploading only the entries its sequences gained or
+    changed since their rows were last used; that launch also writes those entries
+    into the rows. Rows have power-of-two capacities (at least 1.5x the table when
+    placed, so decode growth rarely moves them) and are recycled through
+    per-capacity free lists; a table that outgrows its row moves to a larger one
+    and is uploaded whole once. The array doubles when full (a device copy on the
+    current stream, so every launch that used the old array comes first)."""
+
+    MIN_ROW = 16
+
+    def __init__(self, device: torch.device, capacity: int):
+        self.device = device
+        self.dev = torch.zeros(max(int(capacity), self.MIN_ROW), dtype=torch.int32, device=device)
+        self.top = 0
+        self.free: Dict[int, List[int]] = {}
+
+    def _take(self, need: int) -> Tuple[int, int]:
+        cap = self.MIN_ROW
+        while cap < need:
+            cap *= 2
+        lst = self.free.get(cap)
+        if lst:
+            return lst.pop(), cap
+        if self.top + cap > self.dev.numel():
+            n = self.dev.numel()
+            while n < self.top + cap:
+                n *= 2
+            grown = torch.zeros(n, dtype=torch.int32, device=self.device)
+            grown[:self.top].copy_(self.dev[:self.top])
+            self.dev = grown
+        off = self.top
+        self.top += cap
+        return off, cap
+
+    def place(self, st: _PagedSeqState) -> None:
+        """Make sure st has a row that holds its whole table (a fresh row starts
+        unsynced)."""
+        if st.row >= 0 and st.n_pages <= st.row_cap:
+            return
+        self.release(st)
+        st.row, st.row_cap = self._take(st.n_pages + st.n_pages // 2)
+        st.synced = 0
+
+    def release(self, st: _PagedSeqState) -> None:
+        if st.row >= 0:
+            self.free.setdefault(st.row_cap, []).append(st.row)
+        st.row, st.row_cap, st.synced = -1, 0, 0
 
 
 class PagedCacheContext(CacheContext):
@@ -741,7 +827,7 @@ class PagedCacheContext(CacheContext):
                 raise RuntimeError("KV OOM during CoW")
             cow_src.append(pid)
             cow_dst.append(new)
-            st.bt[p] = new
+            st.set_page(p, new)
             pool.release(pid)
 
         self._decode_launch = None
@@ -753,187 +839,136 @@ class PagedCacheContext(CacheContext):
                 self._plan = plan
                 cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
                 return
+        # Below, the host works per sequence and per written page only. The CSR block
+        # table itself (kv_cache.py:598-615) is built on the device from the cache's
+        # device-resident block tables (PagedKVCache._plan_upload).
+        start = np.fromiter(self.start_positions, np.int64, B)
+        have = np.fromiter((st.n_pages for st in states), np.int64, B)
+        zero = np.asarray(zero_pages if zero_pages else [], np.int32)
         groups = None
+        device_plan = False
         if self._is_decode and iw == 1:
-            # One token per sequence, vectorised over the batch. The page written by
-            # sequence b is the last page of its CSR segment; only a page that is shared
-            # before any copy can need one, so the candidates are re-checked in batch
-            # order, which reproduces the sequential rule exactly.
-            start = np.fromiter(self.start_positions, np.int64, B)
-            have = np.fromiter((st.n_pages for st in states), np.int64, B)
+            # One token per sequence, vectorised over the batch. Only a page that is
+            # shared before any copy can need one, so the candidates are re-checked in
+            # batch order, which reproduces the sequential rule exactly.
             lens = start + 1
             npg = (lens + ps - 1) // ps
-            indptr = np.zeros(B + 1, np.int64)
-            np.cumsum(npg, out=indptr[1:])
-            if bool((npg <= have).all()):
-                indices = np.concatenate([st.bt[:k] for st, k in zip(states, npg.tolist())])
-            else:
-                indices = self._csr_indices(states, npg)
             pi = npg - 1
             sl = start - pi * ps
             ok = pi < have
-            last = indptr[1:] - 1
-            pids = np.where(ok, indices[last], 0).astype(np.int64)
+            pids = np.fromiter((int(st.bt[p]) if o else 0 for st, p, o in zip(states, pi.tolist(), ok.tolist())),
+                               np.int64, B)
             cand = np.nonzero(ok & (pool.ref_count[pids] > 1))[0]
             for b in cand.tolist():
                 st = states[b]
                 if pool.is_shared(int(st.bt[pi[b]])):
                     _cow(st, int(pi[b]))
                     pids[b] = st.bt[pi[b]]
-                    indices[last[b]] = pids[b]
             slot = np.where(ok, pids * ps + sl, 0).astype(np.int32)
             if ok.any():
                 np.maximum.at(pool.tokens_used, pids[ok], sl[ok] + 1)
             lpl = lens - pi * ps
             pos = start.astype(np.int32)
-            q_rows = np.arange(B, dtype=np.int64)
-            qo = np.arange(B + 1, dtype=np.int64)
+            q_rows = np.arange(B, dtype=np.int32)
+            qo = np.arange(B + 1, dtype=np.int32)
             groups = cache._prefix_groups(states, npg)
         else:
             ncnt = np.fromiter(self.new_token_counts, np.int64, B)
-            start = np.fromiter(self.start_positions, np.int64, B)
-            have = np.fromiter((st.n_pages for st in states), np.int64, B)
-            # CSR block table (kv_cache.py:598-615), before copy-on-write
             lens = start + ncnt
             npg = np.where(lens > 0, (lens + ps - 1) // ps, 0)
-            indptr = np.zeros(B + 1, np.int64)
-            np.cumsum(npg, out=indptr[1:])
-            indices = self._csr_indices(states, npg)
-            # copy-on-write, in batch order: a sequence writes its pages
-            # start//ps .. (start+n-1)//ps (those it has); shared ones are copied. Only a
-            # sequence writing a page that is shared before any copy can need one (copies
-            # only lower refcounts), so those are found at once on the CSR and the rule is
-            # then applied to them in batch order; their copies are patched into the CSR.
+            # The pages this forward writes that the sequences have: sequence b writes
+            # pages p0_b .. p0_b + cnt_b - 1 (start//ps .. (start+n-1)//ps, those below
+            # its page count); their ids, concatenated in batch order, are `wp`.
             n = np.maximum(ncnt, 0)
             p0 = start // ps
-            cnt = np.where(n > 0, np.maximum(np.minimum((start + n - 1) // ps + 1, have) - p0, 0), 0)
+            plast = (start + n - 1) // ps
+            cnt = np.where(n > 0, np.maximum(np.minimum(plast + 1, have) - p0, 0), 0)
+            wfirst = np.zeros(B, np.int64)
+            if B:
+                np.cumsum(cnt[:-1], out=wfirst[1:])
             tot = int(cnt.sum())
             if tot:
+                wp = np.concatenate([st.bt[a:a + c] for st, a, c in zip(states, p0.tolist(), cnt.tolist()) if c]
+                                    ).astype(np.int64)
+                # copy-on-write, in batch order. Copies only lower refcounts, so only a
+                # page shared before any copy can need one: those are found on `wp` at
+                # once, then the rule is applied to their sequences in batch order.
                 rep = np.repeat(np.arange(B), cnt)
-                first = np.zeros(B, np.int64)
-                np.cumsum(cnt[:-1], out=first[1:])
-                at = indptr[rep] + p0[rep] + (np.arange(tot, dtype=np.int64) - first[rep])
-                hit = pool.ref_count[indices[at]] > 1
+                hit = pool.ref_count[wp] > 1
                 if bool(hit.any()):
                     for b in np.unique(rep[hit]).tolist():
                         st = states[b]
                         for p in range(int(p0[b]), int(p0[b] + cnt[b])):
                             if pool.is_shared(int(st.bt[p])):
                                 _cow(st, p)
-                                indices[indptr[b] + p] = st.bt[p]
+                                wp[wfirst[b] + p - p0[b]] = st.bt[p]
+                # tokens_used (kv_cache.py:593): each written page once, with its last
+                # slot written; the pages written are distinct after copy-on-write
+                pidx = p0[rep] + (np.arange(tot, dtype=np.int64) - wfirst[rep])
+                last = np.where(pidx == plast[rep], (start + n - 1 - plast * ps)[rep], ps - 1)
+                pool.tokens_used[wp] = np.maximum(pool.tokens_used[wp], last + 1)
+            else:
+                wp = np.zeros(1, np.int64)
             T = int(ncnt.sum())
             device_plan = T >= self.DEVICE_PLAN_TOKENS and hasattr(cache.kernels, "_forward_plan")
-            if device_plan:
-                # per-token slots, positions and the ragged layout are expanded on the
-                # device (kernels.forward_plan); here only tokens_used, per written page
-                self._pages_used(pool, states, start, ncnt, have, indices, indptr, ps)
-            # per new token: absolute position, page, slot; past a sequence's pages the
-            # write goes to the null page's slot 0 (kv_cache.py:583-584)
-            slot = np.full(B * iw, -1, np.int32)
-            if T and not device_plan:
-                rep = np.repeat(np.arange(B), ncnt)
-                first = np.zeros(B, np.int64)
-                np.cumsum(ncnt[:-1], out=first[1:])
-                t_in = np.arange(T, dtype=np.int64) - first[rep]
-                ap = start[rep] + t_in
-                pi = ap // ps
-                ok = pi < have[rep]
-                pids = np.where(ok, indices[indptr[rep] + pi], 0).astype(np.int64)
-                sls = np.where(ok, ap - pi * ps, 0)
-                offs = np.fromiter(self.input_offsets, np.int64, B)
-                slot[rep * iw + offs[rep] + t_in] = (pids * ps + sls).astype(np.int32)
-                # tokens_used: each written page once, with its last (largest) slot;
-                # the pages written are distinct after copy-on-write
-                wp, ws = pids[ok], sls[ok]
-                if wp.size:
-                    last = np.flatnonzero(np.append(wp[1:] != wp[:-1], True))
-                    pu = wp[last]
-                    pool.tokens_used[pu] = np.maximum(pool.tokens_used[pu], ws[last] + 1)
-            slot = slot.reshape(B, iw)
             lpl = np.where(npg > 0, lens - (npg - 1) * ps, 0)
             if B == 0:
                 lpl = np.zeros(1, np.int64)
-            if device_plan:
-                self._plan_on_device(cache, B, iw, T, start, ncnt, have, indptr, indices, lpl, cow_src, cow_dst,
-                                     zero_pages)
-                return
-            pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
+            if not device_plan:
+                # per new token: absolute position, page, slot; past a sequence's pages
+                # the write goes to the null page's slot 0 (kv_cache.py:583-584)
+                slot = np.full(B * iw, -1, np.int32)
+                if T:
+                    rep = np.repeat(np.arange(B), ncnt)
+                    first = np.zeros(B, np.int64)
+                    np.cumsum(ncnt[:-1], out=first[1:])
+                    t_in = np.arange(T, dtype=np.int64) - first[rep]
+                    ap = start[rep] + t_in
+                    pi = ap // ps
+                    ok = pi < have[rep]
+                    pids = np.where(ok, wp[np.where(ok, wfirst[rep] + pi - p0[rep], 0)], 0)
+                    sls = np.where(ok, ap - pi * ps, 0)
+                    offs = np.fromiter(self.input_offsets, np.int64, B)
+                    slot[rep * iw + offs[rep] + t_in] = (pids * ps + sls).astype(np.int32)
+                pos, q_rows, qo = _ragged_layout(self.start_positions, self.new_token_counts, self.input_offsets, iw)
+        indptr = np.zeros(B + 1, np.int64)
+        np.cumsum(npg, out=indptr[1:])
+        total_pages = int(indptr[-1])
         self.cow_pairs = list(zip(cow_src, cow_dst))
-        if indices.size == 0:
-            indices = np.zeros(1, np.int32)
         self._max_q = max(self.new_token_counts) if B else 0
-        self._uniform_rows = int(qo[-1]) == B * iw  # every grid row carries a new token
-
-        group_spec = groups
-        self._plan = _ForwardPlan(pool.device, B, iw, slot.reshape(-1), pos, indptr, indices, lpl, qo,
-                                  q_rows, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32),
-                                  zero_pages, group_slot=group_spec[2] if group_spec else None)
-        if group_spec:
-            self._plan.groups = cache.kernels.DecodeGroups(B, group_spec[0], group_spec[1], pool.device,
-                                                           seq_group_slot=self._plan.group_slot)
+        cs, cd = np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32)
+        kern = cache.kernels
+        if device_plan:
+            # per-token slots, positions and the ragged layout expanded on the device
+            offs = np.fromiter(self.input_offsets, np.int64, B)
+            views, d_idx = cache._plan_upload(states, indptr, [lpl, cs, cd, zero, start, ncnt, offs, have])
+            d_indptr, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have = views
+            slot_t, pos_t, rows_t, qo_t = kern._forward_plan(d_indptr, d_idx, d_start, d_n, d_off, d_have, B, iw,
+                                                             ps, T)
+            self._uniform_rows = T == B * iw
+            self._plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t,
+                                                   d_cs, d_cd, d_zero, total_pages, T)
+        else:
+            parts = [slot.reshape(-1), pos, lpl, qo, q_rows, cs, cd, zero]
+            if groups is not None:
+                parts.append(groups[2])
+            views, d_idx = cache._plan_upload(states, indptr, parts)
+            d_indptr, d_slot, d_pos, d_lpl, d_qo, d_qr, d_cs, d_cd, d_zero = views[:9]
+            self._uniform_rows = int(qo[-1]) == B * iw  # every grid row carries a new token
+            self._plan = _ForwardPlan.from_tensors(B, iw, d_slot, d_pos, d_indptr, d_idx, d_lpl, d_qo, d_qr,
+                                                   d_cs, d_cd, d_zero, total_pages, int(qo[-1]))
+            if groups is not None:
+                self._plan.group_slot = views[9]
+                self._plan.groups = kern.DecodeGroups(B, groups[0], groups[1], pool.device,
+                                                      seq_group_slot=views[9])
         if zero_pages:  # zero-on-alloc of the pages this forward's extensions took
-            cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
+            kern.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
-            cache.kernels.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
+            kern.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
         if self._is_decode and iw == 1:
             cache._record_decode_plan(self.seq_ids, self._plan, self.seq_lens)
 
     DEVICE_PLAN_TOKENS = 256  # forwards with at least this many new tokens expand their plan on the device
-
-    @staticmethod
-    def _pages_used(pool, states, start, ncnt, have, indices, indptr, ps) -> None:
-        """tokens_used of the pages this forward writes (kv_cache.py:593): each page
-        once, with its last slot written; per page rather than per token."""
-        n = np.maximum(ncnt, 0)
-        p0 = start // ps
-        plast = (start + n - 1) // ps
-        pend = np.minimum(plast, have - 1)  # pages past the allocated ones are not counted
-        cnt = np.where(n > 0, np.maximum(pend - p0 + 1, 0), 0)
-        tot = int(cnt.sum())
-        if not tot:
-            return
-        B = len(states)
-        rep = np.repeat(np.arange(B), cnt)
-        first = np.zeros(B, np.int64)
-        np.cumsum(cnt[:-1], out=first[1:])
-        pi = p0[rep] + (np.arange(tot, dtype=np.int64) - first[rep])
-        pid = indices[indptr[rep] + pi].astype(np.int64)
-        last = np.where(pi == plast[rep], (start + n - 1 - plast * ps)[rep], ps - 1)
-        pool.tokens_used[pid] = np.maximum(pool.tokens_used[pid], last + 1)
-
-    def _plan_on_device(self, cache, B, iw, T, start, ncnt, have, indptr, indices, lpl, cow_src, cow_dst,
-                        zero_pages) -> None:
-        """Upload the forward's small tables and expand the per-token plan on the device."""
-        pool = cache.pool
-        offs = np.fromiter(self.input_offsets, np.int64, B)
-        up = _upload_i32([indptr, indices, lpl, np.asarray(cow_src, np.int32), np.asarray(cow_dst, np.int32),
-                          np.asarray(zero_pages if zero_pages else [], np.int32), start, ncnt, offs, have],
-                         pool.device)
-        d_indptr, d_indices, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have = up
-        slot, pos, rows, qo = cache.kernels._forward_plan(d_indptr, d_indices, d_start, d_n, d_off, d_have, B, iw,
-                                                          cache.cfg.page_size, T)
-        self.cow_pairs = list(zip(cow_src, cow_dst))
-        self._max_q = max(self.new_token_counts) if B else 0
-        self._uniform_rows = T == B * iw
-        self._plan = _ForwardPlan.from_tensors(B, iw, slot, pos, d_indptr, d_indices, d_lpl, qo, rows, d_cs, d_cd,
-                                               d_zero, int(indptr[-1]), T)
-        if zero_pages:
-            cache.kernels.zero_pages(pool.k, pool.v, d_zero)
-        if cow_src:
-            cache.kernels.copy_pages(pool.k, pool.v, d_cs, d_cd)
-
-    @staticmethod
-    def _csr_indices(states, npg) -> np.ndarray:
-        """Concatenated block tables, npg[b] pages of sequence b; pages missing from a
-        table read the null page (kv_cache.py:606-607)."""
-        parts = []
-        for k, st in zip(npg.tolist(), states):
-            if k <= st.n_pages:
-                parts.append(st.bt[:k])
-            else:
-                parts.append(st.bt[:st.n_pages])
-                parts.append(np.zeros(k - st.n_pages, np.int32))
-        return np.concatenate(parts) if parts else np.zeros(0, np.int32)
 
     # ---- CacheContext -----------------------------------------------------------------
     def get_position_ids(self, S: int) -> torch.Tensor:
@@ -1018,6 +1053,42 @@ class PagedKVCache(KVCacheManager):
         self._launcher = None  # the last decode forward's kernels.DecodeLaunch
         self._pool_args = None  # the pools as the device planner takes them
         self._decode_rows: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        # the block tables on the device (room for every pool page twice before growing)
+        self._tables = _BlockTableArena(self.pool.device, 2 * cfg.max_pages + 4096)
+        if self.pool.device.type == "cuda":
+            _staging(self.pool.device).reserve(self.STAGING_INTS)
+
+    STAGING_INTS = 1 << 16  # pinned plan-upload buffers (int32 each) set up with the cache
+
+    def _plan_upload(self, states, indptr, parts):
+        """One upload of a forward's host-built plan arrays (`parts`, after the CSR
+        pointers `indptr`) together with the block-table entries its sequences gained
+        or changed since their device rows were last used; then the forward's CSR
+        indices built on the device from those rows (nslg_block_table_csr), which
+        also brings the rows up to date. Returns ([indptr] + views of parts,
+        kv_indices) on the device."""
+        tables = self._tables
+        B = len(states)
+        for st in states:
+            tables.place(st)
+        row = np.fromiter((st.row for st in states), np.int32, B)
+        have = np.fromiter((st.n_pages for st in states), np.int32, B)
+        syn = np.minimum(np.fromiter((st.synced for st in states), np.int32, B), have)
+        pip = np.zeros(B + 1, np.int32)
+        np.cumsum(have - syn, out=pip[1:])
+        npatch = int(pip[-1])
+        patch = (np.concatenate([st.bt[s:h] for st, s, h in zip(states, syn.tolist(), have.tolist()) if h > s])
+                 if npatch else np.zeros(1, np.int32))
+        total = int(indptr[-1])
+        up = _upload_i32([indptr] + list(parts) + [row, have, syn, pip, patch], self.pool.device,
+                         extra=max(total, 1))
+        k = len(parts) + 1
+        d_row, d_have, d_syn, d_pip, d_patch, d_idx = up[k:k + 6]
+        self.kernels._block_table_csr(tables.dev, d_row, d_have, d_syn, d_pip, d_patch, npatch, up[0], d_idx,
+                                      total, B)
+        for st in states:
+            st.synced = st.n_pages
+        return up[:k], d_idx
 
     # ---- decode plans built on the device ---------------------------------------------
     def _record_decode_plan(self, seq_ids, plan, seq_lens) -> None:
@@ -1203,6 +1274,9 @@ class PagedKVCache(KVCacheManager):
         new = total - plen
         if new > 0:
             st.extend(self._alloc(math.ceil(new / self.cfg.page_size)))
+        old = self.seqs.get(seq_id)
+        if old is not None:  # a re-used id: its old table's device row is free again
+            self._tables.release(old)
         self.seqs[seq_id] = st
         return plen
 
@@ -1264,6 +1338,7 @@ class PagedKVCache(KVCacheManager):
                 self.tree.dec_refs(st.token_ids[:st.prefix_len])
         for p in st.bt[:st.n_pages].tolist():
             self.pool.release(p)
+        self._tables.release(st)
         del self.seqs[seq_id]
 
     def append_token_ids(self, seq_id, ids):

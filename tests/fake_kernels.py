@@ -180,6 +180,30 @@ class DecodeGroups:
         self.seq_group_slot = seq_group_slot
 
 
+def _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr,
+                     kv_indices, total_pages, B):
+    """As nanoslg_amd.kernels._block_table_csr, in plain Python on the CPU."""
+    CALLS.append(("block_table_csr", int(B)))
+    row, have, syn = row_offset.tolist(), pages_have.tolist(), synced.tolist()
+    pip, pat, ip = patch_indptr.tolist(), patch.tolist(), kv_indptr.tolist()
+    cap = tables.numel()
+    for b in range(B):
+        for i in range(max(have[b], ip[b + 1] - ip[b])):
+            pid = 0
+            if i < have[b]:
+                at = row[b] + i
+                inside = 0 <= row[b] and at < cap
+                if i >= syn[b]:
+                    k = pip[b] + i - syn[b]
+                    pid = pat[k] if 0 <= k < patch_total else 0
+                    if inside:
+                        tables[at] = pid
+                elif inside:
+                    pid = int(tables[at])
+            if i < ip[b + 1] - ip[b] and ip[b] + i < total_pages:
+                kv_indices[ip[b] + i] = pid
+
+
 def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
     """As nanoslg_amd.kernels._forward_plan, in plain Python on the CPU."""
     CALLS.append(("forward_plan", T))

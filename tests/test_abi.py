@@ -99,6 +99,17 @@ def test_rope_append_argument_checks():
     assert rope(n=0) == 0
 
 
+def test_block_table_csr_argument_checks():
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    A = 4096
+    assert lib.nslg_block_table_csr(None, 0, None, None, None, None, None, 0, None, None, 0, 0, None) == 0
+    assert lib.nslg_block_table_csr(A, 64, A, A, A, A, A, 1, A, A, 4, -1, None) == -1  # negative batch
+    assert lib.nslg_block_table_csr(None, 64, A, A, A, A, A, 1, A, A, 4, 2, None) == -1  # no arena
+    assert lib.nslg_block_table_csr(A, 64, A, A, A, A, None, 3, A, A, 4, 2, None) == -1  # patch missing
+    assert "block_table_csr" in _lib.last_error()
+
+
 def test_noalloc_decode_rejects_oversize_on_host():
     """nslg_paged_decode_noalloc refuses a call whose scratch need exceeds its static
     array before any device work (no device is touched here)."""

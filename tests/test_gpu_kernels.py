@@ -686,3 +686,55 @@ def test_decode_grouped_rejects_bad_groups():
     assert call(1, [1], [0, 9]) == -1          # not a batch row
     assert call(2, [1, 1], [0, 1] + [-1] * 14 + [1]) == -1  # a sequence in two groups
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("B,ps,seed", [(37, 16, 1), (5, 1, 2), (300, 16, 3)])
+def test_block_table_csr_bit_exact(B, ps, seed):
+    """The forward's CSR built from device-resident block-table rows
+    (nslg_block_table_csr) equals the oracle's CSR of the same tables
+    (kv_cache.py:598-615, missing pages -> the null page :606-607): rows partly
+    synced (the rest from the upload), sequences needing more pages than they have,
+    empty sequences; the uploaded entries land in the rows and no other arena entry
+    changes."""
+    _log(f"block table csr B={B} ps={ps}")
+    from nanoslg_amd import kernels as K
+    rng = np.random.default_rng(seed)
+    have = [int(x) for x in rng.integers(0, 300, size=B)]
+    have[0] = 0
+    tables = [rng.integers(1, 1 << 20, size=h).tolist() for h in have]
+    # tokens the forward sees: within the pages the sequence has, or past them
+    lens = []
+    for b, h in enumerate(have):
+        if b % 7 == 3:
+            lens.append((h + 2) * ps)          # two pages past the table: null pages
+        elif h == 0:
+            lens.append(0)
+        else:
+            lens.append(int(rng.integers((h - 1) * ps + 1, h * ps + 1)) if b % 5 else max(0, (h - 3) * ps))
+    synced = [int(rng.integers(0, h + 1)) if h else 0 for h in have]
+    # disjoint rows at random offsets of an arena filled with junk
+    caps = [max(16, h + int(rng.integers(0, 40))) for h in have]
+    order = rng.permutation(B)
+    offs = np.zeros(B, np.int64)
+    o = 0
+    for b in order:
+        offs[b] = o
+        o += caps[b] + int(rng.integers(0, 9))
+    arena = rng.integers(-5, 1 << 20, size=o + 64).astype(np.int32)
+    for b in range(B):
+        arena[offs[b]:offs[b] + synced[b]] = tables[b][:synced[b]]
+    patch = [x for b in range(B) for x in tables[b][synced[b]:]] or [0]
+    pip = np.zeros(B + 1, np.int32)
+    np.cumsum([h - s for h, s in zip(have, synced)], out=pip[1:])
+    indptr, indices, _ = O.plan_csr(tables, lens, ps)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)  # noqa: E731
+    d_arena = t(arena)
+    d_idx = torch.full((max(int(indptr[-1]), 1),), -7, dtype=torch.int32, device=DEV)
+    K.block_table_csr(d_arena, t(offs), t(have), t(synced), t(pip), t(patch), t(indptr), d_idx)
+    torch.cuda.synchronize()
+    n = int(indptr[-1])
+    assert np.array_equal(d_idx.cpu().numpy()[:n], indices[:n])
+    want = arena.copy()
+    for b in range(B):
+        want[offs[b]:offs[b] + have[b]] = tables[b]
+    assert np.array_equal(d_arena.cpu().numpy(), want)

@@ -224,7 +224,7 @@ def test_radix_cow_full_size():
         st = mgr.seqs[sid]
         assert st.bt[:full].tolist() == owner_pages[:full]
         own = int(st.bt[full])
-        st.bt[full] = owner_pages[full]
+        st.set_page(full, owner_pages[full])
         mgr.pool.add_ref(owner_pages[full])
         mgr.pool.release(own)
         st.num_tokens = PRE

@@ -127,7 +127,7 @@ def _share_page(mgr_or_ref, ids, page, tokens):
     for s in ids:
         st = mgr_or_ref.seqs[s]
         if isinstance(st, KC._PagedSeqState):
-            st.bt[0] = page
+            st.set_page(0, page)
             st.n_pages = 1
         else:
             st.block_table = [page]

@@ -34,11 +34,13 @@ def _make(ps, pages, env):
                            page_size=ps, max_pages=pages, dtype=env["dtype"], device=env["device"],
                            enable_prefix_caching=True, backend="paged")
     kernels = FK if env["device"] is None else None
+    mgr = KC.PagedKVCache(cfg, kernels=kernels)
+    if env.get("arena"):  # a small device block-table arena: it grows and rows move often
+        mgr._tables = KC._BlockTableArena(mgr.pool.device, env["arena"])
     # the oracle's match stops at an evicted page, as the product's does (the
     # reference's match returns the pages past it, a block table with a gap)
-    return (KC.PagedKVCache(cfg, kernels=kernels),
-            O.PagedRef(L, pages, ps, env["HKV"], env["D"], torch.float32, enable_prefix_caching=True,
-                       stop_at_gap=True))
+    return (mgr, O.PagedRef(L, pages, ps, env["HKV"], env["D"], torch.float32, enable_prefix_caching=True,
+                            stop_at_gap=True))
 
 
 def _logical(cache, sid, layer, ps):
@@ -87,9 +89,27 @@ def _forward(mgr, ref, ids, ntok, offs, g, env):
     return None
 
 
+def check_device_tables(mgr):
+    """The device-resident block tables: every live sequence's row holds its host
+    table up to the synced mark, and the rows of live sequences do not overlap."""
+    tables = mgr._tables.dev.cpu()
+    spans = []
+    for st in mgr.seqs.values():
+        if st.row < 0:
+            continue
+        # (a table may outgrow its row between forwards: the next forward moves it)
+        assert 0 <= st.synced <= min(st.n_pages, st.row_cap)
+        assert st.row + st.row_cap <= tables.numel()
+        assert tables[st.row:st.row + st.synced].tolist() == st.bt[:st.synced].tolist(), st.seq_id
+        spans.append((st.row, st.row + st.row_cap))
+    spans.sort()
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+
+
 def _check(mgr, ref, live, ps):
     assert mgr.pool.num_free == ref.pool.num_free
     assert mgr.tree.cached_pages == ref.tree.cached_pages
+    check_device_tables(mgr)
     for sid in live:
         assert mgr.seqs[sid].num_tokens == ref.seqs[sid].num_tokens
         for layer in range(L):
@@ -105,6 +125,13 @@ def _check(mgr, ref, live, ps):
                                            (6, 4, 20), (7, 2, 24), (8, 8, 40), (9, 3, 30), (10, 16, 12)])
 def test_random_serving_traffic_matches_oracle(seed, ps, pages):
     run_traffic(seed, ps, pages, CPU)
+
+
+@pytest.mark.parametrize("seed,ps,pages", [(11, 1, 90), (12, 2, 60), (13, 1, 40)])
+def test_random_serving_traffic_with_a_small_block_table_arena(seed, ps, pages):
+    """The same traffic with the device block tables in a 16-entry arena: it grows
+    (device copy) and tables move to larger rows (re-uploaded) many times."""
+    run_traffic(seed, ps, pages, dict(CPU, arena=16))
 
 
 def run_traffic(seed, ps, pages, env):
