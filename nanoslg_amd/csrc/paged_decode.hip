@@ -246,6 +246,15 @@ __device__ inline const uint16_t* token_row(const uint16_t* pool, const int32_t*
   return pool + ((int64_t)pid * page_size + (tok % page_size)) * row_elems + head_off;
 }
 
+// K/V rows are streamed: each byte is read once per decode call, so the loads carry
+// the non-temporal hint (`nt`), which keeps them from displacing other lines in the
+// caches. Measured on the KV-pressure page pattern (pure loads, 3 GB): 6.15 TB/s
+// plain, 6.95 TB/s non-temporal.
+template <typename V>
+__device__ inline V stream_load(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+}
+
 // Loads of one tile whose 16 token rows are consecutive in one page, for the
 // lane's MFMA operand positions. kbase/vbase: wave-uniform byte address of the
 // tile's first row (head offset included); rows past `last` repeat row `last`.
@@ -261,11 +270,11 @@ __device__ inline void load_tile_rows(const char* kbase, const char* vbase, int 
   typedef typename RowVec<NT>::type VT;
   const char* kp = kbase + (r < last ? r : last) * row_bytes + 16 * gq;
 #pragma unroll
-  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = *reinterpret_cast<const u16x8*>(kp + 64 * s);
+  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = stream_load<u16x8>(kp + 64 * s);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int vr = 4 * gq + j;
-    t.v[j] = *reinterpret_cast<const VT*>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
+    t.v[j] = stream_load<VT>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
   }
 }
 
@@ -284,13 +293,14 @@ __device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, 
   tk = tk > t_last ? t_last : tk;
   const uint16_t* krow = token_row(p.k_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tk);
 #pragma unroll
-  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s + 8 * gq);
+  for (int s = 0; s < Tile<D>::kSteps; ++s)
+    t.k[s] = stream_load<u16x8>(reinterpret_cast<const char*>(krow + 32 * s + 8 * gq));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     int tv = t0 + 4 * gq + j;
     tv = tv > t_last ? t_last : tv;
     const uint16_t* vrow = token_row(p.v_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tv);
-    t.v[j] = *reinterpret_cast<const VT*>(vrow + NT * r);
+    t.v[j] = stream_load<VT>(reinterpret_cast<const char*>(vrow + NT * r));
   }
 }
 
