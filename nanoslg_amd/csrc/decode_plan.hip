@@ -79,7 +79,7 @@ __device__ void zero_part(const PlanStepArgs& a, int z) {
   const int64_t end = min(off0 + (int64_t)kZeroBytes, a.page_bytes);
   const u32x4 zero = {0u, 0u, 0u, 0u};
   for (int64_t off = off0 + 16 * (int64_t)threadIdx.x; off < end; off += 16 * (int64_t)blockDim.x)
-    *reinterpret_cast<u32x4*>(base + off) = zero;
+    stream_store(reinterpret_cast<u32x4*>(base + off), zero);
 }
 
 // Pages of sequence s before the step, and whether this step opens one.

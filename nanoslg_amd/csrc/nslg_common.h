@@ -106,6 +106,17 @@ __device__ inline float rows_sum(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- streaming (non-temporal) vector accesses -----------------------------------
+// Pool pages written by the append / zero / copy kernels are not read again by the
+// writing kernel: stored with the non-temporal hint they go out to HBM instead of
+// lingering as dirty lines in the memory-side cache, where the next decode, which
+// streams the whole pool, would pay for writing them back (measured: a decode right
+// after ~300 MB of ordinary stores into the pool, 590 us instead of 470 us).
+template <typename V>
+__device__ inline void stream_store(V* p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 // ---- fp32 attention (attn_f32.hip), shared by the decode and prefill entries ----
 struct AttnF32Args {
   const float* q;

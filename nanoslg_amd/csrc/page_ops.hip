@@ -26,7 +26,7 @@ append_rows_kernel(const char* __restrict__ k_src, const char* __restrict__ v_sr
                                             (int64_t)t * (is_v ? v_src_stride : k_src_stride));
   V* dst = reinterpret_cast<V*>((is_v ? v_pool : k_pool) + (int64_t)slot * row_bytes);
   const int nvec = row_bytes / (int)sizeof(V);
-  for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+  for (int i = threadIdx.x; i < nvec; i += blockDim.x) stream_store(dst + i, src[i]);
 }
 
 // Flat grid over (page list entry, 16-byte word of the page) for one layer
@@ -46,7 +46,7 @@ zero_pages_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t 
   char* base = (blockIdx.z ? v_pool : k_pool) + ((int64_t)blockIdx.y * num_pages + pid) * page_bytes;
   V z;
   __builtin_memset(&z, 0, sizeof(V));
-  reinterpret_cast<V*>(base)[w] = z;
+  stream_store(reinterpret_cast<V*>(base) + w, z);
 }
 
 template <typename V>
@@ -66,7 +66,7 @@ copy_pages_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t 
   const int64_t layer_off = (int64_t)blockIdx.y * num_pages;
   const V* src = reinterpret_cast<const V*>(pool + (layer_off + s) * page_bytes);
   V* dst = reinterpret_cast<V*>(pool + (layer_off + d) * page_bytes);
-  dst[w] = src[w];
+  stream_store(dst + w, src[w]);
 }
 
 // grid (max_len, batch, 2): row t of sequence b, K or V.
@@ -152,8 +152,8 @@ extern "C" int nslg_append_kv(const void* k_src, const void* v_src, int64_t k_sr
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
   switch (w) {
-    case 16: append_rows_kernel<uint4><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
-    case 8: append_rows_kernel<uint2><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
+    case 16: append_rows_kernel<u32x4><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
+    case 8: append_rows_kernel<u32x2><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
     case 4: append_rows_kernel<uint32_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
     default: append_rows_kernel<uint16_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
   }
@@ -192,8 +192,8 @@ extern "C" int nslg_zero_pages(void* k_pool, void* v_pool, int32_t num_layers, i
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
   switch (w) {
-    case 16: zero_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
-    case 8: zero_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
+    case 16: zero_pages_kernel<u32x4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
+    case 8: zero_pages_kernel<u32x2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
     case 4: zero_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
     default: zero_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, page_ids, n); break;
   }
@@ -219,8 +219,8 @@ extern "C" int nslg_copy_pages(void* k_pool, void* v_pool, int32_t num_layers, i
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
   switch (w) {
-    case 16: copy_pages_kernel<uint4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
-    case 8: copy_pages_kernel<uint2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
+    case 16: copy_pages_kernel<u32x4><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
+    case 8: copy_pages_kernel<u32x2><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
     case 4: copy_pages_kernel<uint32_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
     default: copy_pages_kernel<uint16_t><<<grid, 256, 0, s>>>(kp, vp, num_pages, pb, src_ids, dst_ids, n); break;
   }
@@ -253,8 +253,8 @@ extern "C" int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t nu
   char* ko = (char*)k_out;
   char* vo = (char*)v_out;
   switch (w) {
-    case 16: gather_rows_kernel<uint4><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
-    case 8: gather_rows_kernel<uint2><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
+    case 16: gather_rows_kernel<u32x4><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
+    case 8: gather_rows_kernel<u32x2><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
     case 4: gather_rows_kernel<uint32_t><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
     default: gather_rows_kernel<uint16_t><<<grid, threads, 0, s>>>(kp, vp, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len, max_len, (int)row_bytes, ko, vo); break;
   }

@@ -117,14 +117,19 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeArgs a) {
         o_lo[e] = rope_elem<T>(x1, cl, -x2, sl);  // d < H: rot = -x[d + H]
         o_hi[e] = rope_elem<T>(x2, ch, x1, sh);   // d >= H: rot = x[d - H]
       }
-      *reinterpret_cast<u16x8*>(dst + j) = o_lo;
-      *reinterpret_cast<u16x8*>(dst + H + j) = o_hi;
+      if (head < a.num_qo_heads) {  // q: read again right away by the attention kernel
+        *reinterpret_cast<u16x8*>(dst + j) = o_lo;
+        *reinterpret_cast<u16x8*>(dst + H + j) = o_hi;
+      } else {  // pool rows: streamed out (non-temporal)
+        stream_store(reinterpret_cast<u16x8*>(dst + j), o_lo);
+        stream_store(reinterpret_cast<u16x8*>(dst + H + j), o_hi);
+      }
     } else {
       const int k = i - rot_items;
       const int vh = k / kCopyPerHead;
       const int j = (k % kCopyPerHead) * W;
-      *reinterpret_cast<u16x8*>(a.v_pool + (int64_t)slot * row_elems + (int64_t)vh * D + j) =
-          *reinterpret_cast<const u16x8*>(a.v + t * a.v_stride + (int64_t)vh * D + j);
+      stream_store(reinterpret_cast<u16x8*>(a.v_pool + (int64_t)slot * row_elems + (int64_t)vh * D + j),
+                   *reinterpret_cast<const u16x8*>(a.v + t * a.v_stride + (int64_t)vh * D + j));
     }
   }
 }
@@ -187,18 +192,25 @@ __global__ void __launch_bounds__(256) rope_append_f32_kernel(RopeArgs a) {
         o_lo[e] = rope_elem_f32(lo[e], c_lo[e], -hi[e], s_lo[e]);  // d < H: rot = -x[d + H]
         o_hi[e] = rope_elem_f32(hi[e], c_hi[e], lo[e], s_hi[e]);   // d >= H: rot = x[d - H]
       }
-      *reinterpret_cast<f32x4*>(dst + j) = f32x4{o_lo[0], o_lo[1], o_lo[2], o_lo[3]};
-      *reinterpret_cast<f32x4*>(dst + j + 4) = f32x4{o_lo[4], o_lo[5], o_lo[6], o_lo[7]};
-      *reinterpret_cast<f32x4*>(dst + H + j) = f32x4{o_hi[0], o_hi[1], o_hi[2], o_hi[3]};
-      *reinterpret_cast<f32x4*>(dst + H + j + 4) = f32x4{o_hi[4], o_hi[5], o_hi[6], o_hi[7]};
+      const f32x4 w[4] = {f32x4{o_lo[0], o_lo[1], o_lo[2], o_lo[3]}, f32x4{o_lo[4], o_lo[5], o_lo[6], o_lo[7]},
+                          f32x4{o_hi[0], o_hi[1], o_hi[2], o_hi[3]}, f32x4{o_hi[4], o_hi[5], o_hi[6], o_hi[7]}};
+      f32x4* d4[4] = {reinterpret_cast<f32x4*>(dst + j), reinterpret_cast<f32x4*>(dst + j + 4),
+                      reinterpret_cast<f32x4*>(dst + H + j), reinterpret_cast<f32x4*>(dst + H + j + 4)};
+      if (head < a.num_qo_heads) {  // q: read again right away by the attention kernel
+#pragma unroll
+        for (int e = 0; e < 4; ++e) *d4[e] = w[e];
+      } else {  // pool rows: streamed out (non-temporal)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stream_store(d4[e], w[e]);
+      }
     } else {
       const int kk = i - rot_items;
       const int vh = kk / kCopyPerHead;
       const int j = (kk % kCopyPerHead) * W;
       const float* vs = v + t * a.v_stride + (int64_t)vh * D + j;
       float* vd = v_pool + (int64_t)slot * row_elems + (int64_t)vh * D + j;
-      *reinterpret_cast<f32x4*>(vd) = *reinterpret_cast<const f32x4*>(vs);
-      *reinterpret_cast<f32x4*>(vd + 4) = *reinterpret_cast<const f32x4*>(vs + 4);
+      stream_store(reinterpret_cast<f32x4*>(vd), *reinterpret_cast<const f32x4*>(vs));
+      stream_store(reinterpret_cast<f32x4*>(vd + 4), *reinterpret_cast<const f32x4*>(vs + 4));
     }
   }
 }
