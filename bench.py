@@ -33,10 +33,13 @@ import numpy as np
 HQ, HKV, D, PS = 32, 8, 128, 16
 HBM_PEAK_GBS = 8000.0
 
-# HBM bytes per nslg_paged_decode call (split-K kernel + merge) from the FETCH_SIZE and
-# WRITE_SIZE counters, each scaled by what the counter reads for a plain copy of known
-# size; profiles/paged_decode_hbm_traffic_kv_pressure_b64.md holds the runs.
-MEASURED_TRAFFIC = {"kv_pressure": 2995552370}
+# HBM bytes an nslg_paged_decode call (split-K kernel + merge) moves per algorithmic
+# byte: the FETCH_SIZE and WRITE_SIZE counters of the roofline pass of
+# `bench.py --steps 20 --warmup 5`, each scaled by what the counter reads for a plain
+# copy of known size, over that pass's algorithmic bytes
+# (profiles/paged_decode_hbm_traffic_kv_pressure_b64.md). `traffic` in the JSON line is
+# this ratio times the algorithmic bytes of the run being reported.
+TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0057}
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -86,8 +89,18 @@ class DecodeWorkload:
         self.ids = [f"s{b}" for b in range(self.B)]
         for sid, L in zip(self.ids, lens):
             self._admit(sid, L)
-        # prefill content: every page (allocated ones were zeroed on allocation) ~ N(0,1)
         g = torch.Generator(device="cuda:0").manual_seed(seed)
+        # the K/V of the sequences re-admitted at the churn: N(0,1) rows drawn here, at
+        # set-up, and written into their new pages by the cache's append kernel at the
+        # churn, as the prefill of those sequences would write them (drawing them at
+        # the churn would leave ~300 MB of freshly written temporaries in the caches,
+        # which the next decode then writes back: a harness cost, not the cache's)
+        self.fresh = None
+        if churn_frac > 0:
+            rows = int(churn_frac * sum(math.ceil(L / PS) for L in lens) * PS * 1.5) + 2048 * PS
+            self.fresh = (torch.randn(rows, HKV, D, generator=g, device="cuda:0", dtype=torch.float16),
+                          torch.randn(rows, HKV, D, generator=g, device="cuda:0", dtype=torch.float16))
+        # prefill content: every page (allocated ones were zeroed on allocation) ~ N(0,1)
         pool.k.normal_(generator=g)
         pool.v.normal_(generator=g)
         # per-step inputs: a ring of seeded N(0,1) q/k/v, [B, 1, H, D]
@@ -110,8 +123,11 @@ class DecodeWorkload:
 
     def churn(self):
         """Release whole sequences until >= churn_frac of the used pages are free, then
-        re-admit them at the same lengths on freshly shuffled pages with fresh K/V."""
+        re-admit them at the same lengths on freshly shuffled pages with fresh K/V
+        (every slot of their pages, written with the append kernel from the rows drawn
+        at set-up)."""
         torch = self.torch
+        from nanoslg_amd import kernels
         mgr = self.mgr
         used = sum(mgr.seqs[s].n_pages for s in self.ids)
         order = self.rng.permutation(self.B)
@@ -126,13 +142,19 @@ class DecodeWorkload:
         free = np.array(mgr.pool._free, np.int64)
         self.rng.shuffle(free)
         mgr.pool._free = free.tolist()
+        fk, fv = self.fresh
+        o = 0
         for sid, L in victims:
             self._admit(sid, L)
-            pages = torch.from_numpy(mgr.seqs[sid].bt[:mgr.seqs[sid].n_pages].astype(np.int64)).cuda()
-            mgr.pool.k[0].index_copy_(0, pages, torch.randn(len(pages), PS, HKV, D, device="cuda:0",
-                                                            dtype=torch.float16))
-            mgr.pool.v[0].index_copy_(0, pages, torch.randn(len(pages), PS, HKV, D, device="cuda:0",
-                                                            dtype=torch.float16))
+            st = mgr.seqs[sid]
+            pages = st.bt[:st.n_pages].astype(np.int64)
+            slots = (pages[:, None] * PS + np.arange(PS)).reshape(-1).astype(np.int32)
+            n = slots.size
+            if o + n > fk.shape[0]:
+                o = 0
+            kernels.append_kv(fk[o:o + n], fv[o:o + n], torch.from_numpy(slots).to(fk.device),
+                              mgr.pool.k[0], mgr.pool.v[0])
+            o += n
         return freed
 
     def seq_lens(self):
@@ -319,10 +341,11 @@ def cpu_baseline_sample(lens, seed, budget_s=12.0, max_steps=32):
     # (median of 5 repeats after 8 warmup steps)
     sec, _ = O.timed_contiguous_decode(num_steps=64, prefill=512, Hq=HQ, Hkv=HKV, D=D, seed=seed, warmup=8,
                                        repeats=5, threads=threads)
-    lens1 = [512 + 8 + i + 1 for i in range(64)]
+    lens1 = [512 + i + 1 for i in range(64)]
     b1 = np.mean([2 * HKV * D * 4 * L + 2 * HKV * D * 4 * 2 + 2 * HQ * D * 4 for L in lens1])
     contiguous_b1 = {"ms_per_step": round(sec * 1e3, 4), "tok_s_layer": round(1.0 / sec, 1),
-                     "GB_s": round(float(b1) / sec / 1e9, 3), "context": "521..584 tokens", "repeats": 5}
+                     "GB_s": round(float(b1) / sec / 1e9, 3),
+                     "context": "513..576 tokens (8 warmup steps on a separate cache)", "repeats": 5}
     return {
         "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
@@ -344,7 +367,7 @@ def run_decode(args):
     import torch
     if args.workload == "kv_pressure":
         lens = kv_pressure_lens(args.seed)
-        total_steps = args.warmup + 2 * args.steps  # timed pass + roofline pass
+        total_steps = args.warmup + 3 * args.steps  # timed pass + roofline pass + step-timing pass
         npages = sum(math.ceil(L / PS) for L in lens)
         pool_pages = int(math.ceil(npages / 0.9)) + 1
         # room for the steps' growth inside the 10 % headroom
@@ -429,7 +452,48 @@ def run_decode(args):
     kbytes /= args.steps
     achieved = kbytes / (mean_ms * 1e-3) / 1e9
     _log(f"decode call: mean {mean_ms*1e3:.1f} us over {len(timed.events)} launches, {achieved:.1f} GB/s")
-    traffic = MEASURED_TRAFFIC.get(w.name)
+    ratio = TRAFFIC_PER_ALGORITHMIC_BYTE.get(w.name)
+    traffic = int(round(ratio * kbytes)) if ratio else None
+    if traffic:
+        _log(f"decode call: {int(kbytes)} algorithmic bytes per launch, traffic {traffic} bytes "
+             f"(x{ratio} from the HBM counters)")
+
+    # Step-timing pass: the timed pass's structure again (the same step count, the
+    # churn at mid-run) with one event per step boundary on the compute stream. An
+    # interval is a step's time on the GPU's clock; after the churn's synchronisation
+    # the next interval starts from a fresh event, so it also holds that step's host
+    # planning, which the idle GPU waits for (as step 0's does).
+    stream = torch.cuda.current_stream()
+    mark = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    torch.cuda.synchronize()
+    prev = mark()
+    prev.record(stream)
+    spans = []
+    post_churn = -1
+    for i in range(args.steps):
+        if i == churn_at:
+            torch.cuda.synchronize()
+            w.churn()
+            if args.graph:
+                graph = make_graph(0)
+                step = graph.step
+            torch.cuda.synchronize()
+            prev = mark()
+            prev.record(stream)
+            post_churn = i
+        step()
+        e = mark()
+        e.record(stream)
+        spans.append((prev, e))
+        prev = e
+    torch.cuda.synchronize()
+    step_ms = [a.elapsed_time(b) for a, b in spans]
+    med = float(np.median(step_ms))
+    worst = int(np.argmax(step_ms))
+    _log("step wall ms (step-timing pass): " + ", ".join(f"{x:.3f}" for x in step_ms))
+    _log(f"step wall: median {med:.3f} ms, max {step_ms[worst]:.3f} ms (step {worst}), "
+         f"max/median {step_ms[worst] / med:.2f}"
+         + (f", step after the churn {step_ms[post_churn]:.3f} ms" if post_churn >= 0 else ""))
     res = {
         "metric": "paged decode attn+append: achieved HBM GB/s (% of peak) and decode tok/s/layer",
         "value": round(value, 2),
@@ -457,10 +521,16 @@ def run_decode(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_note": (f"{ratio} x the algorithmic bytes per launch (FETCH_SIZE/WRITE_SIZE of the decode "
+                             "call, calibrated on a plain copy, over its algorithmic bytes)") if ratio else None,
             "avg_launch_us": round(mean_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": int(kbytes),
         },
         "churn_ms": round(churn_s * 1e3, 2),
+        "step_wall_ms": {"median": round(med, 4), "max": round(step_ms[worst], 4), "max_step": worst,
+                         "max_over_median": round(step_ms[worst] / med, 3),
+                         "after_churn": round(step_ms[post_churn], 4) if post_churn >= 0 else None,
+                         "pass": "a third pass of the same structure, one HIP event per step boundary"},
     }
     return res, lens
 

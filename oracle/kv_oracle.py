@@ -781,28 +781,32 @@ class _PagedCtxRef:
 def timed_contiguous_decode(num_steps=64, prefill=512, Hq=32, Hkv=8, D=128, seed=0, warmup=8,
                             repeats=5, threads=None):
     """The config-1 CPU baseline: fp32, B=1, prefill `prefill` tokens of N(0,1) K/V, then
-    `num_steps` decode steps through ContiguousRef. Returns (median seconds per step,
-    threads used)."""
+    `num_steps` decode steps through ContiguousRef, timed at contexts prefill+1 ..
+    prefill+num_steps (the `warmup` steps run first on a separate cache of the same
+    shape). Returns (median seconds per step over `repeats`, threads used)."""
     if threads is not None:
         torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(seed)
-    total = prefill + num_steps + warmup
-    cache = ContiguousRef(1, 1, total, Hkv, D)
+    cache = ContiguousRef(1, 1, prefill + num_steps, Hkv, D)
+    warm = ContiguousRef(1, 1, prefill + warmup, Hkv, D)
     times = []
     for _ in range(repeats):
-        cache.release_sequence("s")
-        cache.allocate_sequence("s")
-        cache.k[0, 0, :prefill] = torch.randn(prefill, Hkv, D, generator=g)
-        cache.v[0, 0, :prefill] = torch.randn(prefill, Hkv, D, generator=g)
-        cache.states["s"]["num_tokens"] = prefill
+        for c in (warm, cache):
+            c.release_sequence("s")
+            c.allocate_sequence("s")
+            c.k[0, 0, :prefill] = torch.randn(prefill, Hkv, D, generator=g)
+            c.v[0, 0, :prefill] = torch.randn(prefill, Hkv, D, generator=g)
+            c.states["s"]["num_tokens"] = prefill
         qs = torch.randn(warmup + num_steps, 1, 1, Hq, D, generator=g) / math.sqrt(D)
         ks = torch.randn(warmup + num_steps, 1, 1, Hkv, D, generator=g)
         vs = torch.randn(warmup + num_steps, 1, 1, Hkv, D, generator=g)
         for i in range(warmup + num_steps):
+            c = warm if i < warmup else cache
             if i == warmup:
                 t0 = time.perf_counter()
-            ctx = cache.begin_forward(["s"], [1])
+            ctx = c.begin_forward(["s"], [1])
             ctx.attend(0, qs[i], ks[i], vs[i], Hq, Hkv)
-            cache.end_forward(ctx)
+            c.end_forward(ctx)
+        assert cache.states["s"]["num_tokens"] == prefill + num_steps
         times.append((time.perf_counter() - t0) / num_steps)
     return float(np.median(times)), torch.get_num_threads()
