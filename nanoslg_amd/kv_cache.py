@@ -1621,6 +1621,11 @@ class _GraphDecodeContext(CacheContext):
 
     def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
         B = q.shape[0]
+        # replays rotate at positions the captured tables must hold (step() checks)
+        g = self._graph
+        g.rope_rows = cos.shape[0] if g.rope_rows is None else min(g.rope_rows, cos.shape[0])
+        if self.seq_lens and max(self.seq_lens) > cos.shape[0]:
+            raise IndexError(f"position {max(self.seq_lens) - 1} is outside the rope tables ({cos.shape[0]} rows)")
         return self._launch(layer_idx, q[:, 0], k_new, v_new, rope=(cos, sin, self._plan_t.pos)).reshape(B, 1, -1)
 
 
@@ -1645,7 +1650,9 @@ class DecodeGraph:
         if not hasattr(kern, "_decode_plan_step_device"):
             raise RuntimeError("DecodeGraph needs the HIP kernels")
         self.cache, self.seq_ids, self.forward = cache, list(seq_ids), forward
+        self.rope_rows = None  # rows of the rope tables the captured forward rotates with
         B, ps, pool, cfg = len(self.seq_ids), cache.cfg.page_size, cache.pool, cache.cfg
+        self._zero_pending()
         if not 1 <= B <= 512:
             raise ValueError("DecodeGraph: 1..512 sequences")
         self.states = [cache.seqs[s] for s in self.seq_ids]
@@ -1710,6 +1717,17 @@ class DecodeGraph:
         self.steps = 0
         cache._dev_plan = None
 
+    def _zero_pending(self) -> None:
+        """Zero, now, the pages whose zero-on-alloc the cache still owes (those that
+        extend_sequence took, kv_cache.py:411, or that a failed forward left): the
+        replayed steps write into them and never run the eager forward that would
+        zero them, and that eager forward, run after graph steps, would zero them
+        again after tokens were written into them."""
+        cache = self.cache
+        if cache._pending_zero:
+            pending, cache._pending_zero = cache._pending_zero, []
+            cache.pool.zero(pending)
+
     def step(self):
         """One decode step of the batch: bookkeeping, then the graph replay."""
         cache, pool, ps = self.cache, self.cache.pool, self.cache.cfg.page_size
@@ -1720,24 +1738,36 @@ class DecodeGraph:
             self.done[i].synchronize()  # the page list of two steps ago has been copied in
         B = len(self.states)
         start = np.fromiter((st.num_tokens for st in self.states), np.int64, B)
+        if self.rope_rows is not None and int(start.max()) >= self.rope_rows:
+            raise IndexError(f"position {int(start.max())} is outside the rope tables ({self.rope_rows} rows)")
+        # checks first: a page the step writes that the sequence already has must not
+        # be shared (a page allocated here never is)
+        npg = start // ps + 1
+        for b, st in enumerate(self.states):
+            if st.n_pages >= npg[b] and pool.ref_count[st.bt[npg[b] - 1]] > 1:
+                raise RuntimeError("DecodeGraph: a shared page would be written; use the eager path")
+        self._zero_pending()
         opens = start % ps == 0
         new_np = self.new_np[i]
         new_np[:] = -1
-        pids = np.empty(B, np.int64)
-        for b in np.flatnonzero(opens).tolist():
-            st = self.states[b]
-            need = int(start[b]) // ps + 1
-            if st.n_pages < need:  # zeroed by the graph's planner, not by a launch of its own
-                k = need - st.n_pages
-                st.extend(cache._alloc(k, defer_zero=True))
-                del cache._pending_zero[-k:]
-            # (a page the sequence already had was zeroed when it was allocated)
-            new_np[b] = st.bt[need - 1]
-        npg = start // ps + 1
-        for b, st in enumerate(self.states):
-            pids[b] = st.bt[npg[b] - 1]
-        if bool((pool.ref_count[pids] > 1).any()):
-            raise RuntimeError("DecodeGraph: a shared page would be written; use the eager path")
+        taken: List[int] = []
+        try:
+            for b in np.flatnonzero(opens).tolist():
+                st = self.states[b]
+                need = int(start[b]) // ps + 1
+                if st.n_pages < need:  # zeroed by the graph's planner, not by a launch of its own
+                    k = need - st.n_pages
+                    pages = cache._alloc(k, defer_zero=True)
+                    del cache._pending_zero[-k:]
+                    taken.extend(pages)
+                    st.extend(pages)
+                # (a page the sequence already had has been zeroed: at its allocation,
+                # or by _zero_pending above when its zeroing was deferred)
+                new_np[b] = st.bt[need - 1]
+        except RuntimeError:
+            cache._pending_zero.extend(taken)  # the next forward zeroes them, as allocation would
+            raise
+        pids = np.fromiter((st.bt[npg[b] - 1] for b, st in enumerate(self.states)), np.int64, B)
         sl = start % ps
         pool.tokens_used[pids] = np.maximum(pool.tokens_used[pids], sl + 1)
         ctx = self.ctxs[i]

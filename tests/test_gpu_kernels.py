@@ -738,3 +738,56 @@ def test_block_table_csr_bit_exact(B, ps, seed):
     for b in range(B):
         want[offs[b]:offs[b] + have[b]] = tables[b]
     assert np.array_equal(d_arena.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("B,ps,where", [(64, 16, "device"), (37, 4, "pinned"), (5, 16, "pinned")])
+def test_decode_plan_step_device_list_bit_exact(B, ps, where):
+    """nslg_decode_plan_step_device (the planner of a step replayed from a HIP graph:
+    the opened-page list read from memory at run time, device or pinned host) equals
+    the CSR the oracle builds from the extended block tables (kv_cache.py:598-615),
+    with the new tokens' slots and positions and the opened pages in batch order;
+    sequences whose last page is full or that have none open the page given, or the
+    null page when given none."""
+    _log(f"decode plan step (list in {where} memory) B={B} ps={ps}")
+    import types
+    from nanoslg_amd import kernels as K
+    rng = np.random.default_rng(300 + B)
+    lens = [int(x) for x in rng.integers(0, 3000, size=B)]
+    for b in range(0, B, 4):
+        lens[b] = ps * (b % 9)  # full last page (or empty): opens one
+    npg = [math.ceil(L / ps) for L in lens]
+    perm = rng.permutation(np.arange(1, sum(npg) + B + 10)).tolist()
+    tables, off = [], 0
+    for n in npg:
+        tables.append(perm[off:off + n])
+        off += n
+    spare = perm[off:]
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    opens = [L % ps == 0 for L in lens]
+    new_page = np.full(B, -1, np.int32)
+    for b in range(B):
+        if opens[b] and b % 7 != 3:  # a few openers get no page: the null page
+            new_page[b] = spare.pop()
+    exp_tables = [t + ([int(new_page[b]) if new_page[b] >= 0 else 0] if opens[b] else []) for b, t in
+                  enumerate(tables)]
+    exp_lens = [L + 1 for L in lens]
+    e_indptr, e_indices, e_lpl = O.plan_csr(exp_tables, exp_lens, ps)
+    e_slot = [exp_tables[b][L // ps] * ps + L % ps for b, L in enumerate(lens)]
+    e_new = [exp_tables[b][-1] for b in range(B) if opens[b]]
+    cap = int(e_indptr[-1]) + 8
+    z = lambda n: torch.full((n,), -9, dtype=torch.int32, device=DEV)  # noqa: E731
+    dst = types.SimpleNamespace(indptr=z(B + 1), indices=z(cap), lpl=z(B), slot=z(B), pos=z(B), new_pages=z(B))
+    if where == "device":
+        new = torch.from_numpy(new_page).to(DEV)
+    else:
+        new = torch.from_numpy(new_page).pin_memory()
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)  # noqa: E731
+    K._decode_plan_step_device(t(indptr), t(indices), t(lpl), new, B, ps, dst, (None, None, 0, 0, 0, 0, 0))
+    torch.cuda.synchronize()
+    n = int(e_indptr[-1])
+    assert np.array_equal(dst.indptr.cpu().numpy(), e_indptr)
+    assert np.array_equal(dst.indices.cpu().numpy()[:n], e_indices[:n])
+    assert np.array_equal(dst.lpl.cpu().numpy(), e_lpl)
+    assert np.array_equal(dst.slot.cpu().numpy(), np.array(e_slot, np.int32))
+    assert np.array_equal(dst.pos.cpu().numpy(), np.array(lens, np.int32))
+    assert np.array_equal(dst.new_pages.cpu().numpy()[:len(e_new)], np.array(e_new, np.int32))

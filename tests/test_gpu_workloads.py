@@ -166,9 +166,11 @@ def test_kv_pressure_full_size():
                 torch.randn(B, 1, HKV, D, generator=g, device=DEV, dtype=torch.float16),
                 torch.randn(B, 1, HKV, D, generator=g, device=DEV, dtype=torch.float16))
 
-    # steps 0-2 checked (host plan, then device-planned steps), 3-19 unchecked, 20 checked
+    # step 0 is planned on the host, the others on the device: steps 0-2 and every
+    # 4th after them checked (a page opens every 16 steps of a sequence, at staggered
+    # steps across the batch, so checked device-planned steps include page openings)
     for step in range(21):
-        _decode_and_check(mgr, ids, *inputs(), check=step < 3 or step == 20)
+        _decode_and_check(mgr, ids, *inputs(), check=step < 3 or step % 4 == 0)
     # churn: release whole sequences until 10 % of the used pages are free, re-admit them
     used = sum(mgr.seqs[s].n_pages for s in ids)
     freed, victims = 0, []
@@ -188,8 +190,11 @@ def test_kv_pressure_full_size():
         mgr.pool.v[0].reshape(-1, HKV, D)[rows] = torch.randn(rows.numel(), HKV, D, generator=g, device=DEV,
                                                               dtype=torch.float16)
     _log(f"churn: {len(victims)} sequences, {freed} pages")
-    for step in range(3):
-        _decode_and_check(mgr, ids, *inputs())
+    # the first step after the churn is planned on the host from the device-resident
+    # block tables (only the re-admitted sequences' tables are uploaded), the rest on
+    # the device
+    for step in range(9):
+        _decode_and_check(mgr, ids, *inputs(), check=step < 3 or step % 4 == 0)
     assert mgr.pool.num_free + sum(mgr.seqs[s].n_pages for s in ids) == pages - 1
 
 
