@@ -540,13 +540,13 @@ RADIX_B, RADIX_PREFIX = 16, 2040
 
 def run_radix(args):
     """Radix prefix sharing + copy-on-write: a 2040-token prompt (127 full pages and a
-    page holding 8 tokens) is prefilled once; 16 requests whose prompts start with it
-    are admitted through the radix tree (the 127 full pages are matched by token ids)
-    and also take a reference on the shared partial page, as a caller that shares
-    partial pages does with add_ref (kv_cache.py:713). Their suffixes (128..1024
-    tokens) are then prefilled in one ragged forward: the first write lands in slot 8
-    of the shared page, so 15 requests copy it and the last writes in place
-    (kv_cache.py:586-591). Then `--steps` decode steps of all 16.
+    page holding 8 tokens) is prefilled once and released, which caches its pages in
+    the radix tree, the partial last page included; 16 requests whose prompts start
+    with it are admitted through the tree (all 2040 tokens matched by token ids: the
+    partial page is shared, refcount 17 with the tree's). Their suffixes (128..1024
+    tokens) are then prefilled in one ragged forward: each request's first write
+    lands in slot 8 of the shared page, so each copies it (kv_cache.py:586-591) and
+    the tree keeps the original. Then `--steps` decode steps of all 16.
     Decode bytes count the 127 shared pages once (distinct pages); the kernel reads
     them once per request, and how many of those reads reach HBM is the caches'
     business, so the per-request total is reported beside it as effective GB/s."""
@@ -576,20 +576,13 @@ def run_radix(args):
     ctx.attend(0, randn(1, PRE, HQ, D), randn(1, PRE, HKV, D), randn(1, PRE, HKV, D), HQ, HKV)
     mgr.end_forward(ctx)
     owner_pages = mgr.seqs["owner"].bt[:full + 1].tolist()
-    mgr.tree.insert(prompt[:full * PS], owner_pages[:full])  # the full pages, as release inserts them
+    mgr.release_sequence("owner")  # caches its 127 full pages and its partial page
     ids = [f"r{b}" for b in range(B)]
     for sid, n in zip(ids, suffix):
         tids = prompt + rng.integers(0, 128256, size=n).tolist()
         plen = mgr.allocate_sequence(sid, token_ids=tids)
-        assert plen == full * PS, plen
-        st = mgr.seqs[sid]
-        own = int(st.bt[full])
-        st.set_page(full, owner_pages[full])  # share the partial page
-        mgr.pool.add_ref(owner_pages[full])
-        mgr.pool.release(own)
-        st.num_tokens = PRE
-    mgr.release_sequence("owner")
-    assert mgr.pool.ref_count[owner_pages[full]] == B
+        assert plen == PRE, plen
+    assert mgr.pool.ref_count[owner_pages[full]] == B + 1
     # warm the ragged prefill path (first use loads the gather/scatter kernels) on a
     # throwaway cache, so the timed forward below measures the work, not the loading
     scratch = PagedKVCache(KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D,
@@ -612,7 +605,7 @@ def run_radix(args):
     torch.cuda.synchronize()
     suffix_ms = (time.perf_counter() - t0) * 1e3
     cow = len(ctx.cow_pairs)
-    assert cow == B - 1 and mgr.seqs[ids[-1]].bt[full] == owner_pages[full]
+    assert cow == B and all(mgr.seqs[s].bt[full] != owner_pages[full] for s in ids)
     # decode
     ring = 8
     qd, kd, vd = randn(ring, B, 1, HQ, D), randn(ring, B, 1, HKV, D), randn(ring, B, 1, HKV, D)

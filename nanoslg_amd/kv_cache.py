@@ -66,6 +66,11 @@ class KVCacheConfig:
     enable_prefix_caching: bool = True
     backend: str = "auto"
     max_pages_cap: int = 65536    # the reference's auto-size cap (kv_cache.py:97)
+    # Radix sharing of partial last pages (the reference shares full pages only,
+    # kv_cache.py:459-486): a released sequence also caches its last partial page,
+    # prompts shorter than a page are matched too, and a prefix ending inside a page
+    # shares that page; the first write into it copies it (copy-on-write).
+    share_partial_pages: bool = True
 
     def __post_init__(self):
         if self.backend in ("auto", "flashinfer"):
@@ -551,10 +556,11 @@ class PagePool:
 
 
 class _RNode:
-    __slots__ = ("children", "page_id", "ref", "last_access", "depth")
+    __slots__ = ("children", "partials", "page_id", "ref", "last_access", "depth")
 
     def __init__(self, depth=0):
-        self.children: Dict[tuple, "_RNode"] = {}
+        self.children: Dict[tuple, "_RNode"] = {}  # full pages: edge = its ps token ids
+        self.partials: Dict[tuple, "_RNode"] = {}  # partial pages (leaves): edge = their 1..ps-1 token ids
         self.page_id = -1
         self.ref = 0
         self.last_access = 0
@@ -562,10 +568,15 @@ class _RNode:
 
 
 class RadixTree:
-    """Prefix tree over full pages of token ids. Node depth is in pages; each edge is the
+    """Prefix tree over pages of token ids. Node depth is in pages; each edge is the
     tuple of page_size token ids of one page; a node may hold the id of a pool page with
-    those tokens' K/V. Only full pages are ever shared (as in the reference, whose match
-    returns whole pages only, kv_cache.py:459-472).
+    those tokens' K/V. As in the reference (kv_cache.py:459-486) full pages are shared;
+    with share_partial a node may also hold partial pages: leaves keyed by the 1 ..
+    ps-1 token ids written into a released sequence's last page, whose page then holds
+    those tokens' K/V. match returns, after its full pages, the longest partial page
+    that continues the prompt; the first write into it (at the slot after its tokens)
+    copies it (copy-on-write, kv_cache.py:575-594: the tree holds a reference, so it
+    is always shared then).
 
     Differences from the reference's per-token trie, on purpose:
       * match returns pages only up to the first page node whose page was evicted
@@ -574,12 +585,16 @@ class RadixTree:
         The walk itself, its access stamps and its invalidation of pages whose
         refcount dropped to zero are the reference's, so eviction order stays the same;
       * access times come from a counter, so ties only arise within one call, as
-        with the reference's monotonic clock (LRU ties keep DFS pre-order)."""
+        with the reference's monotonic clock (LRU ties keep DFS pre-order). A call
+        stamps the nodes of one token path, and on one path the trie's pre-order is
+        depth order, so partial children are visited before full ones (shortest
+        first): pre-order on every path is depth order here too."""
 
-    def __init__(self, ps: int, pool: PagePool):
+    def __init__(self, ps: int, pool: PagePool, share_partial: bool = False):
         self.root = _RNode()
         self.ps = ps
         self.pool = pool
+        self.share_partial = share_partial
         self._lock = threading.Lock()
         self._clock = 0
 
@@ -592,31 +607,82 @@ class RadixTree:
         for i in range(len(tokens) // ps):
             yield tuple(tokens[i * ps:(i + 1) * ps])
 
+    def _partials_on_path(self, node, tokens, at):
+        """(length, node) of the partial children of `node` whose ids are a prefix of
+        tokens[at:], shortest first (the token path passes through them in that
+        order)."""
+        if not node.partials:
+            return []
+        out = []
+        for r in range(1, min(self.ps - 1, len(tokens) - at) + 1):
+            pn = node.partials.get(tuple(tokens[at:at + r]))
+            if pn is not None:
+                out.append((r, pn))
+        return out
+
+    def _walk(self, tokens):
+        """The page-tree nodes on the token path of `tokens`, in depth order: at each
+        full-page node reached (the root first), its partial children on the path,
+        then the next full page's node, while one continues the path. Yields
+        (node, partial_len): partial_len > 0 for a partial page of that many tokens."""
+        node, ps, i = self.root, self.ps, 0
+        while True:
+            for r, pn in self._partials_on_path(node, tokens, i * ps):
+                yield pn, r
+            if len(tokens) - i * ps < ps:
+                return
+            ch = node.children.get(tuple(tokens[i * ps:(i + 1) * ps]))
+            if ch is None:
+                return
+            node = ch
+            i += 1
+            yield node, 0
+
     def match(self, tokens) -> Tuple[int, List[int]]:
         with self._lock:
-            node, pages, now = self.root, [], self._now()
+            pages, now, ps = [], self._now(), self.ps
             contiguous = True
-            for key in self._keys(tokens):
-                ch = node.children.get(key)
-                if ch is None:
-                    break
-                node = ch
+            best, best_len = -1, 0  # the longest partial page after the contiguous full pages
+            full_seen = 0
+            for node, r in self._walk(tokens):
                 node.last_access = now
+                if r:
+                    if node.page_id >= 0 and self.pool.ref_count[node.page_id] <= 0:
+                        node.page_id = -1
+                    if self.share_partial and contiguous and node.page_id >= 0 and full_seen == len(pages):
+                        best, best_len = node.page_id, r
+                    continue
+                full_seen += 1
                 if node.page_id < 0:
                     contiguous = False  # evicted inside the path: no page past here
                     continue
                 if self.pool.ref_count[node.page_id] > 0:
                     if contiguous:
                         pages.append(node.page_id)
+                        best, best_len = -1, 0  # a partial page only extends the full pages before it
                 else:
                     node.page_id = -1
                     break
-            return len(pages) * self.ps, pages
+            plen = len(pages) * ps
+            if best >= 0:
+                pages.append(best)
+                plen += best_len
+            return plen, pages
 
     def insert(self, tokens, page_ids) -> None:
+        """Cache the pages of tokens: page i holds tokens [ps*i, ps*i + ps); with
+        share_partial, a last page of fewer than ps tokens (page_ids holding one more
+        id) becomes a partial page. A node keeps the page it already holds."""
         with self._lock:
-            node, now = self.root, self._now()
-            for i, key in enumerate(self._keys(tokens)):
+            node, now, ps = self.root, self._now(), self.ps
+            nf = len(tokens) // ps
+            for i in range(nf + 1):
+                # the token path passes through the partial pages on it: stamped as well
+                for _, pn in self._partials_on_path(node, tokens, i * ps):
+                    pn.last_access = now
+                if i == nf:
+                    break
+                key = tuple(tokens[i * ps:(i + 1) * ps])
                 ch = node.children.get(key)
                 if ch is None:
                     ch = _RNode(i + 1)
@@ -626,25 +692,28 @@ class RadixTree:
                 if i < len(page_ids) and node.page_id < 0:
                     node.page_id = page_ids[i]
                     self.pool.add_ref(page_ids[i])
+            r = len(tokens) - nf * ps
+            if self.share_partial and r and nf < len(page_ids):
+                key = tuple(tokens[nf * ps:])
+                pn = node.partials.get(key)
+                if pn is None:
+                    pn = _RNode(nf + 1)
+                    node.partials[key] = pn
+                pn.last_access = now
+                if pn.page_id < 0:  # a partial page starts unpinned
+                    pn.page_id = page_ids[nf]
+                    pn.ref = 0
+                    self.pool.add_ref(page_ids[nf])
 
     def add_refs(self, tokens, n: int = 1) -> None:
+        """Pin the nodes on the token path (kv_cache.py:488-495)."""
         with self._lock:
-            node = self.root
-            for key in self._keys(tokens):
-                ch = node.children.get(key)
-                if ch is None:
-                    break
-                node = ch
+            for node, _ in self._walk(tokens):
                 node.ref += n
 
     def dec_refs(self, tokens, n: int = 1) -> None:
         with self._lock:
-            node = self.root
-            for key in self._keys(tokens):
-                ch = node.children.get(key)
-                if ch is None:
-                    break
-                node = ch
+            for node, _ in self._walk(tokens):
                 node.ref = max(0, node.ref - n)
 
     def evict_lru(self, need: int) -> int:
@@ -655,7 +724,7 @@ class RadixTree:
             self._collect(self.root, cands)
             cands.sort(key=lambda x: x[0])
             freed = 0
-            for _, nd, par, edge in cands:
+            for _, nd, par, edge, partial in cands:
                 if freed >= need:
                     break
                 if nd.ref > 0:
@@ -664,18 +733,22 @@ class RadixTree:
                     self.pool.release(nd.page_id)
                     nd.page_id = -1
                     freed += 1
-                if not nd.children and par is not None:
-                    par.children.pop(edge, None)
+                if par is not None and not nd.children and not nd.partials:
+                    (par.partials if partial else par.children).pop(edge, None)
             return freed
 
     def _collect(self, node, out, par=None, edge=None):
-        stack = [(node, par, edge)]
+        """Unpinned page nodes in DFS pre-order: a node, its partial children (shortest
+        first), then its full children in insertion order."""
+        stack = [(node, par, edge, False)]
         while stack:
-            nd, pa, ed = stack.pop()
+            nd, pa, ed, partial = stack.pop()
             if nd.page_id >= 0 and nd.ref == 0:
-                out.append((nd.last_access, nd, pa, ed))
+                out.append((nd.last_access, nd, pa, ed, partial))
             for t, ch in reversed(list(nd.children.items())):
-                stack.append((ch, nd, t))
+                stack.append((ch, nd, t, False))
+            for t, ch in sorted(nd.partials.items(), key=lambda kv: -len(kv[0])):
+                stack.append((ch, nd, t, True))
 
     @property
     def cached_pages(self) -> int:
@@ -685,6 +758,7 @@ class RadixTree:
             if n.page_id >= 0:
                 c += 1
             stack.extend(n.children.values())
+            stack.extend(n.partials.values())
         return c
 
 
@@ -819,6 +893,14 @@ class PagedCacheContext(CacheContext):
         def _cow(st, p):
             pid = int(st.bt[p])
             new = pool.cow_alloc(pid)
+            tree = cache.tree
+            if new is None and tree is not None and tree.share_partial and tree.evict_lru(1) > 0:
+                # with partial pages shared, copies are common: a copy may evict a cached
+                # page, as any allocation does (kv_cache.py:760-768); if that released
+                # the page's other reference, the page is written in place
+                if not pool.is_shared(pid):
+                    return
+                new = pool.cow_alloc(pid)
             if new is None:
                 # The copies made so far stand (the reference copies each page as it
                 # goes, kv_cache.py:429-436, and does not undo them on the error).
@@ -1045,7 +1127,8 @@ class PagedKVCache(KVCacheManager):
         self.cfg = cfg
         self.kernels = kernels or _default_kernels()
         self.pool = PagePool(cfg, self.kernels)
-        self.tree = RadixTree(cfg.page_size, self.pool) if cfg.enable_prefix_caching else None
+        self.tree = (RadixTree(cfg.page_size, self.pool, share_partial=cfg.share_partial_pages)
+                     if cfg.enable_prefix_caching else None)
         self.seqs: Dict[str, _PagedSeqState] = {}
         self.workspace = self.kernels.Workspace(self.pool.device, 128 << 20)
         self._pending_zero: List[int] = []
@@ -1259,21 +1342,24 @@ class PagedKVCache(KVCacheManager):
                                         plan.total_pages + n_new, groups=plan.groups)
 
     def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
-        """kv_cache.py:707-722: radix match (full pages), pin, allocate the rest."""
+        """kv_cache.py:707-722: radix match, pin, allocate the rest. The matched prefix
+        is whole pages, or (share_partial_pages) whole pages and a partial page, which
+        the sequence's first write then copies."""
         self._dev_plan = None
         tids = list(token_ids or [])
         total = len(tids) if tids else num_tokens
         plen, ppages = 0, []
-        if self.tree and len(tids) >= self.cfg.page_size:
+        ps = self.cfg.page_size
+        if self.tree and len(tids) >= (1 if self.tree.share_partial else ps):
             plen, ppages = self.tree.match(tids)
             for p in ppages:
                 self.pool.add_ref(p)
             if ppages:
                 self.tree.add_refs(tids[:plen])
         st = _PagedSeqState(seq_id, ppages, plen, tids)
-        new = total - plen
-        if new > 0:
-            st.extend(self._alloc(math.ceil(new / self.cfg.page_size)))
+        need = -(-total // ps) - len(ppages)  # = ceil((total - plen) / ps) when plen is whole pages
+        if need > 0:
+            st.extend(self._alloc(need))
         old = self.seqs.get(seq_id)
         if old is not None:  # a re-used id: its old table's device row is free again
             self._tables.release(old)
@@ -1331,9 +1417,14 @@ class PagedKVCache(KVCacheManager):
             return
         ps = self.cfg.page_size
         if self.tree and st.token_ids:
-            nf = min(st.num_tokens // ps, st.n_pages)
-            if nf:
-                self.tree.insert(st.token_ids[:nf * ps], st.block_table[:nf])
+            if self.tree.share_partial:  # the full pages and the last, partial one
+                n = min(st.num_tokens, len(st.token_ids), st.n_pages * ps)
+                if n:
+                    self.tree.insert(st.token_ids[:n], st.block_table[:-(-n // ps)])
+            else:
+                nf = min(st.num_tokens // ps, st.n_pages)
+                if nf:
+                    self.tree.insert(st.token_ids[:nf * ps], st.block_table[:nf])
             if st.prefix_len:
                 self.tree.dec_refs(st.token_ids[:st.prefix_len])
         for p in st.bt[:st.n_pages].tolist():
@@ -1558,6 +1649,7 @@ def create_cache_manager(hf_config, parallel_config, device, dtype, model_config
         memory_fraction=getattr(model_config, "kv_memory_fraction", 0.30),
         dtype=dtype,
         enable_prefix_caching=getattr(model_config, "enable_prefix_caching", True),
+        share_partial_pages=getattr(model_config, "share_partial_pages", True),
         backend=backend,
     )
     if kv_cfg.backend == "paged":

@@ -505,14 +505,22 @@ class RadixTreeRef:
     stop_at_gap=True restates the build's decision instead: match returns pages only up to the
     first evicted page (a gap-free prefix); the walk, its access stamps and its invalidations are
     unchanged. The golden vectors pin the default; tests that compare the product's cache over
-    whole serving runs use this mode."""
+    whole serving runs use this mode.
 
-    def __init__(self, ps, pool, stop_at_gap=False):
+    share_partial=True adds the build's partial-page sharing (not in the reference, whose tree
+    holds pages at depths that are multiples of the page size only, :478-486): insert also hangs
+    a last page of r < ps tokens on the node at its depth (nf*ps + r), and match returns, after
+    its full pages, the page of the deepest such node on the walk that lies right after them
+    (no gap before it), for a prefix of nf*ps + r tokens. Such a node with a released page is
+    invalidated as the walk passes it, without ending the walk."""
+
+    def __init__(self, ps, pool, stop_at_gap=False, share_partial=False):
         self.root = _RNodeRef()
         self.ps = ps
         self.pool = pool
         self._clock = 0
         self.stop_at_gap = stop_at_gap
+        self.share_partial = share_partial
 
     def _now(self):
         self._clock += 1
@@ -521,6 +529,7 @@ class RadixTreeRef:
     def match(self, tokens):
         node, pages, now = self.root, [], self._now()
         gap = False
+        partial = None  # (page, tokens) of a partial page right after the pages so far
         for i, tok in enumerate(tokens):
             ch = node.children.get(tok)
             if ch is None:
@@ -534,9 +543,17 @@ class RadixTreeRef:
                 if self.pool.ref_count[node.page_id] > 0:
                     if not (self.stop_at_gap and gap):
                         pages.append(node.page_id)
+                        partial = None
                 else:
                     node.page_id = -1
                     break
+            elif d % self.ps and self.share_partial and node.page_id >= 0:
+                if self.pool.ref_count[node.page_id] <= 0:
+                    node.page_id = -1
+                elif not gap and d // self.ps == len(pages):
+                    partial = (node.page_id, d - len(pages) * self.ps)
+        if partial is not None:
+            return len(pages) * self.ps + partial[1], pages + [partial[0]]
         return len(pages) * self.ps, pages
 
     def insert(self, tokens, page_ids):
@@ -553,6 +570,13 @@ class RadixTreeRef:
                 if node.page_id < 0:
                     node.page_id = incoming
                     self.pool.add_ref(incoming)
+        nf = len(tokens) // self.ps
+        if self.share_partial and len(tokens) % self.ps and nf < len(page_ids) and node.page_id < 0:
+            # the last, partial page (node is at depth len(tokens)); it starts unpinned:
+            # pins that passed this token position before it held a page do not count
+            node.page_id = page_ids[nf]
+            node.ref = 0
+            self.pool.add_ref(page_ids[nf])
 
     def add_refs(self, tokens, n=1):
         node = self.root
@@ -624,10 +648,15 @@ class PagedRef:
     FlashInfer replaced by fp32 SDPA over the gathered pages."""
 
     def __init__(self, num_layers, max_pages, page_size, num_kv_heads, head_dim,
-                 dtype=torch.float32, enable_prefix_caching=True, stop_at_gap=False):
+                 dtype=torch.float32, enable_prefix_caching=True, stop_at_gap=False, share_partial_pages=False):
+        """share_partial_pages: the build's partial-page sharing (RadixTreeRef): released
+        sequences also cache their last partial page, prompts of any length are matched,
+        and a prefix ending inside a page shares that page (its first write copies it)."""
         self.ps = page_size
         self.pool = PagePoolRef(num_layers, max_pages, page_size, num_kv_heads, head_dim, dtype)
-        self.tree = RadixTreeRef(page_size, self.pool, stop_at_gap) if enable_prefix_caching else None
+        self.tree = (RadixTreeRef(page_size, self.pool, stop_at_gap, share_partial_pages)
+                     if enable_prefix_caching else None)
+        self.share_partial_pages = share_partial_pages
         self.seqs: Dict[str, _SeqRef] = {}
         self.max_pages = max_pages
 
@@ -646,16 +675,16 @@ class PagedRef:
         tids = token_ids or []
         total = len(tids) if tids else num_tokens
         plen, ppages = 0, []
-        if self.tree and len(tids) >= self.ps:
+        if self.tree and len(tids) >= (1 if self.share_partial_pages else self.ps):
             plen, ppages = self.tree.match(tids)
             for p in ppages:
                 self.pool.add_ref(p)
             if ppages:
                 self.tree.add_refs(tids[:plen])
         st = _SeqRef(seq_id, list(ppages), plen, plen, list(tids))
-        new = total - plen
-        if new > 0:
-            st.block_table.extend(self._alloc(math.ceil(new / self.ps)))
+        need = math.ceil(total / self.ps) - len(ppages)  # = ceil((total - plen) / ps) for whole pages
+        if need > 0:
+            st.block_table.extend(self._alloc(need))
         self.seqs[seq_id] = st
         return plen
 
@@ -679,9 +708,14 @@ class PagedRef:
             return
         st = self.seqs[seq_id]
         if self.tree and st.token_ids:
-            nf = st.num_tokens // self.ps
-            if nf:
-                self.tree.insert(st.token_ids[:nf * self.ps], st.block_table[:nf])
+            if self.share_partial_pages:  # the full pages and the last, partial one
+                n = min(st.num_tokens, len(st.token_ids))
+                if n:
+                    self.tree.insert(st.token_ids[:n], st.block_table[:math.ceil(n / self.ps)])
+            else:
+                nf = st.num_tokens // self.ps
+                if nf:
+                    self.tree.insert(st.token_ids[:nf * self.ps], st.block_table[:nf])
             if st.prefix_len:
                 self.tree.dec_refs(st.token_ids[:st.prefix_len])
         for p in st.block_table:
@@ -729,12 +763,18 @@ class _PagedCtxRef:
                 pid = st.block_table[pi]
                 if pool.is_shared(pid):
                     np_ = pool.cow(pid)
+                    if np_ is None and cache.share_partial_pages and cache.tree and cache.tree.evict_lru(1) > 0:
+                        # the build's extended mode: a copy may evict a cached page, like any
+                        # allocation (kv_cache.py:760-768); if that released the page's other
+                        # reference, the page is written in place
+                        np_ = pool.cow(pid) if pool.is_shared(pid) else -1
                     if np_ is None:
                         raise RuntimeError("KV OOM during CoW")
-                    self.cow_events.append((pid, np_))
-                    st.block_table[pi] = np_
-                    pool.release(pid)
-                    pid = np_
+                    if np_ >= 0:
+                        self.cow_events.append((pid, np_))
+                        st.block_table[pi] = np_
+                        pool.release(pid)
+                        pid = np_
                 info.append((pid, sl))
                 pool.tokens_used[pid] = max(pool.tokens_used[pid], sl + 1)
             self._write_info.append(info)

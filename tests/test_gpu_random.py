@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 GPU = dict(device="cuda:0", dtype=torch.float16, HQ=8, HKV=2, D=64, atol=2e-3, rtol=1e-2)
 
 
-@pytest.mark.parametrize("seed,ps,pages", [(s, [1, 2, 3, 4, 8, 16][s % 6], [12, 20, 24, 30, 40, 64][(s // 6) % 6])
+@pytest.mark.parametrize("seed,ps,pages", [(s, [1, 2, 3, 4, 8, 16][s % 6], [16, 20, 24, 30, 40, 64][(s // 6) % 6])
                                            for s in range(1, 21)])
 def test_random_serving_traffic_on_gpu(seed, ps, pages):
     import test_host_random as R

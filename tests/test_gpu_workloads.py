@@ -15,10 +15,10 @@ pages are compared bit for bit.
   KV pressure   64 sequences, contexts log-uniform [2048, 32768], pool at 90 %
                 occupancy with pages shuffled across sequences, 10 % of the pages
                 released and re-admitted mid-run
-  radix + CoW   16 requests sharing a 2040-token prompt (127 full pages matched
-                through the radix tree, the partial page shared by reference),
-                suffixes U[128, 1024] prefilled in one ragged forward (15 copies),
-                then decode
+  radix + CoW   16 requests on a released 2040-token prompt (its 127 full pages and
+                its 8-token partial page matched through the radix tree),
+                suffixes U[128, 1024] prefilled in one ragged forward (16 copies of
+                the partial page), then 128 decode steps
   chunked prefill  8 prompts of 4096 tokens in 512-token chunks
   contiguous fp32  the reference's own CPU case on the GPU: one sequence, a
                 512-token prompt, then 64 decode steps, fp32, against the oracle's
@@ -199,15 +199,18 @@ def test_kv_pressure_full_size():
 
 
 def test_radix_cow_full_size():
-    """16 requests on one cached 2040-token prompt: radix match of its 127 full pages,
-    shared partial page (refcount 16), ragged suffix prefill with 15 copy-on-writes,
-    then decode; outputs against SDPA, the shared pages untouched, the copies exact."""
-    _log("workload: radix prefix + copy-on-write (16 x 2040-token prefix)")
+    """16 requests on one cached 2040-token prompt, through the cache API alone: the
+    prompt's release caches its 127 full pages and its partial last page (8 tokens);
+    each request's allocation matches all 2040 tokens (refcount of the partial page:
+    the tree + 16); the ragged suffix prefill copies that page for every request
+    (16 copy-on-writes; the tree keeps the original), then 128 decode steps; outputs
+    against SDPA, the cached pages untouched, the copies exact."""
+    _log("workload: radix prefix + copy-on-write (16 x 2040-token prefix, 128 decode steps)")
     B, PRE = 16, 2040
     full = PRE // PS
     rng = np.random.default_rng(4)
     suffix = [int(x) for x in rng.integers(128, 1025, size=B)]
-    steps = 24
+    steps = 128
     pages = full + 1 + sum(math.ceil((PRE % PS + s + steps) / PS) + 1 for s in suffix) + 64
     mgr = _cache(pages, prefix=True)
     g = torch.Generator(device=DEV).manual_seed(4)
@@ -221,20 +224,16 @@ def test_radix_cow_full_size():
     torch.testing.assert_close(out[0].view(PRE, HQ, D).float(), _reference(mgr, "owner", qp[0]),
                                atol=ATOL, rtol=RTOL)
     owner_pages = mgr.seqs["owner"].bt[:full + 1].tolist()
-    mgr.tree.insert(prompt[:full * PS], owner_pages[:full])
+    mgr.release_sequence("owner")
+    assert mgr.tree.cached_pages == full + 1
+    assert mgr.pool.tokens_used[owner_pages[full]] == PRE % PS
     ids = [f"r{b}" for b in range(B)]
     for sid, n in zip(ids, suffix):
         plen = mgr.allocate_sequence(sid, token_ids=prompt + rng.integers(0, 128256, size=n).tolist())
-        assert plen == full * PS
+        assert plen == PRE
         st = mgr.seqs[sid]
-        assert st.bt[:full].tolist() == owner_pages[:full]
-        own = int(st.bt[full])
-        st.set_page(full, owner_pages[full])
-        mgr.pool.add_ref(owner_pages[full])
-        mgr.pool.release(own)
-        st.num_tokens = PRE
-    mgr.release_sequence("owner")
-    assert mgr.pool.ref_count[owner_pages[full]] == B
+        assert st.bt[:full + 1].tolist() == owner_pages and st.num_tokens == PRE
+    assert mgr.pool.ref_count[owner_pages[full]] == B + 1
     shared_rows = _rows(mgr, ids[0], PRE)
     shared_k = mgr.pool.k[0].reshape(-1, HKV, D)[shared_rows].clone()
     S = max(suffix)
@@ -242,8 +241,9 @@ def test_radix_cow_full_size():
     ctx = mgr.begin_forward(ids, suffix)
     out = ctx.attend(0, q, k, v, HQ, HKV)
     mgr.end_forward(ctx)
-    assert len(ctx.cow_pairs) == B - 1
-    assert mgr.seqs[ids[-1]].bt[full] == owner_pages[full]  # the last sharer writes in place
+    assert sorted(s for s, _ in ctx.cow_pairs) == [owner_pages[full]] * B
+    assert all(mgr.seqs[s].bt[full] != owner_pages[full] for s in ids)
+    assert mgr.pool.ref_count[owner_pages[full]] == 1  # the tree's, for the next request
     for b, sid in enumerate(ids):
         n = suffix[b]
         _check_rows_written(mgr, sid, PRE, k[b, :n], v[b, :n])
@@ -254,10 +254,11 @@ def test_radix_cow_full_size():
                                    atol=ATOL, rtol=RTOL, msg=lambda m, sid=sid: f"{sid}: {m}")
     for step in range(steps):
         _decode_and_check(mgr, ids, randn(B, 1, HQ, D), randn(B, 1, HKV, D), randn(B, 1, HKV, D),
-                          check=step in (0, 1, 7, 8, steps - 1))
-    # the 127 full prefix pages were never written
-    assert torch.equal(mgr.pool.k[0].reshape(-1, HKV, D)[shared_rows[:full * PS]].view(torch.int16),
-                       shared_k[:full * PS].view(torch.int16))
+                          check=step < 2 or step % 8 == 7 or step == steps - 1)
+    # the cached prompt pages, the partial one included, were never written
+    cached = torch.from_numpy(np.asarray(owner_pages, np.int64)).to(DEV)
+    rows = (cached[:, None] * PS + torch.arange(PS, device=DEV)[None, :]).reshape(-1)[:PRE]
+    assert torch.equal(mgr.pool.k[0].reshape(-1, HKV, D)[rows].view(torch.int16), shared_k.view(torch.int16))
 
 
 def test_chunked_prefill_full_size():

@@ -18,12 +18,12 @@ from oracle import kv_oracle as O
 L, HQ, HKV, D = 2, 4, 2, 8
 
 
-def make(ps=4, pages=64, prefix=True, dtype=torch.float32):
+def make(ps=4, pages=64, prefix=True, dtype=torch.float32, partial=True):
     cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
                            max_pages=pages, dtype=dtype, device=None, enable_prefix_caching=prefix,
-                           backend="paged")
+                           backend="paged", share_partial_pages=partial)
     mgr = KC.PagedKVCache(cfg, kernels=FK)
-    ref = O.PagedRef(L, pages, ps, HKV, D, dtype, enable_prefix_caching=prefix)
+    ref = O.PagedRef(L, pages, ps, HKV, D, dtype, enable_prefix_caching=prefix, share_partial_pages=partial)
     return mgr, ref
 
 
@@ -241,9 +241,12 @@ def test_kv_oom_message_and_eviction():
     assert mgr.tree.cached_pages == ref.tree.cached_pages
 
 
-def test_radix_prefix_sharing_matches_oracle():
+@pytest.mark.parametrize("partial", [False, True])
+def test_radix_prefix_sharing_matches_oracle(partial):
+    """Full pages shared through the tree (kv_cache.py:459-486); with partial-page
+    sharing the released sequence's last page (one token) is cached too."""
     g = torch.Generator().manual_seed(3)
-    mgr, ref = make(ps=4, pages=64, prefix=True)
+    mgr, ref = make(ps=4, pages=64, prefix=True, partial=partial)
     prompt = [7, 1, 3, 3, 9, 9, 2, 5, 4, 4, 6, 8, 1, 2]  # 3 full pages + 2 tokens
     for impl in (mgr, ref):
         assert impl.allocate_sequence("p", token_ids=prompt) == 0
@@ -254,7 +257,7 @@ def test_radix_prefix_sharing_matches_oracle():
             impl.append_token_ids("p", [11])
     mgr.release_sequence("p")
     ref.release_sequence("p")
-    assert mgr.tree.cached_pages == ref.tree.cached_pages == 4
+    assert mgr.tree.cached_pages == ref.tree.cached_pages == 4 + int(partial)  # 17 tokens: 4 full pages + 1
     # a new request sharing the first 2 pages, then diverging
     q = prompt[:8] + [0, 0, 0, 0, 0]
     p1 = mgr.allocate_sequence("q", token_ids=q)
@@ -382,7 +385,8 @@ def test_stats_and_reset():
     assert st["backend"] == "paged" and st["active_seqs"] == 1 and st["pages_used"] == 3
     mgr.seqs["a"].num_tokens = 9
     mgr.reset()
-    assert mgr.stats["active_seqs"] == 0 and mgr.stats["radix"] == 2 and mgr.pool.num_free == 13
+    # the tree keeps the 2 full pages and the partial third one (1 token)
+    assert mgr.stats["active_seqs"] == 0 and mgr.stats["radix"] == 3 and mgr.pool.num_free == 12
 
 
 @pytest.mark.parametrize("scalar_batch", [16, 0])
@@ -541,3 +545,108 @@ def test_forward_plan_expanded_on_the_device_matches(scenario, monkeypatch):
      "attend_rope": lambda: test_attend_rope_equals_attend_on_rotated_inputs("paged")}[scenario]()
     if scenario in ("prefill_then_decode", "radix_random", "attend_rope"):  # these have multi-token forwards
         assert any(name == "forward_plan" for name, _ in FK.CALLS)
+
+
+def _partial_sharing_scenario(impl, g):
+    """The known-answer case of partial-page sharing (page size 4), on one cache:
+    returns the values the test checks. A 10-token prompt (2 full pages + 2 tokens)
+    is prefilled and released: the tree caches its 3 pages, the last one partial.
+    Then B (the prompt + 2 tokens) matches all 10 tokens and shares the partial page;
+    C and E diverge inside it and match the 2 full pages only; D (the prompt itself)
+    matches it whole. B's first write lands in slot 2 of the shared page, which the
+    tree, B and D hold: B copies it."""
+    ps = 4
+    prompt = list(range(1, 11))
+    out = {}
+    impl.allocate_sequence("A", token_ids=prompt)
+    q = torch.randn(1, 10, HQ, D, generator=g)
+    k = torch.randn(1, 10, HKV, D, generator=g)
+    v = torch.randn(1, 10, HKV, D, generator=g)
+    c = impl.begin_forward(["A"], [10])
+    for layer in range(L):
+        c.attend(layer, q, k, v, HQ, HKV)
+    impl.end_forward(c)
+    a_pages = list(impl.seqs["A"].block_table)
+    impl.release_sequence("A")
+    out["cached"] = impl.tree.cached_pages
+    out["free_after_release"] = impl.pool.num_free
+    out["plen"] = {s: impl.allocate_sequence(s, token_ids=t) for s, t in
+                   (("B", prompt + [11, 12]), ("C", prompt[:9] + [99]), ("D", prompt), ("E", prompt[:9]))}
+    out["B_shares_A_pages"] = list(impl.seqs["B"].block_table) == a_pages
+    out["ref_partial"] = int(impl.pool.ref_count[a_pages[2]])
+    c = impl.begin_forward(["B"], [2])
+    kb = torch.randn(1, 2, HKV, D, generator=g)
+    for layer in range(L):
+        c.attend(layer, torch.randn(1, 2, HQ, D, generator=g), kb, kb, HQ, HKV)
+    impl.end_forward(c)
+    cow = c.cow_pairs if hasattr(c, "cow_pairs") else c.cow_events
+    out["cow"] = [(int(s), int(d)) for s, d in cow]
+    b3 = impl.seqs["B"].block_table[2]
+    out["B_page3_is_copy"] = b3 != a_pages[2] and out["cow"] == [(a_pages[2], b3)]
+    out["tokens_used"] = (int(impl.pool.tokens_used[a_pages[2]]), int(impl.pool.tokens_used[b3]))
+    out["ref_after"] = int(impl.pool.ref_count[a_pages[2]])
+    # B's K at positions 8, 9 are A's (copied), 10, 11 the new ones
+    kk = impl.pool.k
+    out["B_k"] = torch.stack([kk[0, b3, s] for s in range(4)]).float()
+    out["A_k89"] = k[0, 8:10].float()
+    out["new_k"] = kb[0].float()
+    out["shared_untouched"] = torch.equal(kk[0, a_pages[2], :2].float(), k[0, 8:10].float())
+    return out
+
+
+def test_partial_page_sharing_known_answer():
+    """Partial-page radix sharing, the same known answers from the oracle and the product
+    (each checked on its own): cached pages, prefix lengths, refcounts, the single
+    copy-on-write and the copied page's contents and tokens_used."""
+    for impl in make(ps=4, pages=32, prefix=True, partial=True):
+        out = _partial_sharing_scenario(impl, torch.Generator().manual_seed(12))
+        assert out["cached"] == 3 and out["free_after_release"] == 31 - 3
+        assert out["plen"] == {"B": 10, "C": 8, "D": 10, "E": 8}
+        assert out["B_shares_A_pages"]
+        assert out["ref_partial"] == 3  # the tree, B and D
+        assert out["B_page3_is_copy"]
+        assert out["tokens_used"] == (2, 4)  # the source keeps its 2 tokens; the copy has 4
+        assert out["ref_after"] == 2  # the tree and D
+        assert torch.equal(out["B_k"][:2], out["A_k89"]) and torch.equal(out["B_k"][2:], out["new_k"])
+        assert out["shared_untouched"]
+    # with the reference's rule (full pages only) the same prompts match whole pages only
+    for impl in make(ps=4, pages=32, prefix=True, partial=False):
+        out = _partial_sharing_scenario(impl, torch.Generator().manual_seed(12))
+        assert out["cached"] == 2 and out["plen"] == {"B": 8, "C": 8, "D": 8, "E": 8}
+        assert out["cow"] == []
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_partial_page_match_brute_force(seed):
+    """match on released sequences (no eviction) against a tree-free rule: the full
+    pages are the longest common prefix with a cached sequence, in whole pages of it;
+    a partial page is the last page of a cached sequence whose tokens the prompt
+    continues exactly and that ends inside the page after those full pages."""
+    rnd = random.Random(seed)
+    ps = rnd.choice([2, 3, 4])
+    cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=1, num_qo_heads=1, head_dim=8, page_size=ps,
+                           max_pages=400, dtype=torch.float32, device=None, enable_prefix_caching=True,
+                           backend="paged", share_partial_pages=True)
+    for impl in (KC.PagedKVCache(cfg, kernels=FK), O.PagedRef(1, 400, ps, 1, 8, share_partial_pages=True)):
+        cached = []
+        for i in range(12):
+            toks = [rnd.randint(0, 1) for _ in range(rnd.randint(1, 4 * ps))]
+            impl.allocate_sequence(f"s{i}", token_ids=toks)
+            impl.seqs[f"s{i}"].num_tokens = len(toks)
+            impl.release_sequence(f"s{i}")
+            cached.append(toks)
+        rnd2 = random.Random(seed + 100)
+        for j in range(30):
+            prompt = [rnd2.randint(0, 1) for _ in range(rnd2.randint(1, 5 * ps))]
+
+            def lcp(a, b):
+                n = 0
+                while n < min(len(a), len(b)) and a[n] == b[n]:
+                    n += 1
+                return n
+            f = max(min(lcp(prompt, s), len(s)) // ps for s in cached)
+            r = max([len(s) - f * ps for s in cached
+                     if len(s) % ps and len(s) // ps == f and lcp(prompt, s) >= len(s)] or [0])
+            plen, pages = impl.tree.match(prompt)
+            assert plen == f * ps + r, (impl, prompt)
+            assert len(pages) == f + (1 if r else 0)

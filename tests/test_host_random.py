@@ -30,9 +30,10 @@ CPU = dict(device=None, dtype=torch.float32, HQ=4, HKV=2, D=8, atol=1e-5, rtol=1
 
 
 def _make(ps, pages, env):
+    partial = env.get("partial", True)
     cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=env["HKV"], num_qo_heads=env["HQ"], head_dim=env["D"],
                            page_size=ps, max_pages=pages, dtype=env["dtype"], device=env["device"],
-                           enable_prefix_caching=True, backend="paged")
+                           enable_prefix_caching=True, backend="paged", share_partial_pages=partial)
     kernels = FK if env["device"] is None else None
     mgr = KC.PagedKVCache(cfg, kernels=kernels)
     if env.get("arena"):  # a small device block-table arena: it grows and rows move often
@@ -40,7 +41,7 @@ def _make(ps, pages, env):
     # the oracle's match stops at an evicted page, as the product's does (the
     # reference's match returns the pages past it, a block table with a gap)
     return (mgr, O.PagedRef(L, pages, ps, env["HKV"], env["D"], torch.float32, enable_prefix_caching=True,
-                            stop_at_gap=True))
+                            stop_at_gap=True, share_partial_pages=partial))
 
 
 def _logical(cache, sid, layer, ps):
@@ -106,9 +107,27 @@ def check_device_tables(mgr):
     assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
 
 
+def tree_pages(tree):
+    """The cached pages of a radix tree as (token path, pins, last access): the
+    product's page tree and the oracle's per-token trie must hold the same set (page
+    ids aside: allocation order is not part of the contract)."""
+    out = set()
+    stack = [(tree.root, ())]
+    while stack:
+        nd, path = stack.pop()
+        if nd.page_id >= 0:
+            out.add((path, nd.ref, int(nd.last_access)))
+        for k, ch in nd.children.items():
+            stack.append((ch, path + (tuple(k) if isinstance(k, tuple) else (k,))))
+        for k, ch in getattr(nd, "partials", {}).items():
+            stack.append((ch, path + tuple(k)))
+    return out
+
+
 def _check(mgr, ref, live, ps):
     assert mgr.pool.num_free == ref.pool.num_free
     assert mgr.tree.cached_pages == ref.tree.cached_pages
+    assert tree_pages(mgr.tree) == tree_pages(ref.tree)
     check_device_tables(mgr)
     for sid in live:
         assert mgr.seqs[sid].num_tokens == ref.seqs[sid].num_tokens
@@ -125,6 +144,13 @@ def _check(mgr, ref, live, ps):
                                            (6, 4, 20), (7, 2, 24), (8, 8, 40), (9, 3, 30), (10, 16, 12)])
 def test_random_serving_traffic_matches_oracle(seed, ps, pages):
     run_traffic(seed, ps, pages, CPU)
+
+
+@pytest.mark.parametrize("seed,ps,pages", [(1, 4, 48), (3, 4, 24), (5, 1, 60), (8, 8, 40)])
+def test_random_serving_traffic_full_pages_only(seed, ps, pages):
+    """The same traffic with partial-page sharing off: the reference's rule (only full
+    pages are cached and matched, kv_cache.py:459-486)."""
+    run_traffic(seed, ps, pages, dict(CPU, partial=False))
 
 
 @pytest.mark.parametrize("seed,ps,pages", [(11, 1, 90), (12, 2, 60), (13, 1, 40)])
@@ -149,6 +175,12 @@ def run_traffic(seed, ps, pages, env):
         if r < 0.25 and len(pending) + len(running) < 6:
             sid = f"s{it}"
             toks = [rnd.randint(0, 2) for _ in range(rnd.randint(1, 3 * ps + 4))]
+            if tokens and rnd.random() < 0.35:
+                # a prompt that continues an earlier sequence's tokens (a released one's are
+                # cached, with its last partial page when partial pages are shared)
+                base = tokens[rnd.choice(sorted(tokens))]
+                cut = len(base) if rnd.random() < 0.5 else rnd.randint(1, len(base))
+                toks = base[:cut] + toks[:rnd.randint(0, ps)]
             try:
                 p1 = mgr.allocate_sequence(sid, token_ids=toks)
             except RuntimeError:
