@@ -35,6 +35,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 namespace nslg {
 namespace {
@@ -66,6 +67,7 @@ struct DecodeParams {
   float* part_o;   // [max_chunks, slot_members, Hq, D]
   float* part_ml;  // [max_chunks, slot_members, Hq, 2]
   int32_t slot_members;  // partial slots per (chunk, query head): 1, or the members of a group
+  int32_t stream;        // 1: the call's K/V exceed the caches: stream them (non-temporal loads)
 };
 
 // Prefix groups of a grouped decode call: sequences whose first pages are the same
@@ -246,13 +248,20 @@ __device__ inline const uint16_t* token_row(const uint16_t* pool, const int32_t*
   return pool + ((int64_t)pid * page_size + (tok % page_size)) * row_elems + head_off;
 }
 
-// K/V rows are streamed: each byte is read once per decode call, so the loads carry
-// the non-temporal hint (`nt`), which keeps them from displacing other lines in the
-// caches. Measured on the KV-pressure page pattern (pure loads, 3 GB): 6.15 TB/s
-// plain, 6.95 TB/s non-temporal.
-template <typename V>
-__device__ inline V stream_load(const char* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+// K/V rows are read once per decode call. When a call's K/V are larger than the
+// memory-side cache can hold (kStreamBytes), the loads carry the non-temporal hint
+// (`nt`) and stream from HBM: measured on the KV-pressure page pattern (pure loads,
+// 3 GB) 6.15 TB/s plain, 6.95 TB/s non-temporal; the batch-64 decode call 494 ->
+// 456 us. A smaller call's K/V stay in the caches from one decode step to the next,
+// which only ordinary loads keep using (4 sequences of 1-4k tokens: 13.7 us plain,
+// 15.9 us streamed). A group's shared prefix, which every group sharing it reads, is
+// always loaded normally so the later reads can hit in the caches.
+template <typename V, bool kStream>
+__device__ inline V kv_load(const char* p) {
+  if constexpr (kStream)
+    return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+  else
+    return *reinterpret_cast<const V*>(p);
 }
 
 // Loads of one tile whose 16 token rows are consecutive in one page, for the
@@ -260,7 +269,7 @@ __device__ inline V stream_load(const char* p) {
 // tile's first row (head offset included); rows past `last` repeat row `last`.
 //   K: lane l reads row l%16, 16 B at d = 32 s + 8 (l/16)
 //   V: lane l reads rows 4 (l/16) + j, D/16 elements at d = (D/16) (l%16)
-template <int D>
+template <int D, bool kStream>
 __device__ inline void load_tile_rows(const char* kbase, const char* vbase, int row_bytes, int last,
                                       Tile<D>& t) {
   const int lane = threadIdx.x & 63;
@@ -270,17 +279,17 @@ __device__ inline void load_tile_rows(const char* kbase, const char* vbase, int 
   typedef typename RowVec<NT>::type VT;
   const char* kp = kbase + (r < last ? r : last) * row_bytes + 16 * gq;
 #pragma unroll
-  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = stream_load<u16x8>(kp + 64 * s);
+  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = kv_load<u16x8, kStream>(kp + 64 * s);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int vr = 4 * gq + j;
-    t.v[j] = stream_load<VT>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
+    t.v[j] = kv_load<VT, kStream>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
   }
 }
 
 // Same operand positions, each lane resolving its own token's page (page sizes that
 // are not a multiple of 16, where a tile can straddle pages).
-template <int D>
+template <int D, bool kStream>
 __device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, int head_off, int t0,
                                      int t_last, Tile<D>& t) {
   const int lane = threadIdx.x & 63;
@@ -294,13 +303,13 @@ __device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, 
   const uint16_t* krow = token_row(p.k_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tk);
 #pragma unroll
   for (int s = 0; s < Tile<D>::kSteps; ++s)
-    t.k[s] = stream_load<u16x8>(reinterpret_cast<const char*>(krow + 32 * s + 8 * gq));
+    t.k[s] = kv_load<u16x8, kStream>(reinterpret_cast<const char*>(krow + 32 * s + 8 * gq));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     int tv = t0 + 4 * gq + j;
     tv = tv > t_last ? t_last : tv;
     const uint16_t* vrow = token_row(p.v_pool, idx, p.num_pages, p.page_size, row_elems, head_off, tv);
-    t.v[j] = stream_load<VT>(reinterpret_cast<const char*>(vrow + NT * r));
+    t.v[j] = kv_load<VT, kStream>(reinterpret_cast<const char*>(vrow + NT * r));
   }
 }
 
@@ -474,85 +483,94 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
   // last tile is issued again, an L2 hit) so the compiler's wait counts stay exact
   // and no wait drains the prefetched tiles.
   const int n_tiles = (t_end - t_begin + 15) >> 4;
-  Tile<D> buf[kDepth];
-  if constexpr (kTileInPage) {
-    // Every tile lies inside one page. The ids of a window of 128 pages sit one per
-    // lane in two registers and each tile's id is broadcast to a scalar register
-    // (readlane), so page lookups never wait behind the K/V loads in flight; a chunk
-    // longer than the window refills it once per 128 pages.
-    const int ps = p.page_size;
-    const int row_bytes = p.num_kv_heads * D * 2;
-    const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
-    const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
-    const int first_page = t_begin / ps;
-    const int np_seq = p.indptr[b + 1] - p.indptr[b];
-    int win_lo = 0, win_hi = 0;  // window = pages [first_page + win_base, +128)
-    int win_base = 0;
-    auto load_window = [&]() {
-      const int pg0 = first_page + win_base + lane;
-      int a = pg0 < np_seq ? idx[pg0] : 0;
-      int c = pg0 + 64 < np_seq ? idx[pg0 + 64] : 0;
-      win_lo = (a < 0 || (int64_t)a >= p.num_pages) ? 0 : a;
-      win_hi = (c < 0 || (int64_t)c >= p.num_pages) ? 0 : c;
-    };
-    load_window();
-    int ld_tile = 0;
-    int page_ld = 0;  // page of the next tile, relative to first_page
-    int slot_ld = t_begin - first_page * ps;
-    const char* kb = kpool;
-    const char* vb = vpool;
-    int last = 0;
-    auto issue = [&](Tile<D>& dst) {
-      if (ld_tile < n_tiles) {
-        if (page_ld - win_base == 128) {
-          win_base += 128;
-          load_window();
+  auto pipeline = [&](auto stream_tag) {
+    constexpr bool kStream = decltype(stream_tag)::value;
+    Tile<D> buf[kDepth];
+    if constexpr (kTileInPage) {
+      // Every tile lies inside one page. The ids of a window of 128 pages sit one per
+      // lane in two registers and each tile's id is broadcast to a scalar register
+      // (readlane), so page lookups never wait behind the K/V loads in flight; a chunk
+      // longer than the window refills it once per 128 pages.
+      const int ps = p.page_size;
+      const int row_bytes = p.num_kv_heads * D * 2;
+      const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
+      const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
+      const int first_page = t_begin / ps;
+      const int np_seq = p.indptr[b + 1] - p.indptr[b];
+      int win_lo = 0, win_hi = 0;  // window = pages [first_page + win_base, +128)
+      int win_base = 0;
+      auto load_window = [&]() {
+        const int pg0 = first_page + win_base + lane;
+        int a = pg0 < np_seq ? idx[pg0] : 0;
+        int c = pg0 + 64 < np_seq ? idx[pg0 + 64] : 0;
+        win_lo = (a < 0 || (int64_t)a >= p.num_pages) ? 0 : a;
+        win_hi = (c < 0 || (int64_t)c >= p.num_pages) ? 0 : c;
+      };
+      load_window();
+      int ld_tile = 0;
+      int page_ld = 0;  // page of the next tile, relative to first_page
+      int slot_ld = t_begin - first_page * ps;
+      const char* kb = kpool;
+      const char* vb = vpool;
+      int last = 0;
+      auto issue = [&](Tile<D>& dst) {
+        if (ld_tile < n_tiles) {
+          if (page_ld - win_base == 128) {
+            win_base += 128;
+            load_window();
+          }
+          const int j = page_ld - win_base;
+          const int pid = j < 64 ? __builtin_amdgcn_readlane(win_lo, j) : __builtin_amdgcn_readlane(win_hi, j - 64);
+          const int64_t row0 = (int64_t)pid * ps + slot_ld;
+          kb = kpool + row0 * row_bytes;
+          vb = vpool + row0 * row_bytes;
+          last = min(15, t_last - (t_begin + 16 * ld_tile));
+          slot_ld += 16;
+          if (slot_ld == ps) {
+            slot_ld = 0;
+            ++page_ld;
+          }
+          ++ld_tile;
         }
-        const int j = page_ld - win_base;
-        const int pid = j < 64 ? __builtin_amdgcn_readlane(win_lo, j) : __builtin_amdgcn_readlane(win_hi, j - 64);
-        const int64_t row0 = (int64_t)pid * ps + slot_ld;
-        kb = kpool + row0 * row_bytes;
-        vb = vpool + row0 * row_bytes;
-        last = min(15, t_last - (t_begin + 16 * ld_tile));
-        slot_ld += 16;
-        if (slot_ld == ps) {
-          slot_ld = 0;
-          ++page_ld;
+        load_tile_rows<D, kStream>(kb, vb, row_bytes, last, dst);
+      };
+  #pragma unroll
+      for (int j = 0; j < kDepth - 1; ++j) issue(buf[j]);
+      for (int i = 0; i < n_tiles; i += kDepth) {
+  #pragma unroll
+        for (int j = 0; j < kDepth; ++j) {
+          if (i + j >= n_tiles) break;
+          issue(buf[(j + kDepth - 1) % kDepth]);
+          // keep the prefetch ahead of this tile's math (the scheduler would otherwise
+          // sink the loads below the first MFMAs)
+          __builtin_amdgcn_sched_barrier(0);
+          process(buf[j], t_begin + 16 * (i + j));
         }
-        ++ld_tile;
       }
-      load_tile_rows<D>(kb, vb, row_bytes, last, dst);
-    };
-#pragma unroll
-    for (int j = 0; j < kDepth - 1; ++j) issue(buf[j]);
-    for (int i = 0; i < n_tiles; i += kDepth) {
-#pragma unroll
-      for (int j = 0; j < kDepth; ++j) {
-        if (i + j >= n_tiles) break;
-        issue(buf[(j + kDepth - 1) % kDepth]);
-        // keep the prefetch ahead of this tile's math (the scheduler would otherwise
-        // sink the loads below the first MFMAs)
-        __builtin_amdgcn_sched_barrier(0);
-        process(buf[j], t_begin + 16 * (i + j));
+    } else {
+      const int head_off = h * D;
+      auto issue_any = [&](int tile, Tile<D>& dst) {
+        load_tile_any<D, kStream>(p, idx, head_off, t_begin + 16 * min(tile, n_tiles - 1), t_last, dst);
+      };
+  #pragma unroll
+      for (int j = 0; j < kDepth - 1; ++j) issue_any(j, buf[j]);
+      for (int i = 0; i < n_tiles; i += kDepth) {
+  #pragma unroll
+        for (int j = 0; j < kDepth; ++j) {
+          if (i + j >= n_tiles) break;
+          issue_any(i + j + kDepth - 1, buf[(j + kDepth - 1) % kDepth]);
+          __builtin_amdgcn_sched_barrier(0);
+          process(buf[j], t_begin + 16 * (i + j));
+        }
       }
     }
-  } else {
-    const int head_off = h * D;
-    auto issue_any = [&](int tile, Tile<D>& dst) {
-      load_tile_any<D>(p, idx, head_off, t_begin + 16 * min(tile, n_tiles - 1), t_last, dst);
-    };
-#pragma unroll
-    for (int j = 0; j < kDepth - 1; ++j) issue_any(j, buf[j]);
-    for (int i = 0; i < n_tiles; i += kDepth) {
-#pragma unroll
-      for (int j = 0; j < kDepth; ++j) {
-        if (i + j >= n_tiles) break;
-        issue_any(i + j + kDepth - 1, buf[(j + kDepth - 1) % kDepth]);
-        __builtin_amdgcn_sched_barrier(0);
-        process(buf[j], t_begin + 16 * (i + j));
-      }
-    }
-  }
+  };
+  bool stream = p.stream != 0;
+  if constexpr (kGrouped) stream = stream && g < 0;  // a group's prefix: read by every group sharing it
+  if (stream)
+    pipeline(std::true_type{});
+  else
+    pipeline(std::false_type{});
 
   const float l_tot = rows_sum(l_run);
   if (!head_ok) return;
@@ -765,6 +783,10 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupA
 // is used: 256 CUs x 3 workgroups of 4 waves.
 constexpr int kMaxDevices = 64;
 constexpr int kDefaultSlots = 768;
+
+// Calls whose K/V (both, all KV heads) exceed this stream them with non-temporal
+// loads; smaller ones are left in the caches (MI355X: 256 MB of memory-side cache).
+constexpr int64_t kStreamBytes = (int64_t)128 << 20;
 
 template <typename T, int D, bool kTileInPage, bool kGrouped>
 int decode_wg_slots(int waves) {
@@ -982,6 +1004,21 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
   p.out = (uint16_t*)out;
   p.out_stride = out_stride;
   p.slot_members = slot_members;
+  // distinct K/V tokens of the call: the members' own tokens and, since the groups of
+  // a batch usually share one cached prompt, the longest group prefix once
+  int64_t distinct_tokens = total_tokens;
+  if constexpr (kGrouped) {
+    int64_t longest = 0;
+    for (int g = 0; g < num_groups; ++g) {
+      int members = 0;
+      for (int m = 0; m < kGroupCols; ++m) members += ga.member_seq[g * kGroupCols + m] >= 0 ? 1 : 0;
+      const int64_t prefix = (int64_t)ga.prefix_pages[g] * page_size;
+      distinct_tokens -= members * prefix;
+      longest = prefix > longest ? prefix : longest;
+    }
+    distinct_tokens += longest;
+  }
+  p.stream = distinct_tokens * num_kv_heads * head_dim * 2 * 2 > kStreamBytes ? 1 : 0;
   char* ws = (char*)workspace;
   p.part_o = (float*)ws;
   p.part_ml = p.part_o + mc * slot_members * num_qo_heads * head_dim;
