@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # copy of known size, over that pass's algorithmic bytes
 # (profiles/paged_decode_hbm_traffic_kv_pressure_b64.md). `traffic` in the JSON line is
 # this ratio times the algorithmic bytes of the run being reported.
-TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0057}
+TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0113}
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 

@@ -531,6 +531,11 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
             ++page_ld;
           }
           ++ld_tile;
+        } else {
+          // past the chunk's end: the issue only keeps the wait counts exact and its
+          // tile is never computed, so every lane reads the last tile's first row
+          // (512 B per wave, not the whole 8 KB tile again)
+          last = 0;
         }
         load_tile_rows<D, kStream>(kb, vb, row_bytes, last, dst);
       };
