@@ -24,12 +24,13 @@ def _log(msg):
     sys.stdout.flush()
 
 
-def make(ps=16, pages=256, prefix=True, dtype=torch.float16):
+def make(ps=16, pages=256, prefix=True, dtype=torch.float16, partial=True):
     from nanoslg_amd import kv_cache as KC
     cfg = KC.KVCacheConfig(num_layers=L, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=ps,
                            max_pages=pages, dtype=dtype, device=DEV, enable_prefix_caching=prefix,
-                           backend="paged")
-    return KC.PagedKVCache(cfg), O.PagedRef(L, pages, ps, HKV, D, torch.float32, enable_prefix_caching=prefix)
+                           backend="paged", share_partial_pages=partial)
+    return KC.PagedKVCache(cfg), O.PagedRef(L, pages, ps, HKV, D, torch.float32, enable_prefix_caching=prefix,
+                                            share_partial_pages=partial)
 
 
 def forward_both(mgr, ref, ids, ntok, offs, g, dtype=torch.float16):
