@@ -6,11 +6,12 @@ heads, head_dim 128, fp16, page size 16), batch 64, context lengths log-uniform
 in [2048, 32768], pool sized to 90 % occupancy with pages shuffled across
 sequences, 10 % of pages released and re-allocated mid-run. One step = one decode
 step of that layer through the drop-in API (begin_forward -> attend -> end_forward):
-plan upload, K/V append kernel, split-K decode kernel and merge.
+planning, the split-K decode kernel (which writes the step's new K/V rows) and
+the merge.
 
 Prints ONE JSON line. `value` = algorithmic HBM bytes per step / wall time per
-step (GB/s). `roofline` = the nslg_paged_decode call (split-K decode kernel + merge
-kernel), timed with HIP events on its stream around every call of a second pass of
+step (GB/s). `roofline` = the nslg_paged_decode_append call (split-K decode kernel
++ merge kernel), timed with HIP events on its stream around every call of a second pass of
 `--steps` steps of the same workload (timing events slow the queue by ~10 us per
 step, so the pass that gives `value` runs without them).
 `cpu_baseline` = the CPU restatement of the reference's contiguous SDPA path on a
@@ -180,12 +181,14 @@ def step_bytes(lens_after, B, total_pages):
 
 
 def decode_call_bytes(lens_after, B, total_pages):
-    """Algorithmic HBM bytes of one nslg_paged_decode call: K and V of every cached
-    token once, q read and out written once, the CSR block table once."""
+    """Algorithmic HBM bytes of one nslg_paged_decode_append call: K and V of every
+    cached token once, the step's new K/V rows read and written once, q read and out
+    written once, the CSR block table once."""
     kv = sum(lens_after) * HKV * D * 2 * 2
+    append = B * HKV * D * 2 * 2 * 2
     qo = B * HQ * D * 2 * 2
     csr = 4 * (total_pages + 2 * B + 1)
-    return kv + qo + csr
+    return kv + append + qo + csr
 
 
 def kv_pressure_lens(seed, B=64):
@@ -213,13 +216,12 @@ class EventTimedKernels:
     def DecodeLaunch(self, k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages,
                      num_qo_heads, workspace=None, sm_scale=None, groups=None):
         """The per-forward launcher (re-bound from forward to forward as the product's
-        is); while recording, each layer runs as append_kv and then an event-timed
-        paged_decode (the same launches, the same results)."""
+        is); while recording, each layer's call (nslg_paged_decode_append: the decode
+        with the step's new rows written inside it) is bracketed by events."""
         real = self._k.DecodeLaunch(k_pool, v_pool, slot_mapping, kv_indptr, kv_indices, kv_last_page_len,
                                     total_pages, num_qo_heads, workspace=workspace, sm_scale=sm_scale,
                                     groups=groups)
-        return _TimedLaunch(self, real, (k_pool, v_pool), sm_scale,
-                            (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups))
+        return _TimedLaunch(self, real)
 
     def paged_decode(self, *args, **kw):
         if not self.recording:
@@ -253,28 +255,28 @@ class EventTimedKernels:
 
 
 class _TimedLaunch:
-    """A kernels.DecodeLaunch whose decode calls are event-timed while recording."""
+    """A kernels.DecodeLaunch whose calls are event-timed while recording."""
 
-    def __init__(self, timed, real, pools, sm_scale, plan):
-        self.timed, self.real, self.pools, self.sm_scale, self.plan = timed, real, pools, sm_scale, plan
+    def __init__(self, timed, real):
+        self.timed, self.real = timed, real
         self.B, self.Hq, self.workspace = real.B, real.Hq, real.workspace
 
     def rebind(self, slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups=None, check=True):
         self.real.rebind(slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups, check=check)
-        self.plan = (slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups)
         return self
 
     def __call__(self, layer, q, k_new, v_new, rope=None):
         timed = self.timed
-        if q.dim() == 4 and timed.recording and rope is None:  # a forward's [B, 1, Hq, D] grid
-            return self(layer, q[:, 0], k_new, v_new).reshape(q.shape[0], 1, -1)
         if not timed.recording or rope is not None:
             return self.real(layer, q, k_new, v_new, rope=rope)
-        slots, indptr, indices, lpl, total_pages, groups = self.plan
-        k_pool, v_pool = self.pools
-        timed._k.append_kv(k_new, v_new, slots, k_pool[layer], v_pool[layer])
-        return timed.paged_decode(q, k_pool[layer], v_pool[layer], indptr, indices, lpl, total_pages,
-                                  sm_scale=self.sm_scale, workspace=self.workspace, groups=groups)
+        torch = timed._torch
+        stream = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        out = self.real(layer, q, k_new, v_new)
+        b.record(stream)
+        timed.events.append((a, b))
+        return out
 
 
 def copy_calibration():
@@ -513,7 +515,7 @@ def run_decode(args):
         "bytes_per_step": {k: int(v / args.steps) for k, v in zip(["kv_read", "append", "q_out", "csr"], nbytes)},
         "roofline": {
             "bound": "hbm",
-            "kernel": "nslg_paged_decode (split-K decode kernel + LSE merge kernel)",
+            "kernel": "nslg_paged_decode_append (split-K decode kernel, which also writes the step's new K/V rows, + LSE merge kernel)",
             "timing": (f"HIP events on the launch stream around each of {args.steps} decode calls, "
                        "in a second pass of the same workload after the timed steps"),
             "achieved": round(achieved, 2),
@@ -691,7 +693,7 @@ def run_radix(args):
         "decode_call_kernel_us_prefix16384": long_ab,
         "roofline": {
             "bound": "hbm",
-            "kernel": "nslg_paged_decode (split-K decode kernel + LSE merge kernel)",
+            "kernel": "nslg_paged_decode_append (split-K decode kernel, which also writes the step's new K/V rows, + LSE merge kernel)",
             "timing": f"HIP events around each of {steps} decode calls in a second pass",
             "achieved": round(kbytes / (mean_ms * 1e-3) / 1e9, 2),
             "peak": HBM_PEAK_GBS,

@@ -150,6 +150,38 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
                       nslg_stream_t stream);
 
 /*
+ * The decode step of one layer: each sequence's new token written into the pool,
+ * then decode attention over its tokens including that one. Replaces the write of
+ * FlashInferCacheContext.attend (_write_kv, nanoslg/kv_cache.py:661-674; the slot
+ * mapping of :575-594) together with the decode run (:650), which the reference
+ * issues back to back for one decode forward (:639-655). Same result as
+ * nslg_append_kv of the rows followed by nslg_paged_decode (bit-identical).
+ *
+ *   k_new, v_new   [batch] rows of Hkv*D elements at element strides k_new_stride,
+ *                  v_new_stride (device, the pool's dtype; f16/bf16: 16-byte aligned
+ *                  rows, f32: 4-byte)
+ *   other arguments as nslg_paged_decode
+ * Row b is sequence b's token L_b - 1 (the last token its block table covers, the
+ * reference's slot for the decode write): the slot is found through the block
+ * table, so no slot mapping is passed. The chunk that reads that token writes it
+ * first, in the same kernel (f32 pools: one launch ahead of the attention kernel).
+ * Precondition, which the reference's copy-on-write rule gives (kv_cache.py:575-594):
+ * no other sequence of the call reads a row being written (a written page is not
+ * shared). A row whose page id is out of the pool is not written.
+ */
+int nslg_paged_decode_append(const void* q, int64_t q_stride,
+                             const void* k_new, int64_t k_new_stride,
+                             const void* v_new, int64_t v_new_stride,
+                             void* k_pool, void* v_pool, int64_t num_pages,
+                             int32_t page_size, const int32_t* kv_indptr,
+                             const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                             int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                             int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                             int32_t dtype, void* out, int64_t out_stride,
+                             void* workspace, size_t workspace_bytes,
+                             nslg_stream_t stream);
+
+/*
  * nslg_paged_decode without a caller workspace: the split-K partials live in a
  * static device array of NSLG_NOALLOC_SCRATCH_BYTES (16 MiB) that the library
  * holds on every GPU it runs on until the process ends. No counterpart in the
@@ -215,6 +247,26 @@ int nslg_paged_decode_grouped(const void* q, int64_t q_stride,
                               void* out, int64_t out_stride,
                               void* workspace, size_t workspace_bytes,
                               nslg_stream_t stream);
+
+/*
+ * nslg_paged_decode_grouped with each sequence's new token written first, as
+ * nslg_paged_decode_append does for nslg_paged_decode (the same replacement of
+ * kv_cache.py:661-674 + 650). Group prefixes must lie below every member's last
+ * page (the page the new row goes to), as a shared page is never written.
+ */
+int nslg_paged_decode_grouped_append(const void* q, int64_t q_stride,
+                                     const void* k_new, int64_t k_new_stride,
+                                     const void* v_new, int64_t v_new_stride,
+                                     void* k_pool, void* v_pool, int64_t num_pages,
+                                     int32_t page_size, const int32_t* kv_indptr,
+                                     const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                     int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, float sm_scale,
+                                     int32_t dtype, const int32_t* seq_group_slot,
+                                     int32_t num_groups, const int32_t* group_prefix_pages,
+                                     const int32_t* group_members, void* out, int64_t out_stride,
+                                     void* workspace, size_t workspace_bytes,
+                                     nslg_stream_t stream);
 
 /*
  * Paged causal prefill attention over a ragged batch of new tokens whose K/V

@@ -68,6 +68,12 @@ struct DecodeParams {
   float* part_ml;  // [max_chunks, slot_members, Hq, 2]
   int32_t slot_members;  // partial slots per (chunk, query head): 1, or the members of a group
   int32_t stream;        // 1: the call's K/V exceed the caches: stream them (non-temporal loads)
+  // New rows (null: none). Sequence b's row of k_new / v_new is its token L_b - 1:
+  // the chunk holding that token writes it into the pool before reading it.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t k_new_stride;  // elements between batch rows
+  int64_t v_new_stride;
 };
 
 // Prefix groups of a grouped decode call: sequences whose first pages are the same
@@ -401,6 +407,29 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
   const int t_end = base + min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
   const int t_last = t_end - 1;
   const int32_t* idx = p.indices + p.indptr[b];
+
+  // The new row of sequence b (its last token, in its last page) is written by its
+  // last chunk, this wave for its own KV head, before any of the chunk's loads: the
+  // loads of one wave after its store to the same address return the stored data,
+  // and no other chunk (nor, by the copy-on-write rule, any other sequence) reads
+  // that row. 16-byte vectors: lanes [0, D/8) carry K, [D/8, D/4) V.
+  if (p.k_new != nullptr && u < p.batch && c_local == nchunks - 1 && t_end > t_begin) {
+    const int tok = t_end - 1;
+    const int pid = idx[tok / p.page_size];
+    if (pid >= 0 && (int64_t)pid < p.num_pages) {
+      constexpr int kVecs = D / 8;
+      const int64_t row = ((int64_t)pid * p.page_size + tok % p.page_size) * p.num_kv_heads * D + (int64_t)h * D;
+      if (lane < 2 * kVecs) {
+        const bool is_v = lane >= kVecs;
+        const int e = 8 * (is_v ? lane - kVecs : lane);
+        const uint16_t* src = (is_v ? p.v_new + (int64_t)b * p.v_new_stride : p.k_new + (int64_t)b * p.k_new_stride) +
+                              (int64_t)h * D + e;
+        uint16_t* dst = const_cast<uint16_t*>(is_v ? p.v_pool : p.k_pool) + row + e;
+        *reinterpret_cast<u16x8*>(dst) = *reinterpret_cast<const u16x8*>(src);
+      }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the compiler from moving loads above the store
+  }
 
   // Column r of the MFMA tiles (lane l: r = l % 16) is query head h*G + r of sequence
   // b; in a group's prefix it is head h*G + r%G of member r/G.
@@ -890,6 +919,27 @@ int launch_decode(const DecodeParams& p, const MergeParams& mp, const GroupArgs<
   return check_launch("paged_decode_merge");
 }
 
+// New rows of an fp32 decode call (whose attention kernel has no folded write):
+// grid (batch, 2), workgroup b writes sequence b's K (y = 0) or V (y = 1) row as
+// its token L_b - 1, the slot found through its block table. 4-byte words.
+__global__ void __launch_bounds__(256)
+write_last_rows_kernel(const uint32_t* __restrict__ k_new, const uint32_t* __restrict__ v_new,
+                       int64_t k_stride_words, int64_t v_stride_words, const int32_t* __restrict__ indptr,
+                       const int32_t* __restrict__ indices, const int32_t* __restrict__ last_len,
+                       int32_t page_size, int64_t num_pages, int32_t row_words, uint32_t* __restrict__ k_pool,
+                       uint32_t* __restrict__ v_pool) {
+  const int b = blockIdx.x;
+  const int len = seq_len_of(indptr, last_len, b, page_size);
+  if (len <= 0) return;
+  const int tok = len - 1;
+  const int pid = indices[indptr[b] + tok / page_size];
+  if (pid < 0 || (int64_t)pid >= num_pages) return;
+  const bool is_v = blockIdx.y != 0;
+  const uint32_t* src = is_v ? v_new + (int64_t)b * v_stride_words : k_new + (int64_t)b * k_stride_words;
+  uint32_t* dst = (is_v ? v_pool : k_pool) + ((int64_t)pid * page_size + tok % page_size) * row_words;
+  for (int i = threadIdx.x; i < row_words; i += blockDim.x) dst[i] = src[i];
+}
+
 inline size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace: partials [max_chunks, slot_members, Hq, D] and [..., 2] fp32, then each
@@ -907,13 +957,21 @@ bool shape_ok(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t
          num_qo_heads % num_kv_heads == 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
+// The new rows of an append-and-decode call (k = v = null: a decode call alone).
+struct NewRows {
+  const void* k = nullptr;
+  const void* v = nullptr;
+  int64_t k_stride = 0;  // elements between batch rows
+  int64_t v_stride = 0;
+};
+
 template <bool kGrouped>
 int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void* v_pool, int64_t num_pages,
                 int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
                 const int32_t* kv_last_page_len, int64_t total_pages, int32_t batch, int32_t num_qo_heads,
                 int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype, void* out,
                 int64_t out_stride, GroupArgs<kGrouped>& ga, int32_t num_groups, int32_t slot_members,
-                void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
+                void* workspace, size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr = NewRows{}) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_pages < 0)
     return fail(NSLG_EINVAL, "paged_decode: bad sizes");
@@ -922,6 +980,18 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     return fail(NSLG_EINVAL, "paged_decode: null pointer");
   if (num_qo_heads % num_kv_heads != 0)
     return fail(NSLG_EINVAL, "paged_decode: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
+  if (nr.k || nr.v) {
+    const int eb = dtype == NSLG_F32 ? 4 : 2;
+    const int64_t row = (int64_t)num_kv_heads * head_dim;
+    if (!nr.k || !nr.v) return fail(NSLG_EINVAL, "paged_decode_append: null k_new or v_new");
+    if (batch > 1 && (nr.k_stride < row || nr.v_stride < row))
+      return fail(NSLG_EINVAL, "paged_decode_append: new rows overlap (strides %lld, %lld < Hkv*D = %lld)",
+                  (long long)nr.k_stride, (long long)nr.v_stride, (long long)row);
+    const int64_t align = dtype == NSLG_F32 ? 4 : 16;
+    if ((int64_t)((uintptr_t)nr.k % align) || (int64_t)((uintptr_t)nr.v % align) || (nr.k_stride * eb) % align ||
+        (nr.v_stride * eb) % align)
+      return fail(NSLG_EINVAL, "paged_decode_append: new rows must be %lld-byte aligned", (long long)align);
+  }
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_decode: GQA group %d > 16", group);
   if (num_qo_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_decode: %d query heads", num_qo_heads);
@@ -964,6 +1034,14 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
         if (((uintptr_t)workspace) & 255) return fail(NSLG_EINVAL, "paged_decode: workspace must be 256-byte aligned");
         a.part_o = (float*)workspace;
         a.part_ml = a.part_o + (int64_t)batch * num_qo_heads * a.splits * head_dim;
+      }
+      if (nr.k) {
+        const int row_words = num_kv_heads * head_dim;
+        write_last_rows_kernel<<<dim3(batch, 2), row_words < 256 ? 64 : 256, 0, as_stream(stream)>>>(
+            (const uint32_t*)nr.k, (const uint32_t*)nr.v, nr.k_stride, nr.v_stride, kv_indptr, kv_indices,
+            kv_last_page_len, page_size, num_pages, row_words, (uint32_t*)k_pool, (uint32_t*)v_pool);
+        const int rc = check_launch("paged_decode_append (rows)");
+        if (rc) return rc;
       }
       return attention_f32(a, batch, head_dim, as_stream(stream));
     }
@@ -1024,6 +1102,10 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     distinct_tokens += longest;
   }
   p.stream = distinct_tokens * num_kv_heads * head_dim * 2 * 2 > kStreamBytes ? 1 : 0;
+  p.k_new = (const uint16_t*)nr.k;
+  p.v_new = (const uint16_t*)nr.v;
+  p.k_new_stride = nr.k_stride;
+  p.v_new_stride = nr.v_stride;
   char* ws = (char*)workspace;
   p.part_o = (float*)ws;
   p.part_ml = p.part_o + mc * slot_members * num_qo_heads * head_dim;
@@ -1168,16 +1250,36 @@ extern "C" int nslg_paged_decode_noalloc(const void* q, int64_t q_stride, const 
                             dtype, out, out_stride, ga, 0, 1, ws, (size_t)NSLG_NOALLOC_SCRATCH_BYTES, stream);
 }
 
-extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const void* k_pool,
-                                         const void* v_pool, int64_t num_pages, int32_t page_size,
-                                         const int32_t* kv_indptr, const int32_t* kv_indices,
-                                         const int32_t* kv_last_page_len, int64_t total_pages,
-                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
-                                         int32_t head_dim, float sm_scale, int32_t dtype,
-                                         const int32_t* seq_group_slot, int32_t num_groups,
-                                         const int32_t* group_prefix_pages, const int32_t* group_members,
-                                         void* out, int64_t out_stride, void* workspace,
-                                         size_t workspace_bytes, nslg_stream_t stream) {
+extern "C" int nslg_paged_decode_append(const void* q, int64_t q_stride, const void* k_new,
+                                        int64_t k_new_stride, const void* v_new, int64_t v_new_stride,
+                                        void* k_pool, void* v_pool, int64_t num_pages, int32_t page_size,
+                                        const int32_t* kv_indptr, const int32_t* kv_indices,
+                                        const int32_t* kv_last_page_len, int64_t total_pages,
+                                        int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                        int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                        nslg_stream_t stream) {
+  if (batch > 0 && (!k_new || !v_new)) return fail(NSLG_EINVAL, "paged_decode_append: null k_new or v_new");
+  NewRows nr;
+  nr.k = k_new;
+  nr.v = v_new;
+  nr.k_stride = k_new_stride;
+  nr.v_stride = v_new_stride;
+  GroupArgs<false> ga;
+  return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
+                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, nr);
+}
+
+namespace {
+
+int grouped_impl(const void* q, int64_t q_stride, const void* k_pool, const void* v_pool, int64_t num_pages,
+                 int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
+                 const int32_t* kv_last_page_len, int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+                 int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
+                 const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
+                 const int32_t* group_members, void* out, int64_t out_stride, void* workspace,
+                 size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr) {
   if (num_groups < 1 || num_groups > kMaxGroups)
     return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: %d groups (1..%d)", num_groups, kMaxGroups);
   if (!seq_group_slot || !group_prefix_pages || !group_members)
@@ -1223,5 +1325,44 @@ extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const 
   if (batch > 32767) return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: batch %d > 32767", batch);
   return decode_impl<true>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
-                           dtype, out, out_stride, ga, num_groups, max_members, workspace, workspace_bytes, stream);
+                           dtype, out, out_stride, ga, num_groups, max_members, workspace, workspace_bytes, stream,
+                           nr);
+}
+
+}  // namespace
+
+extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const void* k_pool,
+                                         const void* v_pool, int64_t num_pages, int32_t page_size,
+                                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                                         const int32_t* kv_last_page_len, int64_t total_pages,
+                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, float sm_scale, int32_t dtype,
+                                         const int32_t* seq_group_slot, int32_t num_groups,
+                                         const int32_t* group_prefix_pages, const int32_t* group_members,
+                                         void* out, int64_t out_stride, void* workspace,
+                                         size_t workspace_bytes, nslg_stream_t stream) {
+  return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
+                      total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
+                      num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,
+                      stream, NewRows{});
+}
+
+extern "C" int nslg_paged_decode_grouped_append(
+    const void* q, int64_t q_stride, const void* k_new, int64_t k_new_stride, const void* v_new,
+    int64_t v_new_stride, void* k_pool, void* v_pool, int64_t num_pages, int32_t page_size,
+    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_last_page_len, int64_t total_pages,
+    int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
+    const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
+    const int32_t* group_members, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
+    nslg_stream_t stream) {
+  if (batch > 0 && (!k_new || !v_new)) return fail(NSLG_EINVAL, "paged_decode_grouped_append: null k_new or v_new");
+  NewRows nr;
+  nr.k = k_new;
+  nr.v = v_new;
+  nr.k_stride = k_new_stride;
+  nr.v_stride = v_new_stride;
+  return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
+                      total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
+                      num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,
+                      stream, nr);
 }

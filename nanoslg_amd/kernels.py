@@ -276,6 +276,26 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     """Decode attention. q: [B, Hq, D] (rows may be strided); returns [B, Hq, D].
     With `groups`, the shared prefix pages of each group are read once for all its
     members (nslg_paged_decode_grouped)."""
+    return _decode(q, None, None, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                   sm_scale, out, workspace, groups)
+
+
+def paged_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_layer: torch.Tensor,
+                        v_layer: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                        kv_last_page_len: torch.Tensor, total_pages: int, sm_scale: Optional[float] = None,
+                        out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
+                        groups: Optional[DecodeGroups] = None) -> torch.Tensor:
+    """One decode step of a layer (nslg_paged_decode_append / _grouped_append): row b
+    of k_new / v_new ([B, ..., Hkv, D], one token per sequence, rows may be strided)
+    is written into the pool as sequence b's last token (the slot its block table
+    gives for token L_b - 1), then decode attention as paged_decode. Same result as
+    append_kv of those rows followed by paged_decode."""
+    return _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                   sm_scale, out, workspace, groups)
+
+
+def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages, sm_scale,
+            out, workspace, groups):
     _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
         _i32(t, n)
@@ -295,9 +315,28 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
         raise ValueError("paged_decode: bad out tensor")
     lib = _lib.load()
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    rows = None
+    if k_new is not None:
+        _require_gpu(q, k_new, v_new)
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise TypeError("paged_decode_append: k_new/v_new dtype must match the pool")
+        rows = []
+        for t, name in ((k_new, "k_new"), (v_new, "v_new")):
+            n, stride, h = _rows(t, name)
+            if n != B or h != Hkv or t.shape[-1] != D:
+                raise ValueError(f"paged_decode_append: {name} must hold {B} rows of [{Hkv}, {D}]")
+            rows += [t.data_ptr(), stride]
     if groups is None:
         need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(total_pages), ps, dtype_code(q.dtype)))
         ws = (workspace or Workspace(q.device)).get(need)
+        if rows is not None:
+            rc = lib.nslg_paged_decode_append(q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(),
+                                              v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                              kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
+                                              dtype_code(q.dtype), out.data_ptr(), out.stride(0), ws.data_ptr(),
+                                              ws.numel(), _stream(q))
+            _lib.check(rc, "nslg_paged_decode_append")
+            return out
         rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
                                    kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
                                    int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
@@ -313,6 +352,15 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
     if need == 0:
         raise ValueError("paged_decode: unsupported grouped decode shape")
     ws = (workspace or Workspace(q.device)).get(need)
+    if rows is not None:
+        rc = lib.nslg_paged_decode_grouped_append(
+            q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+            kv_indices.data_ptr(), kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
+            dtype_code(q.dtype), groups.seq_group_slot.data_ptr(), groups.num_groups,
+            groups.prefix_pages_np.ctypes.data, groups.members_np.ctypes.data, out.data_ptr(), out.stride(0),
+            ws.data_ptr(), ws.numel(), _stream(q))
+        _lib.check(rc, "nslg_paged_decode_grouped_append")
+        return out
     rc = lib.nslg_paged_decode_grouped(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
                                        kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
                                        int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
@@ -381,11 +429,20 @@ def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_
     return _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args)
 
 
-def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args):
+def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args, out=None):
     """decode_plan_step without the argument checks, for callers whose inputs are the
     previous plan's outputs (the cache manager). new_page: contiguous int32 numpy;
-    pool_args: (k_pool ptr, v_pool ptr, L, P, Hkv, D, dtype code) or all-null."""
+    pool_args: (k_pool ptr, v_pool ptr, L, P, Hkv, D, dtype code) or all-null. `out`:
+    preallocated outputs (an object with indptr, indices, lpl, slot, pos, new_pages
+    tensors, `ptrs` = their six addresses, indices with room for this step's pages),
+    else new tensors (indices exactly this step's pages)."""
     B = kv_indptr.numel() - 1
+    if out is not None:
+        rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                              kv_last_page_len.data_ptr(), B, int(page_size), new_page.ctypes.data,
+                                              *out.ptrs, *pool_args, _stream(kv_indptr))
+        _lib.check(rc, "nslg_decode_plan_step")
+        return out.indptr, out.indices, out.lpl, out.slot, out.pos, out.new_pages
     cap = kv_indices.numel() + num_new
     sizes = [B + 1, cap, B, B, B, num_new]
     buf = torch.empty(sum(sizes) + 1, dtype=torch.int32, device=kv_indptr.device)
@@ -486,9 +543,11 @@ class DecodeLaunch:
 
     What is the same for all layers of the forward (pools, block table, slot
     mapping, sizes, the workspace and its size) is checked and computed once, here;
-    each call checks that layer's tensors and issues nslg_append_kv (or
-    nslg_rope_append) then the decode on the current stream. Same results as
-    append_kv followed by paged_decode on the layer's pool slices.
+    each call checks that layer's tensors and issues, on the current stream, one
+    nslg_paged_decode_append (each sequence's new row written by the decode chunk
+    that reads it; rows that are not 16-byte aligned, 4-byte for fp32, take
+    nslg_append_kv then the decode), or nslg_rope_append then the decode. Same
+    results as append_kv followed by paged_decode on the layer's pool slices.
 
     A launcher can be re-bound to the next forward's plan (rebind) when the pools,
     batch size and head count stay: the pool geometry is then not checked again."""
@@ -505,6 +564,9 @@ class DecodeLaunch:
         self.device, self.dtype = k_pool.device, k_pool.dtype
         self.dev_index = k_pool.get_device()
         self.code = dtype_code(k_pool.dtype)
+        # new rows written inside the decode launch: 16-byte rows (4-byte for fp32)
+        self.esize = k_pool.element_size()
+        self.row_align = 3 if k_pool.dtype == torch.float32 else 15
         self.L, self.P, self.ps, self.Hkv, self.D, self.Hq = L, P, ps, Hkv, D, num_qo_heads
         self.layer_bytes = P * ps * Hkv * D * k_pool.element_size()
         self.kp0, self.vp0 = k_pool.data_ptr(), v_pool.data_ptr()
@@ -512,6 +574,8 @@ class DecodeLaunch:
         self.workspace = workspace or Workspace(self.device)
         self.scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
         self.B = kv_indptr.numel() - 1
+        self._kv_grid = torch.Size((self.B, 1, Hkv, D))
+        self.groups, self._ws_pages = None, -1
         self.rebind(slot_mapping, kv_indptr, kv_indices, kv_last_page_len, total_pages, groups, check=True)
 
     def rebind(self, slot_mapping: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
@@ -530,31 +594,37 @@ class DecodeLaunch:
         self.slots, self.indptr, self.indices, self.lpl = (slot_mapping.data_ptr(), kv_indptr.data_ptr(),
                                                            kv_indices.data_ptr(), kv_last_page_len.data_ptr())
         self.total_pages = int(total_pages)
+        if groups is self.groups and self.total_pages <= self._ws_pages:
+            return self  # the workspace was sized for up to _ws_pages pages
         self.groups = groups
         lib = self.lib
+        # the size grows with the page count: size it for some headroom, so the steps of
+        # a decode batch (a page more now and then) do not query it again
+        bound = self.total_pages + max(self.total_pages // 4, 1024)
         if groups is None:
-            need = int(lib.nslg_paged_decode_workspace_size(B, self.Hq, self.Hkv, self.D, self.total_pages,
-                                                            self.ps, self.code))
+            need = int(lib.nslg_paged_decode_workspace_size(B, self.Hq, self.Hkv, self.D, bound, self.ps, self.code))
         else:
             if check:
                 _require_gpu(self.pools[0], groups.seq_group_slot)
                 _i32(groups.seq_group_slot, "seq_group_slot")
                 if groups.seq_group_slot.numel() != B:
                     raise ValueError("DecodeLaunch: one group slot per sequence")
-            need = int(lib.nslg_paged_decode_grouped_workspace_size(B, self.Hq, self.Hkv, self.D, self.total_pages,
-                                                                    self.ps, self.code, groups.num_groups))
+            need = int(lib.nslg_paged_decode_grouped_workspace_size(B, self.Hq, self.Hkv, self.D, bound, self.ps,
+                                                                    self.code, groups.num_groups))
             if need == 0:
                 raise ValueError("DecodeLaunch: unsupported grouped decode shape")
             self.keep = self.keep + (groups.seq_group_slot,)
         self.ws = self.workspace.get(need)
+        self._ws_pages = bound
         return self
 
     def _kv_rows(self, t: torch.Tensor, name: str) -> int:
         """Row stride of k_new / v_new: [B, ..., Hkv, D] rows of one token each."""
         sh = t.shape
-        if (len(sh) == 4 and sh[0] == self.B and sh[1] == 1 and sh[2] == self.Hkv and sh[3] == self.D
-                and t.stride(3) == 1 and t.stride(2) == self.D):
-            return t.stride(0)
+        if sh == self._kv_grid:  # [B, 1, Hkv, D]
+            st = t.stride()
+            if st[3] == 1 and st[2] == self.D:
+                return st[0]
         n, stride, h = _rows(t, name)
         if n != self.B or h != self.Hkv or sh[-1] != self.D:
             raise ValueError(f"DecodeLaunch: {name} must hold {self.B} rows of [{self.Hkv}, {self.D}]")
@@ -574,11 +644,12 @@ class DecodeLaunch:
                 or k_new.get_device() != di or v_new.get_device() != di):
             raise ValueError(f"DecodeLaunch: tensors must be {self.dtype} on {self.device}")
         B, Hq, D = self.B, self.Hq, self.D
-        if q.dim() == 4:  # [B, 1, Hq, D], a forward's input grid: the output is [B, 1, Hq * D]
-            if q.shape != (B, 1, Hq, D) or q.stride(3) != 1 or q.stride(2) != D:
+        qs, qst = q.shape, q.stride()
+        if len(qs) == 4:  # [B, 1, Hq, D], a forward's input grid: the output is [B, 1, Hq * D]
+            if qs != (B, 1, Hq, D) or qst[3] != 1 or qst[2] != D:
                 raise ValueError(f"DecodeLaunch: q must be [{B}, 1, {Hq}, {D}] with a contiguous [Hq, D] block")
             out_shape = (B, 1, Hq * D)
-        elif q.shape != (B, Hq, D) or q.stride(2) != 1 or q.stride(1) != D:
+        elif qs != (B, Hq, D) or qst[2] != 1 or qst[1] != D:
             raise ValueError(f"DecodeLaunch: q must be [{B}, {Hq}, {D}] with a contiguous [Hq, D] block")
         else:
             out_shape = (B, Hq, D)
@@ -588,11 +659,32 @@ class DecodeLaunch:
         off = layer * self.layer_bytes
         kp, vp = self.kp0 + off, self.vp0 + off
         lib = self.lib
+        out = torch.empty(out_shape, dtype=self.dtype, device=self.device)
+        grp = self.groups
         if rope is None:
-            rc = lib.nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, self.slots, B, kp, vp,
-                                    self.P * self.ps, self.Hkv, D, self.code, stream)
+            kn, vn = k_new.data_ptr(), v_new.data_ptr()
+            if not (kn | vn | (ks | vs) * self.esize) & self.row_align:
+                # one launch: each sequence's new row is written by the chunk that reads it
+                q_ptr, q_stride = q.data_ptr(), qst[0]
+                if grp is None:
+                    rc = lib.nslg_paged_decode_append(q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps,
+                                                      self.indptr, self.indices, self.lpl, self.total_pages, B, Hq,
+                                                      self.Hkv, D, self.scale, self.code, out.data_ptr(), Hq * D,
+                                                      self.ws.data_ptr(), self.ws.numel(), stream)
+                    _lib.check(rc, "nslg_paged_decode_append")
+                else:
+                    rc = lib.nslg_paged_decode_grouped_append(
+                        q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps, self.indptr, self.indices,
+                        self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
+                        grp.seq_group_slot.data_ptr(), grp.num_groups, grp.prefix_pages_np.ctypes.data,
+                        grp.members_np.ctypes.data, out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(),
+                        stream)
+                    _lib.check(rc, "nslg_paged_decode_grouped_append")
+                return out
+            rc = lib.nslg_append_kv(kn, vn, ks, vs, self.slots, B, kp, vp, self.P * self.ps, self.Hkv, D,
+                                    self.code, stream)
             _lib.check(rc, "nslg_append_kv")
-            q_ptr, q_stride = q.data_ptr(), q.stride(0)
+            q_ptr, q_stride = q.data_ptr(), qst[0]
         else:
             cos, sin, pos = rope
             if pos.get_device() != di or pos.dtype != torch.int32 or pos.numel() != B or not pos.is_contiguous():
@@ -607,8 +699,6 @@ class DecodeLaunch:
                                       self.P * self.ps, self.code, stream)
             _lib.check(rc, "nslg_rope_append")
             q_ptr, q_stride = q_rot.data_ptr(), Hq * D
-        out = torch.empty(out_shape, dtype=self.dtype, device=self.device)
-        grp = self.groups
         if grp is None:
             rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
                                        self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,

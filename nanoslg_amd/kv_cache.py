@@ -1136,6 +1136,7 @@ class PagedKVCache(KVCacheManager):
         self._launcher = None  # the last decode forward's kernels.DecodeLaunch
         self._pool_args = None  # the pools as the device planner takes them
         self._decode_rows: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._plan_ring = None  # [batch, capacity, buffers, last used] of device-planned decode steps
         # the block tables on the device (room for every pool page twice before growing)
         self._tables = _BlockTableArena(self.pool.device, 2 * cfg.max_pages + 4096)
         if self.pool.device.type == "cuda":
@@ -1323,14 +1324,20 @@ class PagedKVCache(KVCacheManager):
         if step is None:
             return None
         new_page, n_new = step
-        plan = prev[1]
+        return self._plan_on_device(B, prev[1], new_page, n_new)
+
+    def _plan_on_device(self, B, plan, new_page, n_new) -> "_ForwardPlan":
+        """The next decode plan from `plan` on the device (kernels.decode_plan_step):
+        new_page int32 [B], the page sequence b opens this step or -1."""
+        kern, pool, ps = self.kernels, self.pool, self.cfg.page_size
         fast = getattr(kern, "_decode_plan_step", None)
         if fast is not None:  # inputs are the previous plan's outputs: no argument checks
             if self._pool_args is None:
                 L, P, _, Hkv, D = pool.k.shape
                 self._pool_args = (pool.k.data_ptr(), pool.v.data_ptr(), L, P, Hkv, D, kern.dtype_code(pool.k.dtype))
+            dst = self._plan_buffers(B, plan.total_pages + n_new)
             indptr, indices, lpl, slot, pos, new = fast(plan.indptr, plan.indices, plan.lpl, new_page, ps, n_new,
-                                                        self._pool_args)
+                                                        self._pool_args, out=dst)
         else:
             indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
                                                                         new_page, ps, n_new, pool.k, pool.v)
@@ -1340,6 +1347,80 @@ class PagedKVCache(KVCacheManager):
             rows = self._decode_rows[B] = (qo, qr)
         return _ForwardPlan.from_device(B, slot, pos, indptr, indices, lpl, rows[0], rows[1], new,
                                         plan.total_pages + n_new, groups=plan.groups)
+
+    def _begin_steady_decode(self, seq_ids, ntoks) -> Optional["PagedCacheContext"]:
+        """begin_forward of a steady decode step of a small batch, in one pass over it:
+        the batch the previous decode forward planned on the device, one token per
+        sequence, each at the length that forward left it with the pages it had then,
+        no shared page written, the pages it opens free in the pool and no zeroing owed.
+        Same pages, tokens_used, plan and context as the general path, which takes every
+        other case (eviction, OOM, copy-on-write, a changed batch) and is left untouched
+        when this returns None."""
+        ids, plan, lens = self._dev_plan
+        B = len(ids)
+        if (B > self.SCALAR_PLAN_BATCH or self._pending_zero or len(seq_ids) != B or tuple(seq_ids) != ids
+                or list(ntoks).count(1) != B):
+            return None
+        ps, pool, seqs = self.cfg.page_size, self.pool, self.seqs
+        rc = pool.ref_count
+        states, opening = [], 0
+        for s, n in zip(ids, lens):
+            st = seqs[s]
+            k = n // ps  # the page of the new token
+            if st.num_tokens != n:
+                return None
+            if n % ps:
+                if st.n_pages != k + 1 or rc[st.bt[k]] > 1:
+                    return None
+            elif st.n_pages != k:
+                return None
+            else:
+                opening += 1
+            states.append(st)
+        if opening > pool.num_free:
+            return None
+        new_page = [-1] * B
+        if opening:
+            pages = pool.alloc(opening, zero=False)  # zeroed by the planner, as the general path does
+            it = iter(pages)
+            for b, (st, n) in enumerate(zip(states, lens)):
+                if n % ps == 0:
+                    pid = next(it)
+                    st.extend([pid])
+                    new_page[b] = pid
+        tu = pool.tokens_used
+        for st, n in zip(states, lens):
+            pid = int(st.bt[n // ps])
+            used = n % ps + 1
+            if tu[pid] < used:
+                tu[pid] = used
+        new_plan = self._plan_on_device(B, plan, np.array(new_page, np.int32), opening)
+        ctx = PagedCacheContext.__new__(PagedCacheContext)
+        ctx.cache, ctx.seq_ids, ctx.batch_size = self, list(ids), B
+        ctx.new_token_counts, ctx.input_offsets = [1] * B, [0] * B
+        ctx.start_positions = list(lens)
+        ctx.seq_lens = [n + 1 for n in lens]
+        ctx.max_kv_len = max(ctx.seq_lens)
+        ctx._is_decode, ctx._iw, ctx._max_q, ctx._uniform_rows = True, 1, 1, True
+        ctx.cow_pairs, ctx._plan, ctx._decode_launch = [], new_plan, None
+        self._dev_plan = (ids, new_plan, ctx.seq_lens)
+        return ctx
+
+    PLAN_RING = 3  # device-planned decode steps write their plans into a ring of this many buffers
+
+    def _plan_buffers(self, B, total_pages):
+        """The next plan buffer of the ring for decode batches of B sequences, with room
+        for total_pages block-table entries. Plans of consecutive steps are distinct
+        buffers; the plan of a step is overwritten PLAN_RING steps later (the kernels of
+        those steps run after it on the same stream), so a context's plan stays valid
+        for its own forward and the next ones."""
+        ring = self._plan_ring
+        if ring is None or ring[0] != B or ring[1] < total_pages:
+            cap = total_pages + 16 * B + 4096
+            ring = self._plan_ring = [B, cap, [_GraphPlan(self.pool.device, B, cap) for _ in range(self.PLAN_RING)],
+                                      0]
+        i = ring[3] = (ring[3] + 1) % self.PLAN_RING
+        return ring[2][i]
 
     def allocate_sequence(self, seq_id, token_ids=None, num_tokens=0):
         """kv_cache.py:707-722: radix match, pin, allocate the rest. The matched prefix
@@ -1373,6 +1454,10 @@ class PagedKVCache(KVCacheManager):
             st.extend(self._alloc(need - st.n_pages, defer_zero=True))
 
     def begin_forward(self, seq_ids, ntoks, offsets=None):
+        if offsets is None and self._dev_plan is not None:
+            ctx = self._begin_steady_decode(seq_ids, ntoks)
+            if ctx is not None:
+                return ctx
         ps = self.cfg.page_size
         if any(n != 1 for n in ntoks):
             self._dev_plan = None
@@ -1684,7 +1769,13 @@ class _GraphPlan:
         self.buf = torch.zeros(sum(sizes), dtype=torch.int32, device=device)
         (self.indptr, self.indices, self.lpl, self.slot, self.pos, self.new_pages) = self.buf.split(sizes)
         self.batch, self.iw = batch, 1
+        self.capacity = capacity
         self.groups = None
+        base, o = self.buf.data_ptr(), 0
+        self.ptrs = []
+        for n in sizes:
+            self.ptrs.append(base + 4 * o)
+            o += n
 
 
 class _GraphDecodeContext(CacheContext):

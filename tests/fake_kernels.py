@@ -112,6 +112,17 @@ class DecodeLaunch:
         slots, indptr, indices, lpl, total = self.args
         k_layer, v_layer = self.k_pool[layer], self.v_pool[layer]
         if rope is None:
+            # the product's launch writes row b at the slot of sequence b's last token
+            # through its block table (nslg_paged_decode_append): it must be the
+            # plan's slot for that row
+            ps = k_layer.shape[1]
+            ip, ix, lp = (t.tolist() for t in (indptr, indices, lpl))
+            table_slots = []
+            for b in range(len(ip) - 1):
+                n = ip[b + 1] - ip[b]
+                L = (n - 1) * ps + min(max(lp[b], 1), ps) if n > 0 else 0
+                table_slots.append(ix[ip[b] + (L - 1) // ps] * ps + (L - 1) % ps if L > 0 else -1)
+            assert table_slots == slots.tolist(), (table_slots, slots.tolist())
             append_kv(k_new, v_new, slots, k_layer, v_layer)
         else:
             cos, sin, pos = rope

@@ -76,6 +76,34 @@ def test_host_side_argument_checks():
                                      None) == -1  # half a pool
 
 
+def test_decode_append_argument_checks():
+    """nslg_paged_decode_append / _grouped_append: the new rows are checked on the host
+    (present, not overlapping, aligned for the folded 16-byte writes) before any launch."""
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    geo = (256, 256, 100, 16, 256, 256, 256, 10, 2, 32, 8, 128, 0.1)  # pools .. sm_scale
+    tail = (256, 4096, None, 0, None)  # out, out_stride, workspace, bytes, stream
+    # f16: k_new missing; rows overlapping (stride < Hkv*D); unaligned row stride / pointer
+    assert lib.nslg_paged_decode_append(256, 4096, None, 1024, 256, 1024, *geo, 0, *tail) == -1
+    assert "k_new" in _lib.last_error()
+    assert lib.nslg_paged_decode_append(256, 4096, 256, 1000, 256, 1024, *geo, 0, *tail) == -1
+    assert "overlap" in _lib.last_error()
+    assert lib.nslg_paged_decode_append(256, 4096, 256, 1028, 256, 1024, *geo, 0, *tail) == -1
+    assert "aligned" in _lib.last_error()
+    assert lib.nslg_paged_decode_append(256, 4096, 258, 1024, 256, 1024, *geo, 0, *tail) == -1
+    # fp32 rows only need 4-byte alignment: this one gets as far as the workspace check
+    rc = lib.nslg_paged_decode_append(256, 4096, 260, 1028, 256, 1024, 256, 256, 4096, 16, 256, 256, 256, 2048, 1,
+                                      32, 8, 128, 0.1, 2, *tail)
+    assert rc == -4, _lib.last_error()
+    # batch 0 is a no-op
+    assert lib.nslg_paged_decode_append(None, 0, None, 0, None, 0, *geo[:8], 0, *geo[9:], 0, *tail) == 0
+    members = (ctypes.c_int32 * 16)(0, 1, *([-1] * 14))
+    prefix = (ctypes.c_int32 * 1)(4)
+    rc = lib.nslg_paged_decode_grouped_append(256, 4096, None, 1024, 256, 1024, *geo, 0, 256, 1, prefix, members,
+                                              *tail)
+    assert rc == -1 and "k_new" in _lib.last_error()
+
+
 def test_rope_append_argument_checks():
     from nanoslg_amd import _lib
     lib = _lib.load()

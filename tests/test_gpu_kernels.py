@@ -474,9 +474,10 @@ def test_decode_chunks_longer_than_the_page_window():
 
 
 def test_decode_launch_matches_separate_calls():
-    """The per-forward launcher (append + decode per layer) gives the same pool bytes
-    and the same outputs as append_kv followed by paged_decode on each layer, with q
-    as [B, Hq, D] rows or as a forward's [B, 1, Hq, D] grid (output [B, 1, Hq * D])."""
+    """The per-forward launcher (append + decode per layer, one launch when the new rows
+    are 16-byte aligned) gives the same pool bytes and the same outputs as append_kv
+    followed by paged_decode on each layer, with q as [B, Hq, D] rows or as a forward's
+    [B, 1, Hq, D] grid (output [B, 1, Hq * D]), and with unaligned new rows."""
     _log("decode launcher vs separate calls")
     from nanoslg_amd import kernels as K
     g = torch.Generator().manual_seed(72)
@@ -494,6 +495,9 @@ def test_decode_launch_matches_separate_calls():
         q = torch.randn(len(lens), Hq, D, generator=g).half().to(DEV)
         kn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
         vn = torch.randn(len(lens), 1, Hkv, D, generator=g).half().to(DEV)
+        if layer == 2:  # rows 2 bytes off 16-byte alignment: the append runs as its own launch
+            kn = torch.cat([torch.zeros(1, dtype=kn.dtype, device=DEV), kn.reshape(-1)])[1:].view(kn.shape)
+            assert kn.data_ptr() % 16 == 2
         grid = layer % 2 == 1  # odd layers: the forward's [B, 1, Hq, D] grid
         o1 = launch(layer, q.unsqueeze(1) if grid else q, kn, vn)
         K.append_kv(kn, vn, slots, k2[layer], v2[layer])
@@ -510,6 +514,90 @@ def test_decode_launch_matches_separate_calls():
         launch(0, q.unsqueeze(1).expand(-1, 2, -1, -1), kn, vn)
     with pytest.raises(IndexError):
         launch(L, q, kn, vn)
+
+
+@pytest.mark.parametrize("dtype,D,ps,Hq,Hkv,lens", [
+    (torch.float16, 128, 16, 32, 8, [700, 33, 1500, 1, 16, 17]),
+    (torch.bfloat16, 128, 16, 32, 8, [4096, 2, 31]),
+    (torch.float16, 64, 8, 16, 2, [300, 1, 65]),
+    (torch.bfloat16, 256, 24, 8, 8, [100, 999]),
+    (torch.float16, 128, 1, 16, 1, [40, 3]),
+    (torch.float16, 128, 64, 48, 3, [5000, 64, 65]),
+    (torch.float32, 128, 16, 32, 8, [700, 33, 1]),
+    (torch.float32, 64, 5, 8, 2, [2100, 9]),
+])
+def test_decode_append_bit_exact(dtype, D, ps, Hq, Hkv, lens):
+    """nslg_paged_decode_append (the new rows written by the decode chunk that reads
+    them) against nslg_append_kv at the block table's slots followed by
+    nslg_paged_decode: pools and outputs bit-identical, k_new/v_new as strided views of
+    one projection buffer (the model's layout); and the outputs against the oracle."""
+    _log(f"decode_append {dtype} D={D} ps={ps} Hq={Hq} Hkv={Hkv} lens={lens}")
+    K = _k()
+    g = torch.Generator().manual_seed(D + ps + len(lens))
+    B = len(lens)
+    P = sum(math.ceil(L / ps) for L in lens) + 9
+    k_pool = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    v_pool = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    k2, v2 = k_pool.clone(), v_pool.clone()
+    tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, D + ps)
+    slots = torch.tensor([tables[b][(n - 1) // ps] * ps + (n - 1) % ps for b, n in enumerate(lens)],
+                         dtype=torch.int32, device=DEV)
+    ip, ix, lp = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl))
+    qkv = torch.randn(B, 1, (Hq + 2 * Hkv) * D, generator=g).to(dtype).to(DEV)
+    q = qkv[:, 0, :Hq * D].view(B, Hq, D)
+    kn = qkv[:, :, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D)
+    vn = qkv[:, :, (Hq + Hkv) * D:].view(B, 1, Hkv, D)
+    o1 = K.paged_decode_append(q, kn, vn, k_pool, v_pool, ip, ix, lp, int(indptr[-1]))
+    K.append_kv(kn, vn, slots, k2, v2)
+    o2 = K.paged_decode(q, k2, v2, ip, ix, lp, int(indptr[-1]))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(k_pool), _bits(k2)) and torch.equal(_bits(v_pool), _bits(v2))
+    assert torch.equal(_bits(o1), _bits(o2))
+    ref = O.paged_attention_ref([q[b:b + 1].cpu() for b in range(B)], k2.cpu().view(-1, Hkv, D),
+                                v2.cpu().view(-1, Hkv, D), ps, indptr, indices, lpl, [1] * B)
+    ref = torch.stack([r[0] for r in ref])
+    tol = (2e-5, 1e-4) if dtype == torch.float32 else (ATOL, RTOL)
+    torch.testing.assert_close(o1.cpu().float(), ref, atol=tol[0], rtol=tol[1])
+
+
+def test_decode_append_grouped_bit_exact():
+    """nslg_paged_decode_grouped_append against append + the grouped decode: groups of
+    sequences sharing prefix pages, each writing its new row past the prefix."""
+    _log("decode_append grouped")
+    K = _k()
+    rng = np.random.default_rng(5)
+    ps, Hq, Hkv, D = 16, 32, 8, 128
+    members = [[0, 3, 5], [1, 4]]
+    prefix = [20, 7]
+    pages = iter(rng.permutation(np.arange(1, 3000)).tolist())
+    tables, lens = [None] * 7, [0] * 7
+    for ms, pp in zip(members, prefix):
+        shared = [next(pages) for _ in range(pp)]
+        for b in ms:
+            own = int(rng.integers(1, 200))
+            lens[b] = pp * ps + own
+            tables[b] = shared + [next(pages) for _ in range(math.ceil(own / ps))]
+    for b in (2, 6):
+        lens[b] = int(rng.integers(1, 900))
+        tables[b] = [next(pages) for _ in range(math.ceil(lens[b] / ps))]
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    g = torch.Generator().manual_seed(5)
+    k_pool = torch.randn(3000, ps, Hkv, D, generator=g).half().to(DEV)
+    v_pool = torch.randn(3000, ps, Hkv, D, generator=g).half().to(DEV)
+    k2, v2 = k_pool.clone(), v_pool.clone()
+    q = torch.randn(7, Hq, D, generator=g).half().to(DEV)
+    kn = torch.randn(7, Hkv, D, generator=g).half().to(DEV)
+    vn = torch.randn(7, Hkv, D, generator=g).half().to(DEV)
+    slots = torch.tensor([tables[b][(n - 1) // ps] * ps + (n - 1) % ps for b, n in enumerate(lens)],
+                         dtype=torch.int32, device=DEV)
+    ip, ix, lp = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl))
+    groups = K.DecodeGroups(7, members, prefix, DEV)
+    o1 = K.paged_decode_append(q, kn, vn, k_pool, v_pool, ip, ix, lp, int(indptr[-1]), groups=groups)
+    K.append_kv(kn, vn, slots, k2, v2)
+    o2 = K.paged_decode(q, k2, v2, ip, ix, lp, int(indptr[-1]), groups=groups)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(k_pool), _bits(k2)) and torch.equal(_bits(v_pool), _bits(v2))
+    assert torch.equal(_bits(o1), _bits(o2))
 
 
 @pytest.mark.parametrize("B,ps", [(64, 16), (1, 16), (37, 32), (512, 8)])
