@@ -58,6 +58,27 @@ def _parse():
     return ap.parse_args()
 
 
+class _GcPaused:
+    """A timed region with Python's cyclic garbage collector paused, as timeit runs
+    its loops: a collection walks every object of the process (tens of milliseconds
+    with torch loaded) and would land in whichever step happened to trigger it. A
+    collection runs before the region; reference counting frees the steps' objects
+    as usual inside it."""
+
+    def __enter__(self):
+        import gc
+        gc.collect()
+        self.was_enabled = gc.isenabled()
+        gc.disable()
+        return self
+
+    def __exit__(self, *exc):
+        import gc
+        if self.was_enabled:
+            gc.enable()
+        return False
+
+
 def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -109,6 +130,9 @@ class DecodeWorkload:
         self.q = torch.randn(ring, self.B, 1, HQ, D, generator=g, device="cuda:0", dtype=torch.float16)
         self.kn = torch.randn(ring, self.B, 1, HKV, D, generator=g, device="cuda:0", dtype=torch.float16)
         self.vn = torch.randn(ring, self.B, 1, HKV, D, generator=g, device="cuda:0", dtype=torch.float16)
+        # the ring's per-step tensors, sliced once (a model hands its q/k/v to attend
+        # without this harness's indexing in between)
+        self.inputs = [(self.q[i], self.kn[i], self.vn[i]) for i in range(ring)]
         self.step_idx = 0
         self.last_ctx = None
 
@@ -162,10 +186,10 @@ class DecodeWorkload:
         return [self.mgr.seqs[s].num_tokens for s in self.ids]
 
     def step(self):
-        i = self.step_idx % self.q.shape[0]
+        q, kn, vn = self.inputs[self.step_idx % len(self.inputs)]
         self.step_idx += 1
         ctx = self.mgr.begin_forward(self.ids, [1] * self.B)
-        out = ctx.attend(0, self.q[i], self.kn[i], self.vn[i], HQ, HKV)
+        out = ctx.attend(0, q, kn, vn, HQ, HKV)
         self.mgr.end_forward(ctx)
         self.last_ctx = ctx
         return out
@@ -419,21 +443,23 @@ def run_decode(args):
             nbytes[j] += x
     kbytes = 0
     churn_s = 0.0
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        if i == churn_at:
-            # re-admission of released sequences is not a decode step: timed apart
-            torch.cuda.synchronize()
-            c0 = time.perf_counter()
-            w.churn()
-            if args.graph:  # the batch changed: capture the step again
-                graph = make_graph(0)
-                step = graph.step
-            torch.cuda.synchronize()
-            churn_s = time.perf_counter() - c0
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0 - churn_s
+    with _GcPaused():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            if i == churn_at:
+                # re-admission of released sequences is not a decode step: timed apart
+                torch.cuda.synchronize()
+                c0 = time.perf_counter()
+                w.churn()
+                if args.graph:  # the batch changed: capture the step again
+                    graph = make_graph(0)
+                    step = graph.step
+                torch.cuda.synchronize()
+                churn_s = time.perf_counter() - c0
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0 - churn_s
     assert w.seq_lens() == [L + args.steps for L in lens_before]
     ms_step = wall / args.steps * 1e3
     total_bytes = sum(nbytes)
@@ -444,11 +470,12 @@ def run_decode(args):
     # events around every decode call on its stream. Timing events add about 10 us
     # of queue overhead per step, so the pass that gives `value` runs without them.
     timed.recording = True
-    for _ in range(args.steps):
-        lens_i = [L + 1 for L in w.seq_lens()]
-        kbytes += decode_call_bytes(lens_i, w.B, sum(math.ceil(L / PS) for L in lens_i))
-        w.step()
-    torch.cuda.synchronize()
+    with _GcPaused():
+        for _ in range(args.steps):
+            lens_i = [L + 1 for L in w.seq_lens()]
+            kbytes += decode_call_bytes(lens_i, w.B, sum(math.ceil(L / PS) for L in lens_i))
+            w.step()
+        torch.cuda.synchronize()
     timed.recording = False
     mean_ms = timed.mean_ms()
     kbytes /= args.steps
@@ -467,28 +494,29 @@ def run_decode(args):
     # planning, which the idle GPU waits for (as step 0's does).
     stream = torch.cuda.current_stream()
     mark = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    torch.cuda.synchronize()
-    prev = mark()
-    prev.record(stream)
     spans = []
     post_churn = -1
-    for i in range(args.steps):
-        if i == churn_at:
-            torch.cuda.synchronize()
-            w.churn()
-            if args.graph:
-                graph = make_graph(0)
-                step = graph.step
-            torch.cuda.synchronize()
-            prev = mark()
-            prev.record(stream)
-            post_churn = i
-        step()
-        e = mark()
-        e.record(stream)
-        spans.append((prev, e))
-        prev = e
-    torch.cuda.synchronize()
+    with _GcPaused():
+        torch.cuda.synchronize()
+        prev = mark()
+        prev.record(stream)
+        for i in range(args.steps):
+            if i == churn_at:
+                torch.cuda.synchronize()
+                w.churn()
+                if args.graph:
+                    graph = make_graph(0)
+                    step = graph.step
+                torch.cuda.synchronize()
+                prev = mark()
+                prev.record(stream)
+                post_churn = i
+            step()
+            e = mark()
+            e.record(stream)
+            spans.append((prev, e))
+            prev = e
+        torch.cuda.synchronize()
     step_ms = [a.elapsed_time(b) for a, b in spans]
     med = float(np.median(step_ms))
     worst = int(np.argmax(step_ms))
@@ -611,10 +639,12 @@ def run_radix(args):
     # decode
     ring = 8
     qd, kd, vd = randn(ring, B, 1, HQ, D), randn(ring, B, 1, HKV, D), randn(ring, B, 1, HKV, D)
+    inputs = [(qd[i], kd[i], vd[i]) for i in range(ring)]  # sliced once, outside the steps
 
     def step(i):
         c = mgr.begin_forward(ids, [1] * B)
-        c.attend(0, qd[i % ring], kd[i % ring], vd[i % ring], HQ, HKV)
+        q, k, v = inputs[i % ring]
+        c.attend(0, q, k, v, HQ, HKV)
         mgr.end_forward(c)
 
     def lens():
@@ -632,18 +662,21 @@ def run_radix(args):
         kv, app, qo, csr = step_bytes(L, B, tp)
         nbytes += kv - (B - 1) * shared_bytes + app + qo + csr
         eff += kv + app + qo + csr
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with _GcPaused():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(i)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     assert lens() == [x + steps for x in L0]
     timed.recording = True
-    for i in range(steps):
-        L = lens()
-        kbytes += decode_call_bytes(L, B, sum(math.ceil(x / PS) for x in L)) - (B - 1) * shared_bytes
-        step(i)
-    torch.cuda.synchronize()
+    with _GcPaused():
+        for i in range(steps):
+            L = lens()
+            kbytes += decode_call_bytes(L, B, sum(math.ceil(x / PS) for x in L)) - (B - 1) * shared_bytes
+            step(i)
+        torch.cuda.synchronize()
     timed.recording = False
     mean_ms = timed.mean_ms()
     kbytes /= steps
