@@ -304,6 +304,30 @@ int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr
                        nslg_stream_t stream);
 
 /*
+ * nslg_paged_prefill on the forward's padded input grid: q and out hold
+ * batch x grid_width rows (the [B, S, Hq, D] grid of a padded forward, S =
+ * grid_width), sequence b's block being rows b * grid_width .. + grid_width - 1.
+ * Its n_b new tokens are rows q_rows[qo_indptr[b]] .. + n_b - 1 of the grid,
+ * contiguous inside that block (the rows the forward's input offsets give,
+ * kv_cache.py:567-573); every other row of the block is written as zeros.
+ * Replaces the pack of the forward's rows into the ragged layout FlashInfer runs
+ * on and the unpack of its output into the padded grid (kv_cache.py:676-691):
+ * the kernel reads and writes the grid rows directly. q_rows: int32[total_q]
+ * (device); a row outside the grid is neither read nor written. Other arguments
+ * as nslg_paged_prefill (workspace unused).
+ */
+int nslg_paged_prefill_grid(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                            const int32_t* q_rows, int32_t grid_width, int64_t total_q,
+                            int32_t max_q, const void* k_pool, const void* v_pool,
+                            int64_t num_pages, int32_t page_size, const int32_t* kv_indptr,
+                            const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                            int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                            int32_t head_dim, float sm_scale, int32_t dtype,
+                            void* out, int64_t out_stride,
+                            void* workspace, size_t workspace_bytes,
+                            nslg_stream_t stream);
+
+/*
  * Device-side plan of one decode step in which every sequence gains one token:
  * the CSR block table, slot mapping and positions of the next step from those of
  * this one. Replaces, for a steady decode batch, the per-step rebuild of the CSR

@@ -25,6 +25,13 @@ constexpr int kRowsF = 16;
 constexpr int kKeysF = 32;
 constexpr int kThreadsF = 256;
 
+// Row of q / out holding new token t (-1: a grid row out of range, not read or written).
+__device__ inline int64_t f32_grid_row(const AttnF32Args& p, int t) {
+  if (!p.q_rows) return t;
+  const int64_t r = p.q_rows[t];
+  return r >= 0 && r < (int64_t)p.batch * p.grid_width ? r : -1;
+}
+
 __device__ inline int kv_len_f32(const AttnF32Args& p, int s) {
   const int np = p.indptr[s + 1] - p.indptr[s];
   if (np <= 0) return 0;
@@ -77,6 +84,13 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
   __shared__ float p_lds[kRowsF][kKeysF + 1];
 
   const int tid = threadIdx.x;
+  const int64_t work = (int64_t)p.row_tiles * p.num_kv_heads;
+  if ((int64_t)blockIdx.x >= work) {  // a padded grid's pad rows: one workgroup per sequence
+    if (p.q_rows && blockIdx.y == 0)
+      zero_pad_rows(p.qo_indptr, p.q_rows, p.grid_width, (int)(blockIdx.x - work), p.out, p.out_stride,
+                    (int64_t)p.num_qo_heads * D, (int64_t)p.batch * p.grid_width);
+    return;
+  }
   const int h = blockIdx.x / p.row_tiles;
   int b = 0, tile = 0;
   if (!locate_f32(p, blockIdx.x - h * p.row_tiles, b, tile)) return;  // uniform over the workgroup
@@ -108,7 +122,8 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
     f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
     if (row < nrows) {
       const int t = row / G, g = row % G;
-      v = *reinterpret_cast<const f32x4*>(p.q + (int64_t)(q0 + t) * p.q_stride + (int64_t)(h * G + g) * D + 4 * c);
+      const int64_t qr = f32_grid_row(p, q0 + t);
+      if (qr >= 0) v = *reinterpret_cast<const f32x4*>(p.q + qr * p.q_stride + (int64_t)(h * G + g) * D + 4 * c);
     }
     *reinterpret_cast<f32x4*>(&q_lds[i * kPitch + 4 * c]) = v;
   }
@@ -202,7 +217,9 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
     return;
   }
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  float* orow = p.out + (int64_t)(q0 + t) * p.out_stride + (int64_t)(h * G + g) * D + rj * kCols;
+  const int64_t orr = f32_grid_row(p, q0 + t);
+  if (orr < 0) return;
+  float* orow = p.out + orr * p.out_stride + (int64_t)(h * G + g) * D + rj * kCols;
 #pragma unroll
   for (int c = 0; c < kCols; c += 4)
     *reinterpret_cast<f32x4*>(orow + c) = f32x4{o[c] * inv, o[c + 1] * inv, o[c + 2] * inv, o[c + 3] * inv};
@@ -270,9 +287,13 @@ int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipSt
     return fail(NSLG_EUNSUPPORTED, "attention_f32: head_dim %d (64, 128 or 256)", head_dim);
   if (a.splits < 1 || a.splits > 64) return fail(NSLG_EINVAL, "attention_f32: %d splits", a.splits);
   if (a.splits > 1 && (!a.part_o || !a.part_ml)) return fail(NSLG_EWORKSPACE, "attention_f32: no workspace");
+  if (a.q_rows && (a.splits != 1 || !a.qo_indptr || a.grid_width < 1))
+    return fail(NSLG_EINVAL, "attention_f32: a padded grid needs ragged rows, a width and one split");
   AttnF32Args p = a;
   p.row_tiles = (int32_t)tiles;
-  const dim3 grid((unsigned)(tiles * a.num_kv_heads), (unsigned)a.splits);
+  const int64_t pad_wgs = a.q_rows ? a.batch : 0;
+  if (tiles * a.num_kv_heads + pad_wgs > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "attention_f32: too many rows");
+  const dim3 grid((unsigned)(tiles * a.num_kv_heads + pad_wgs), (unsigned)a.splits);
   switch (head_dim) {
     case 64: attention_f32_kernel<64><<<grid, kThreadsF, 0, s>>>(p); break;
     case 128: attention_f32_kernel<128><<<grid, kThreadsF, 0, s>>>(p); break;

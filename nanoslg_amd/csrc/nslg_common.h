@@ -117,11 +117,39 @@ __device__ inline void stream_store(V* p, V v) {
   __builtin_nontemporal_store(v, p);
 }
 
+// ---- padded output grids of the prefill entries ----------------------------------
+// One workgroup's share of a padded grid of batch x width rows (row_elems elements
+// each, rows 16-byte aligned): the rows of sequence b's block (rows b * width ..
+// b * width + width - 1) that hold none of its new tokens are set to zero. The
+// sequence's n_b = qo[b + 1] - qo[b] tokens sit at rows q_rows[qo[b]] .. + n_b - 1,
+// contiguous and inside the block (the forward's padded layout).
+template <typename E>
+__device__ inline void zero_pad_rows(const int32_t* qo, const int32_t* q_rows, int width, int b, E* out,
+                                     int64_t out_stride, int64_t row_elems, int64_t grid_rows) {
+  const int q0 = qo[b];
+  const int n = qo[b + 1] - q0;
+  int64_t first = n > 0 ? (int64_t)q_rows[q0] - (int64_t)b * width : 0;
+  first = first < 0 ? 0 : (first > width ? width : first);
+  int64_t last = first + (n > 0 ? n : 0);
+  last = last > width ? width : last;
+  const int64_t vecs = row_elems * (int64_t)sizeof(E) / 16;
+  const int64_t pads = width - (last - first);
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  for (int64_t i = threadIdx.x; i < pads * vecs; i += blockDim.x) {
+    const int64_t pr = i / vecs;
+    const int64_t r = (int64_t)b * width + (pr < first ? pr : pr + (last - first));
+    if (r >= grid_rows) continue;
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(out + r * out_stride) + 16 * (i - pr * vecs)) = z;
+  }
+}
+
 // ---- fp32 attention (attn_f32.hip), shared by the decode and prefill entries ----
 struct AttnF32Args {
   const float* q;
   int64_t q_stride;            // elements between query tokens
   const int32_t* qo_indptr;    // [B+1] new-token offsets; null: one token per sequence
+  const int32_t* q_rows = nullptr;  // null, or row of q / out of each new token (a padded grid)
+  int32_t grid_width = 0;           // rows per sequence of that grid (q_rows set)
   const float* k_pool;         // one layer, [P, ps, Hkv, D]
   const float* v_pool;
   int64_t num_pages;

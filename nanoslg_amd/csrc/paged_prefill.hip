@@ -35,10 +35,7 @@
 namespace nslg {
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerWG = kWaves * kRowsPerWave;  // 256
+constexpr int kRowsPerWG = 256;  // query rows of a workgroup: 16 x kCB per wave
 constexpr int kKeys = 128;
 constexpr int kPageWin = 2048;                     // page ids per LDS window
 constexpr float kRescaleSlack = 8.0f;
@@ -64,7 +61,14 @@ struct PrefillParams {
   int64_t out_stride;
   int32_t row_tiles;  // row-tile slots per KV head (an upper bound over the batch)
   int32_t num_work;   // row_tiles * num_kv_heads
-  int32_t per_xcd;    // ceil(num_work / 8)
+  int32_t per_xcd;    // ceil((num_work + pad_work) / 8)
+  // Grid rows (null: q and out are the ragged rows themselves): ragged row t is row
+  // q_rows[t] of q and out, [batch x grid_width] rows, sequence b's block being rows
+  // b * grid_width .. + grid_width - 1; pad_work workgroups zero the rows of each
+  // block that hold no new token.
+  const int32_t* q_rows;
+  int32_t grid_width;
+  int32_t pad_work;
   int32_t by_round;   // > 0: longest-first rounds of this many tiles per sequence (see below)
 };
 
@@ -72,6 +76,13 @@ template <int N>
 struct Vec {
   typedef unsigned short type __attribute__((ext_vector_type(N)));
 };
+
+// Row of q / out holding ragged row t (-1 for a grid row out of range: not read or written).
+__device__ inline int64_t grid_row(const PrefillParams& p, int t) {
+  if (!p.q_rows) return t;
+  const int64_t r = p.q_rows[t];
+  return r >= 0 && r < (int64_t)p.batch * p.grid_width ? r : -1;
+}
 
 __device__ inline int kv_len_of(const PrefillParams& p, int s) {
   const int np = p.indptr[s + 1] - p.indptr[s];
@@ -143,8 +154,11 @@ __device__ inline bool locate_tile(const PrefillParams& p, int g, int& b, int& t
   return false;
 }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p) {
+template <typename T, int D, int kCB>
+__global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_kernel(PrefillParams p) {
+  constexpr int kRowsPerWave = 16 * kCB;  // kCB column blocks of 16 rows
+  constexpr int kWaves = kRowsPerWG / kRowsPerWave;
+  constexpr int kThreads = 64 * kWaves;
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
   constexpr int kPitch = D + 8;   // K tile row pitch in elements: 16 B reads of 16 lanes span all banks
@@ -162,7 +176,12 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   // w = (i % 8) * per_xcd + i / 8 gives each XCD a contiguous run of row tiles of
   // one KV head, which read the same K/V and so share that XCD's L2.
   const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
-  if (w >= p.num_work) return;
+  if (w >= p.num_work) {
+    if (w < p.num_work + p.pad_work)
+      zero_pad_rows(p.qo_indptr, p.q_rows, p.grid_width, w - p.num_work, p.out, p.out_stride,
+                    (int64_t)p.num_qo_heads * D, (int64_t)p.batch * p.grid_width);
+    return;
+  }
   const int h = w / p.row_tiles;
   int b = 0, tile = 0;
   const int g = w - h * p.row_tiles;
@@ -196,17 +215,18 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   const int gq = lane >> 4;
 
   // ---- per-wave rows: two 16-row column blocks --------------------------------------
-  u16x8 qb[2][kSteps];
-  int row_tok[2];
-  bool row_ok[2];
+  u16x8 qb[kCB][kSteps];
+  int row_tok[kCB];
+  bool row_ok[kCB];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
+  for (int cb = 0; cb < kCB; ++cb) {
     const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
     row_ok[cb] = row < nrows;
     const int t = row_ok[cb] ? row / G : 0;
     row_tok[cb] = start + t;  // absolute position of this row's token
-    if (row_ok[cb]) {
-      const uint16_t* qrow = p.q + (int64_t)(q0 + t) * p.q_stride + (int64_t)(h * G + row % G) * D;
+    const int64_t qr = row_ok[cb] ? grid_row(p, q0 + t) : -1;
+    if (qr >= 0) {
+      const uint16_t* qrow = p.q + qr * p.q_stride + (int64_t)(h * G + row % G) * D;
 #pragma unroll
       for (int s = 0; s < kSteps; ++s) qb[cb][s] = *reinterpret_cast<const u16x8*>(qrow + 32 * s + 8 * gq);
     } else {
@@ -221,22 +241,27 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   // lowest position among the wave's rows: keys below start + first_tok + 1 are visible to all
   const int wave_first_tok = __builtin_amdgcn_readfirstlane(start + (row0_wg + wave * kRowsPerWave) / G);
 
-  float m_run[2] = {-INFINITY, -INFINITY};
+  float m_run[kCB];
   // row sums of P on the MFMA: an all-ones A operand makes every row of the 16x16
   // output tile the column's sum over the block's keys
-  f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  f32x4 lsum[kCB];
   const unsigned short one16 = T::from_f32(1.f);
   const u16x8 ones = u16x8{one16, one16, one16, one16, one16, one16, one16, one16};
   // per column block: raw-score threshold above which the running max must be raised,
   // and the exponent offset -m (0 while m = -inf); both change only with m
-  float thr[2] = {-INFINITY, -INFINITY};
-  float neg_m[2] = {0.f, 0.f};
+  float thr[kCB];
+  float neg_m[kCB];
   const float inv_scale_log2 = 1.f / p.scale_log2;
-  f32x4 o[2][NT];
+  f32x4 o[kCB][NT];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb)
+  for (int cb = 0; cb < kCB; ++cb) {
+    m_run[cb] = -INFINITY;
+    thr[cb] = -INFINITY;
+    neg_m[cb] = 0.f;
+    lsum[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[cb][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // ---- cooperative tile loads: kKeys keys x D for K and V in two halves ------------
   // Each half (kKeys / 2 keys) is fetched into registers and stashed into the next LDS
@@ -244,7 +269,7 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   // are live at a time.
   constexpr int kChunks = D / 8;                             // 16 B chunks per row
   constexpr int kHalf = kKeys / 2;
-  constexpr int kPerThreadH = kHalf * kChunks / kThreads;    // 2 (D=128) or 1 (D=64)
+  constexpr int kPerThreadH = kHalf * kChunks / kThreads;    // D=128: 2 (8 waves) or 4 (4 waves)
   u32x4 kreg[kPerThreadH], vreg[kPerThreadH];
   int win_base = -1;
 
@@ -313,10 +338,10 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
     }
   };
   // S^T of both column blocks: keys kbase + 16t + 4gq + j in lane (r, gq), element j
-  auto qk = [&](const u16x8 (&ka)[2][kSteps], f32x4 (&sacc)[2][2]) {
+  auto qk = [&](const u16x8 (&ka)[2][kSteps], f32x4 (&sacc)[kCB][2]) {
 
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int cb = 0; cb < kCB; ++cb)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         sacc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -345,10 +370,10 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   // rescale: the row's running max m is raised only when some score of the block
   // exceeds it by more than the slack, which each lane checks on its own 8 scores;
   // the cross-lane row max is needed only then
-  auto mask_and_rescale = [&](int kbase, f32x4 (&sacc)[2][2]) {
+  auto mask_and_rescale = [&](int kbase, f32x4 (&sacc)[kCB][2]) {
     const bool full = kbase + 32 <= wave_first_tok + 1 && kbase + 32 <= kv_end;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < kCB; ++cb) {
       if (!full) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -373,9 +398,9 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   };
   // probabilities of both column blocks as 16-bit MFMA B operands (k index 8gq + j
   // stands for the lane's keys: j < 4 the first 16-key tile, j >= 4 the second)
-  auto probs = [&](const f32x4 (&sacc)[2][2], u16x8 (&pb)[2], u16x8 (&pb_lo)[2]) {
+  auto probs = [&](const f32x4 (&sacc)[kCB][2], u16x8 (&pb)[kCB], u16x8 (&pb_lo)[kCB]) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int cb = 0; cb < kCB; ++cb)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float pj = fast_exp2(fmaf(sacc[cb][j >> 2][j & 3], p.scale_log2, neg_m[cb]));
@@ -383,10 +408,10 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
         if constexpr (kSplitP) pb_lo[cb][j] = T::from_f32(pj - T::to_f32(pb[cb][j]));
       }
   };
-  auto pv = [&](const u16x8 (&va)[NT], const u16x8 (&pb)[2], const u16x8 (&pb_lo)[2]) {
+  auto pv = [&](const u16x8 (&va)[NT], const u16x8 (&pb)[kCB], const u16x8 (&pb_lo)[kCB]) {
 
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < kCB; ++cb) {
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         o[cb][n] = T::mma_k32(va[n], pb[cb], o[cb][n]);
@@ -423,7 +448,7 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
       // computed (MFMA) while the probabilities of block kb are (VALU), and P.V of
       // block kb runs while the K operands of block kb + 2 are read from LDS.
       u16x8 ka[2][kSteps];
-      f32x4 sacc[2][2][2];
+      f32x4 sacc[2][kCB][2];
       load_k(stage, 0, ka);
       qk(ka, sacc[0]);
       if (nb > 1) load_k(stage, 1, ka);
@@ -434,7 +459,7 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
         const int kbase = key0 + 32 * kb;
         mask_and_rescale(kbase, sacc[cur]);
         u16x8 va[NT];
-        u16x8 pb[2], pb_lo[2];
+        u16x8 pb[kCB], pb_lo[kCB];
         load_v(stage, kb, va);
         if (kb + 1 < nb) qk(ka, sacc[cur ^ 1]);
         probs(sacc[cur], pb, pb_lo);
@@ -468,13 +493,15 @@ __global__ void __launch_bounds__(kThreads) paged_prefill_kernel(PrefillParams p
   }
   // ---- epilogue: normalise and store rows ----------------------------------------
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
+  for (int cb = 0; cb < kCB; ++cb) {
     const float l_tot = lsum[cb][0];
     if (!row_ok[cb]) continue;
     const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
     const int t = row / G;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + t) * p.out_stride + (int64_t)(h * G + row % G) * D;
+    const int64_t orr = grid_row(p, q0 + t);
+    if (orr < 0) continue;
+    uint16_t* orow = p.out + orr * p.out_stride + (int64_t)(h * G + row % G) * D;
     // lane holds O[row][16n + 4gq + i] in o[cb][n][i]
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -495,7 +522,10 @@ inline int64_t grid_tiles(int64_t total_q, int32_t batch, int group) {
 
 template <typename T, int D>
 int launch_prefill(const PrefillParams& p, int64_t tiles, hipStream_t s) {
-  paged_prefill_kernel<T, D><<<dim3((unsigned)(8 * p.per_xcd)), kThreads, 0, s>>>(p);
+  // two column blocks (32 rows) per wave, 8 waves: measured faster than four per
+  // wave at one wave per SIMD (chunk 3584..4095 of 8 x 4096: 276 vs 338 us)
+  constexpr int kCB = 2;
+  paged_prefill_kernel<T, D, kCB><<<dim3((unsigned)(8 * p.per_xcd)), 64 * (kRowsPerWG / (16 * kCB)), 0, s>>>(p);
   return check_launch("paged_prefill");
 }
 
@@ -515,22 +545,24 @@ extern "C" size_t nslg_paged_prefill_workspace_size(int32_t batch, int32_t num_q
   return 256;  // the prefill kernel keeps all state on chip
 }
 
-extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr,
-                                  int64_t total_q, int32_t max_q, const void* k_pool,
-                                  const void* v_pool, int64_t num_pages, int32_t page_size,
-                                  const int32_t* kv_indptr, const int32_t* kv_indices,
-                                  const int32_t* kv_last_page_len, int32_t batch,
-                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                                  float sm_scale, int32_t dtype, void* out, int64_t out_stride,
-                                  void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
+namespace {
+
+int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, const int32_t* q_rows,
+                 int32_t grid_width, int64_t total_q, int32_t max_q, const void* k_pool, const void* v_pool,
+                 int64_t num_pages, int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
+                 const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                 int32_t head_dim, float sm_scale, int32_t dtype, void* out, int64_t out_stride,
+                 nslg_stream_t stream) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_q < 0)
     return fail(NSLG_EINVAL, "paged_prefill: bad sizes");
+  if (q_rows && (grid_width < 1 || (int64_t)batch * grid_width > 0x7fffffff || total_q > (int64_t)batch * grid_width))
+    return fail(NSLG_EINVAL, "paged_prefill_grid: grid of %d x %d rows for %lld tokens", batch, grid_width,
+                (long long)total_q);
   if (!(sm_scale > 0.f) || !(sm_scale < INFINITY))
     return fail(NSLG_EINVAL, "paged_prefill: sm_scale must be positive and finite");
-  if (batch == 0 || total_q == 0) return NSLG_OK;
+  if (batch == 0) return NSLG_OK;
+  if (total_q == 0 && !q_rows) return NSLG_OK;  // (a grid without tokens still has its pad rows zeroed)
   if (!q || !qo_indptr || !k_pool || !v_pool || !kv_indptr || !kv_indices || !kv_last_page_len || !out)
     return fail(NSLG_EINVAL, "paged_prefill: null pointer");
   if (num_qo_heads % num_kv_heads != 0)
@@ -560,6 +592,8 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
     a.out = (float*)out;
     a.out_stride = out_stride;
     a.row_tiles = 0;
+    a.q_rows = q_rows;
+    a.grid_width = grid_width;
     a.splits = 1;  // the query rows fill the GPU
     a.part_o = nullptr;
     a.part_ml = nullptr;
@@ -611,8 +645,46 @@ extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t
   if (slots * num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
   p.row_tiles = (int32_t)slots;
   p.num_work = (int32_t)(slots * num_kv_heads);
-  p.per_xcd = (p.num_work + 7) / 8;
+  p.q_rows = q_rows;
+  p.grid_width = grid_width;
+  p.pad_work = q_rows ? batch : 0;
+  if ((int64_t)p.num_work + p.pad_work > 0x7fffffff - 8) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
+  p.per_xcd = (p.num_work + p.pad_work + 7) / 8;
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) return head_dim == 64 ? launch_prefill<F16, 64>(p, tiles, s) : launch_prefill<F16, 128>(p, tiles, s);
   return head_dim == 64 ? launch_prefill<BF16, 64>(p, tiles, s) : launch_prefill<BF16, 128>(p, tiles, s);
+}
+
+}  // namespace
+
+extern "C" int nslg_paged_prefill(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                                  int64_t total_q, int32_t max_q, const void* k_pool,
+                                  const void* v_pool, int64_t num_pages, int32_t page_size,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices,
+                                  const int32_t* kv_last_page_len, int32_t batch,
+                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  float sm_scale, int32_t dtype, void* out, int64_t out_stride,
+                                  void* workspace, size_t workspace_bytes, nslg_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return prefill_impl(q, q_stride, qo_indptr, nullptr, 0, total_q, max_q, k_pool, v_pool, num_pages, page_size,
+                      kv_indptr, kv_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                      dtype, out, out_stride, stream);
+}
+
+extern "C" int nslg_paged_prefill_grid(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                                       const int32_t* q_rows, int32_t grid_width, int64_t total_q,
+                                       int32_t max_q, const void* k_pool, const void* v_pool,
+                                       int64_t num_pages, int32_t page_size, const int32_t* kv_indptr,
+                                       const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                       int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                       int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                       nslg_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (batch > 0 && !q_rows) return fail(NSLG_EINVAL, "paged_prefill_grid: null q_rows");
+  return prefill_impl(q, q_stride, qo_indptr, q_rows, grid_width, total_q, max_q, k_pool, v_pool, num_pages,
+                      page_size, kv_indptr, kv_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads,
+                      head_dim, sm_scale, dtype, out, out_stride, stream);
 }

@@ -718,9 +718,19 @@ def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q:
                   k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
                   kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                   sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                  workspace: Optional[Workspace] = None) -> torch.Tensor:
-    """Causal (bottom-right) prefill attention. q: ragged [T, Hq, D]; returns [T, Hq, D]."""
+                  workspace: Optional[Workspace] = None, q_rows: Optional[torch.Tensor] = None,
+                  grid_width: int = 0) -> torch.Tensor:
+    """Causal (bottom-right) prefill attention. q: ragged [T, Hq, D]; returns [T, Hq, D].
+    With q_rows (int32 [total_q] on the device) q and the result are the forward's
+    padded grid of B * grid_width rows instead (nslg_paged_prefill_grid): ragged row t
+    is grid row q_rows[t], sequence b's rows contiguous in its block of grid_width
+    rows, and the rows holding no token come out as zeros."""
     _require_gpu(q, qo_indptr, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
+    if q_rows is not None:
+        _require_gpu(q, q_rows)
+        _i32(q_rows, "q_rows")
+        if q_rows.numel() < total_q or grid_width < 1 or q.shape[0] != (kv_indptr.numel() - 1) * grid_width:
+            raise ValueError("paged_prefill: a grid of B x grid_width rows of q and one q_rows entry per token")
     for t, n in ((qo_indptr, "qo_indptr"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
                  (kv_last_page_len, "kv_last_page_len")):
         _i32(t, n)
@@ -735,10 +745,21 @@ def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q:
         raise ValueError("paged_prefill: qo_indptr must have B+1 entries and q at least total_q rows")
     if out is None:
         out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
+    elif q_rows is not None and (out.shape[0] != T or out.dim() != 3 or out.shape[1:] != (Hq, D)
+                                 or out.stride(2) != 1 or out.stride(1) != D or out.dtype != q.dtype):
+        raise ValueError("paged_prefill: out must be the grid's [B * grid_width, Hq, D] rows")
     lib = _lib.load()
     need = int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q)))
     ws = (workspace or Workspace(q.device)).get(need)
     scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    if q_rows is not None:
+        rc = lib.nslg_paged_prefill_grid(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), q_rows.data_ptr(),
+                                         int(grid_width), int(total_q), int(max_q), k_layer.data_ptr(),
+                                         v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                         kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
+                                         out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+        _lib.check(rc, "nslg_paged_prefill_grid")
+        return out
     rc = lib.nslg_paged_prefill(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), int(total_q), int(max_q),
                                 k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
                                 kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale,

@@ -415,6 +415,19 @@ class _ForwardPlan:
             self._slot_by_S[S] = s
         return s
 
+    def rows_for(self, S: int) -> torch.Tensor:
+        """Rows of the [B, S] input grid holding the forward's tokens, in ragged order
+        (q_rows is for the plan's own width iw: sequence b's rows move by b * (S - iw))."""
+        if S == self.iw:
+            return self.q_rows
+        cache = self.__dict__.setdefault("_rows_by_S", {})
+        r = cache.get(S)
+        if r is None:
+            if S < self.iw:
+                raise ValueError(f"the input grid has {S} columns; this forward's tokens need {self.iw}")
+            r = cache[S] = self.q_rows + torch.div(self.q_rows, self.iw, rounding_mode="floor") * (S - self.iw)
+        return r
+
     def pos_for(self, S: int) -> torch.Tensor:
         """int32 positions of the [B, S] input grid, flattened (zeros on padding)."""
         if S == self.iw:
@@ -1102,17 +1115,15 @@ class PagedCacheContext(CacheContext):
         kern = cache.kernels
         B, S = q.shape[0], q.shape[1]
         Hq, D = q.shape[2], q.shape[3]
-        if self._uniform_rows and S == self._iw:
-            q_rag = q.reshape(B * S, Hq, D)
-        else:
-            q_rag = q.reshape(B * S, Hq, D).index_select(0, plan.q_rows.long())
-        o_rag = kern.paged_prefill(q_rag, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+        q_grid = q.reshape(B * S, Hq, D)
+        if self._uniform_rows and S == self._iw:  # every grid row is a token: the ragged rows themselves
+            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
                                    plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace)
-        if self._uniform_rows and S == self._iw:
-            return o_rag.reshape(B, S, Hq * D)
-        out = q.new_zeros(B * S, Hq * D)
-        out.index_copy_(0, plan.q_rows.long(), o_rag.reshape(-1, Hq * D))
-        return out.view(B, S, Hq * D)
+        else:  # padded or ragged: the kernel reads and writes the grid rows (pad rows zero)
+            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace,
+                                   q_rows=plan.rows_for(S), grid_width=S)
+        return o.view(B, S, Hq * D)
 
     # ---- introspection used by tests and the bench -------------------------------------
     @property
@@ -1639,17 +1650,15 @@ class ContiguousCacheContext(CacheContext):
                                     plan.total_pages, workspace=cache.workspace)
             return out.reshape(B, 1, -1)
         Hq, D = q.shape[2], q.shape[3]
-        if self._uniform_rows and S == self._iw:
-            q_rag = q.reshape(B * S, Hq, D)
-        else:
-            q_rag = q.reshape(B * S, Hq, D).index_select(0, plan.q_rows.long())
-        o_rag = kern.paged_prefill(q_rag, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+        q_grid = q.reshape(B * S, Hq, D)
+        if self._uniform_rows and S == self._iw:  # every grid row is a token: the ragged rows themselves
+            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
                                    plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace)
-        if self._uniform_rows and S == self._iw:
-            return o_rag.reshape(B, S, Hq * D)
-        out = q.new_zeros(B * S, Hq * D)
-        out.index_copy_(0, plan.q_rows.long(), o_rag.reshape(-1, Hq * D))
-        return out.view(B, S, Hq * D)
+        else:  # padded or ragged: the kernel reads and writes the grid rows (pad rows zero)
+            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace,
+                                   q_rows=plan.rows_for(S), grid_width=S)
+        return o.view(B, S, Hq * D)
 
 
 class ContiguousKVCache(KVCacheManager):

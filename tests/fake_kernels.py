@@ -81,10 +81,25 @@ def paged_decode(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, t
 
 
 def paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,
-                  sm_scale=None, out=None, workspace=None):
+                  sm_scale=None, out=None, workspace=None, q_rows=None, grid_width=0):
     CALLS.append(("paged_prefill", int(total_q)))
     qo = qo_indptr.tolist()
     B = len(qo) - 1
+    if q_rows is not None:  # the padded grid: rows of each sequence contiguous in its block, pads zero
+        rows = q_rows[:int(total_q)].long()
+        assert q.shape[0] == B * grid_width
+        for b in range(B):
+            r = rows[qo[b]:qo[b + 1]].tolist()
+            assert r == list(range(r[0], r[0] + len(r))) if r else True
+            assert all(b * grid_width <= x < (b + 1) * grid_width for x in r)
+        res = paged_prefill(q.index_select(0, rows), qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr,
+                            kv_indices, kv_last_page_len, sm_scale)
+        grid = q.new_zeros(q.shape)
+        grid.index_copy_(0, rows, res)
+        if out is not None:
+            out.copy_(grid)
+            return out
+        return grid
     qs = [q[qo[b]:qo[b + 1]] for b in range(B)]
     outs = _attend(qs, [qo[b + 1] - qo[b] for b in range(B)], k_layer, v_layer, kv_indptr, kv_indices,
                    kv_last_page_len, sm_scale)

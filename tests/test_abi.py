@@ -104,6 +104,19 @@ def test_decode_append_argument_checks():
     assert rc == -1 and "k_new" in _lib.last_error()
 
 
+def test_prefill_grid_argument_checks():
+    """nslg_paged_prefill_grid: the grid rows map and the grid's shape are checked on
+    the host before any launch."""
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    tail = (256, 256, 100, 16, 256, 256, 256, 2, 32, 8, 128, 0.1, 0, 256, 4096, None, 0, None)
+    assert lib.nslg_paged_prefill_grid(256, 4096, 256, None, 8, 10, 8, *tail) == -1
+    assert "q_rows" in _lib.last_error()
+    assert lib.nslg_paged_prefill_grid(256, 4096, 256, 256, 0, 10, 8, *tail) == -1  # no width
+    assert lib.nslg_paged_prefill_grid(256, 4096, 256, 256, 4, 10, 8, *tail) == -1  # 10 tokens, 2 x 4 rows
+    assert "grid" in _lib.last_error()
+
+
 def test_rope_append_argument_checks():
     from nanoslg_amd import _lib
     lib = _lib.load()

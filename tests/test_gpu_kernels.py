@@ -301,6 +301,46 @@ def test_prefill_sequence_without_new_tokens():
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64), (torch.float32, 128),
+                                     (torch.float32, 256)])
+def test_prefill_grid_rows_bit_exact(dtype, D):
+    """nslg_paged_prefill_grid on a padded [B, S] grid (left and right padding, a
+    sequence without new tokens, a full row) against nslg_paged_prefill on the ragged
+    rows gathered from it: the token rows bit-identical, every pad row zero (the output
+    starts as NaN), and the ragged result against the oracle."""
+    _log(f"prefill grid rows {dtype} D={D}")
+    K = _k()
+    ps, Hq, Hkv = 16, 32, 8
+    lens, news, offs = [300, 77, 40, 129, 9], [64, 20, 0, 129, 9], [3, 0, 5, 0, 100]
+    S = max(o + n for o, n in zip(offs, news))
+    B = len(lens)
+    g = torch.Generator().manual_seed(D + len(lens))
+    P = sum(math.ceil(L / ps) for L in lens) + 5
+    k = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    v = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    tables, (indptr, indices, lpl) = _csr_random(lens, ps, P, D)
+    qo = np.zeros(B + 1, np.int32)
+    np.cumsum(news, out=qo[1:])
+    rows = np.concatenate([b * S + o + np.arange(n) for b, (o, n) in enumerate(zip(offs, news))]).astype(np.int32)
+    grid = torch.randn(B * S, Hq, D, generator=g).to(dtype).to(DEV)
+    ip, ix, lp, qo_d, rows_d = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl, qo, rows))
+    T = int(qo[-1])
+    out = torch.full((B * S, Hq, D), float("nan"), dtype=dtype, device=DEV)
+    K.paged_prefill(grid, qo_d, T, max(news), k, v, ip, ix, lp, out=out, q_rows=rows_d, grid_width=S)
+    rag = K.paged_prefill(grid.index_select(0, rows_d.long()).contiguous(), qo_d, T, max(news), k, v, ip, ix, lp)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out[rows_d.long()]), _bits(rag))
+    pad = torch.ones(B * S, dtype=torch.bool)
+    pad[torch.from_numpy(rows).long()] = False
+    assert torch.count_nonzero(out[pad.to(DEV)]) == 0
+    q_list = [grid[torch.from_numpy(rows[qo[b]:qo[b + 1]]).long().to(DEV)].cpu() for b in range(B)]
+    ref = O.paged_attention_ref(q_list, k.cpu().view(-1, Hkv, D), v.cpu().view(-1, Hkv, D), ps, indptr, indices,
+                                lpl, news)
+    ref = torch.cat([r for r in ref if r.shape[0]], 0)
+    tol = F32_TOL if dtype == torch.float32 else dict(atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(rag.cpu().float(), ref, **tol)
+
+
 # ------------------------------------------------------------------ fp32 pools
 
 F32_TOL = dict(atol=2e-5, rtol=1e-4)  # fp32 kernel against fp32 SDPA: summation-order differences only
