@@ -524,6 +524,16 @@ def run_decode(args):
     _log(f"step wall: median {med:.3f} ms, max {step_ms[worst]:.3f} ms (step {worst}), "
          f"max/median {step_ms[worst] / med:.2f}"
          + (f", step after the churn {step_ms[post_churn]:.3f} ms" if post_churn >= 0 else ""))
+    # Kernel time of the last step's decode call alone (no host work or timing events
+    # in it): the call captured 10 times in a HIP graph, replayed with events around
+    # the replays. It writes the same new rows again, so the pool does not change.
+    call_us = None
+    ctx = w.last_ctx
+    launch = getattr(ctx, "_decode_launch", None) if ctx is not None else None
+    if launch is not None and not args.graph:
+        q, kn, vn = w.inputs[(w.step_idx - 1) % len(w.inputs)]
+        call_us = _graph_time_us(torch, torch.device("cuda:0"), lambda: launch(0, q, kn, vn))
+        _log(f"decode call, kernel time (graph-timed): {call_us} us")
     res = {
         "metric": "paged decode attn+append: achieved HBM GB/s (% of peak) and decode tok/s/layer",
         "value": round(value, 2),
@@ -556,6 +566,7 @@ def run_decode(args):
             "avg_launch_us": round(mean_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": int(kbytes),
         },
+        "decode_call_kernel_us": call_us,
         "churn_ms": round(churn_s * 1e3, 2),
         "step_wall_ms": {"median": round(med, 4), "max": round(step_ms[worst], 4), "max_step": worst,
                          "max_over_median": round(step_ms[worst] / med, 3),

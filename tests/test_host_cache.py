@@ -395,12 +395,14 @@ def test_device_decode_plan_matches_host_plan(scalar_batch, monkeypatch):
     each such plan equals, entry for entry, the plan the host builds for the same
     step, and pages, refcounts and tokens_used stay identical. Batch changes, prefill
     and shared pages fall back to the host plan. Both host checks of a step run: the
-    per-sequence one of small batches and the vectorised one."""
+    per-sequence one of small batches (begin_forward's one-pass steady step) and the
+    vectorised one."""
     monkeypatch.setattr(KC.PagedKVCache, "SCALAR_PLAN_BATCH", scalar_batch)
     g = torch.Generator().manual_seed(11)
     fast, _ = make(ps=4, pages=96, prefix=False)
     slow, _ = make(ps=4, pages=96, prefix=False)
     slow._advance_decode_plan = lambda *a: None
+    slow._begin_steady_decode = lambda *a: None
     ids = ["a", "b", "c", "d"]
     for m in (fast, slow):
         for s, n in zip(ids, [5, 8, 1, 3]):
@@ -444,6 +446,46 @@ def test_device_decode_plan_matches_host_plan(scalar_batch, monkeypatch):
         m.pool.add_ref(int(m.seqs["c"].bt[m.seqs["c"].n_pages - 1]))
     step([1, 1, 1], ["a", "c", "d"], expect_fast=False)
     step([1, 1, 1], ["a", "c", "d"], expect_fast=True)
+    # pages taken ahead by extend_sequence (their zeroing deferred): the host plans
+    for m in (fast, slow):
+        m.extend_sequence("a", 9)
+    step([1, 1, 1], ["a", "c", "d"], expect_fast=False)
+    for _ in range(10):
+        step([1, 1, 1], ["a", "c", "d"])
+
+
+def test_steady_decode_step_out_of_pages_matches_oracle():
+    """A steady decode step that needs more pages than are free leaves the one-pass
+    path untouched and fails in the general one, with the reference's error, at the
+    same step as the oracle, both caches unchanged by the failed step."""
+    g = torch.Generator().manual_seed(3)
+    mgr, ref = make(ps=4, pages=12, prefix=False)
+    ids = ["a", "b", "c"]
+    for m in (mgr, ref):
+        for s, n in zip(ids, [4, 7, 11]):
+            m.allocate_sequence(s, num_tokens=n)
+    forward_both(mgr, ref, ids, [4, 7, 11], [0, 0, 0], g)
+    for step in range(40):
+        errs = []
+        for m in (mgr, ref):
+            try:
+                c = m.begin_forward(ids, [1, 1, 1])
+            except RuntimeError as e:
+                errs.append(str(e))
+                continue
+            m.end_forward(c) if m is ref else None
+            if m is mgr:
+                q = torch.randn(3, 1, HQ, D, generator=g)
+                kv = torch.randn(3, 1, HKV, D, generator=g)
+                c.attend(0, q, kv, kv, HQ, HKV)
+                m.end_forward(c)
+        if errs:
+            assert len(errs) == 2 and errs[0] == errs[1] and errs[0].startswith("KV OOM"), errs
+            break
+        assert mgr.pool.num_free == ref.pool.num_free
+    else:
+        raise AssertionError("the pool never ran out")
+    assert [mgr.seqs[s].num_tokens for s in ids] == [ref.seqs[s].num_tokens for s in ids]
 
 
 @pytest.mark.parametrize("backend", ["paged", "contiguous"])
