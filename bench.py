@@ -58,16 +58,23 @@ def _parse():
     return ap.parse_args()
 
 
+def _settle_gc():
+    """Before the warmup steps: one collection, then every object alive so far moved
+    out of the collector's generations (gc.freeze, as serving processes do after
+    start-up), so later collections only walk the few objects the steps create."""
+    import gc
+    gc.collect()
+    gc.freeze()
+
+
 class _GcPaused:
     """A timed region with Python's cyclic garbage collector paused, as timeit runs
     its loops: a collection walks every object of the process (tens of milliseconds
-    with torch loaded) and would land in whichever step happened to trigger it. A
-    collection runs before the region; reference counting frees the steps' objects
-    as usual inside it."""
+    with torch loaded) and would land in whichever step happened to trigger it.
+    Reference counting frees the steps' objects as usual inside it."""
 
     def __enter__(self):
         import gc
-        gc.collect()
         self.was_enabled = gc.isenabled()
         gc.disable()
         return self
@@ -415,6 +422,7 @@ def run_decode(args):
     from nanoslg_amd import kernels
     timed = EventTimedKernels(kernels)
     w.mgr.kernels = timed
+    _settle_gc()
     for _ in range(args.warmup):
         w.step()
     torch.cuda.synchronize()
@@ -524,13 +532,14 @@ def run_decode(args):
     _log(f"step wall: median {med:.3f} ms, max {step_ms[worst]:.3f} ms (step {worst}), "
          f"max/median {step_ms[worst] / med:.2f}"
          + (f", step after the churn {step_ms[post_churn]:.3f} ms" if post_churn >= 0 else ""))
-    # Kernel time of the last step's decode call alone (no host work or timing events
-    # in it): the call captured 10 times in a HIP graph, replayed with events around
-    # the replays. It writes the same new rows again, so the pool does not change.
+    # Small batches: kernel time of the last step's decode call alone (its events
+    # above also hold launch gaps): the call captured 10 times in a HIP graph, replayed
+    # with events around the replays. It writes the same new rows again, so the pool
+    # does not change.
     call_us = None
     ctx = w.last_ctx
     launch = getattr(ctx, "_decode_launch", None) if ctx is not None else None
-    if launch is not None and not args.graph:
+    if launch is not None and not args.graph and w.B <= 16:
         q, kn, vn = w.inputs[(w.step_idx - 1) % len(w.inputs)]
         call_us = _graph_time_us(torch, torch.device("cuda:0"), lambda: launch(0, q, kn, vn))
         _log(f"decode call, kernel time (graph-timed): {call_us} us")
@@ -661,6 +670,7 @@ def run_radix(args):
     def lens():
         return [mgr.seqs[s].num_tokens + 1 for s in ids]
 
+    _settle_gc()
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
