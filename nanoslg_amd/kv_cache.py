@@ -36,6 +36,16 @@ import torch
 _BACKENDS = ("paged", "contiguous")
 
 
+def _check_head_dim(cfg: "KVCacheConfig", kernels) -> None:
+    """A cache is only built for a (dtype, head_dim) every kernel it uses supports,
+    so an unsupported model fails at construction rather than at its first prefill."""
+    dims = getattr(kernels, "HEAD_DIMS", None)
+    dev = torch.device(cfg.device) if cfg.device is not None else None
+    if dims is not None and dev is not None and dev.type == "cuda" and cfg.head_dim not in dims.get(cfg.dtype, ()):
+        raise ValueError(f"KV cache: head_dim {cfg.head_dim} is not supported for {cfg.dtype} "
+                         f"(supported: {dims.get(cfg.dtype, ())})")
+
+
 def _default_kernels():
     from . import kernels
     return kernels
@@ -1137,6 +1147,7 @@ class PagedKVCache(KVCacheManager):
     def __init__(self, cfg: KVCacheConfig, kernels=None):
         self.cfg = cfg
         self.kernels = kernels or _default_kernels()
+        _check_head_dim(cfg, self.kernels)
         self.pool = PagePool(cfg, self.kernels)
         self.tree = (RadixTree(cfg.page_size, self.pool, share_partial=cfg.share_partial_pages)
                      if cfg.enable_prefix_caching else None)
@@ -1668,6 +1679,7 @@ class ContiguousKVCache(KVCacheManager):
     def __init__(self, cfg: KVCacheConfig, kernels=None):
         self.cfg = cfg
         self.kernels = kernels or _default_kernels()
+        _check_head_dim(cfg, self.kernels)
         self.device = torch.device(cfg.device) if cfg.device is not None else torch.device("cpu")
         shape = (cfg.num_layers, cfg.max_batch_size, cfg.max_seq_len, cfg.num_kv_heads, cfg.head_dim)
         self.k = torch.zeros(shape, dtype=cfg.dtype, device=self.device)

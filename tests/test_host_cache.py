@@ -378,6 +378,22 @@ def test_config_and_factory():
     assert isinstance(mgr, KC.PagedKVCache) and mgr.pool.k.shape == (2, 256, 8, 2, 8)
 
 
+def test_unsupported_head_dim_is_rejected_at_construction():
+    """A GPU cache whose dtype and head_dim some kernel it uses does not support (the
+    16-bit prefill: head_dim 64 or 128) is refused when it is built, not at its first
+    prefill; fp32 pools take 256."""
+    from nanoslg_amd import kernels as K
+    for dt, hd, ok in ((torch.float16, 256, False), (torch.bfloat16, 96, False), (torch.float16, 128, True),
+                       (torch.float32, 256, True), (torch.bfloat16, 64, True)):
+        cfg = KC.KVCacheConfig(1, 2, 4, hd, page_size=16, max_pages=8, dtype=dt, device=None)
+        cfg.device = torch.device("cuda", 0)  # the check only; nothing is allocated here
+        if ok:
+            KC._check_head_dim(cfg, K)
+        else:
+            with pytest.raises(ValueError, match="head_dim"):
+                KC._check_head_dim(cfg, K)
+
+
 def test_stats_and_reset():
     mgr, _ = make(ps=4, pages=16, prefix=True)
     mgr.allocate_sequence("a", token_ids=list(range(9)))
