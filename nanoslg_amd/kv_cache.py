@@ -534,6 +534,27 @@ class PagePool:
                     self._is_free[pid] = True
                     self._free.append(pid)
 
+    def release_many(self, pids) -> None:
+        """release(p) for each p of pids, in order (the same refcounts, tokens_used and
+        free-list order), vectorised when the ids are distinct (a block table's are)."""
+        ids = np.asarray(pids, np.int64)
+        ids = ids[ids > 0]
+        if ids.size == 0:
+            return
+        if np.unique(ids).size != ids.size:
+            for p in ids.tolist():
+                self.release(p)
+            return
+        with self._lock:
+            rc = self.ref_count[ids] - 1
+            gone = rc <= 0
+            self.ref_count[ids] = np.where(gone, 0, rc)
+            freed = ids[gone]
+            self.tokens_used[freed] = 0
+            freed = freed[~self._is_free[freed]]
+            self._is_free[freed] = True
+            self._free.extend(freed.tolist())
+
     def add_ref(self, pid: int) -> None:
         with self._lock:
             self.ref_count[pid] += 1
@@ -1534,8 +1555,7 @@ class PagedKVCache(KVCacheManager):
                     self.tree.insert(st.token_ids[:nf * ps], st.block_table[:nf])
             if st.prefix_len:
                 self.tree.dec_refs(st.token_ids[:st.prefix_len])
-        for p in st.bt[:st.n_pages].tolist():
-            self.pool.release(p)
+        self.pool.release_many(st.bt[:st.n_pages])
         self._tables.release(st)
         del self.seqs[seq_id]
 

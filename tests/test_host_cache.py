@@ -378,6 +378,29 @@ def test_config_and_factory():
     assert isinstance(mgr, KC.PagedKVCache) and mgr.pool.k.shape == (2, 256, 8, 2, 8)
 
 
+def test_release_many_equals_one_release_per_page():
+    """PagePool.release_many (used when a sequence is released) leaves the same
+    refcounts, tokens_used, free flags and free-list order as release() page by page,
+    with shared pages, page 0 and repeated ids in the list."""
+    rng = np.random.default_rng(4)
+    for trial in range(20):
+        pools = [make(ps=4, pages=64, prefix=False)[0].pool for _ in range(2)]
+        pages = pools[0].alloc(40, zero=False)
+        assert pools[1].alloc(40, zero=False) == pages
+        for pool in pools:
+            for p in pages[::3]:
+                pool.add_ref(p)
+            pool.tokens_used[pages] = np.arange(40) % 4 + 1
+        sel = rng.choice(pages, size=int(rng.integers(1, 40)), replace=bool(trial % 2)).tolist() + [0]
+        rng.shuffle(sel)
+        for p in sel:
+            pools[0].release(p)
+        pools[1].release_many(sel)
+        a, b = pools
+        assert np.array_equal(a.ref_count, b.ref_count) and np.array_equal(a.tokens_used, b.tokens_used)
+        assert np.array_equal(a._is_free, b._is_free) and a._free == b._free
+
+
 def test_unsupported_head_dim_is_rejected_at_construction():
     """A GPU cache whose dtype and head_dim some kernel it uses does not support (the
     16-bit prefill: head_dim 64 or 128) is refused when it is built, not at its first
