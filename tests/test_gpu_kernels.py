@@ -725,7 +725,7 @@ def test_decode_plan_step_zeroes_opened_pages(L, ps, Hkv, D, B):
     assert torch.equal(v_pool, v_exp)
 
 
-def _grouped_case(Hq, Hkv, ps, dtype, seed, group_sizes, prefix_pages, n_alone, own_max=300):
+def _grouped_case(Hq, Hkv, ps, dtype, seed, group_sizes, prefix_pages, n_alone, own_max=300, D=128):
     """A batch in which groups of sequences share their first pages (same page ids),
     plus sequences of their own, in shuffled batch order. Returns the grouped and the
     plain decode outputs and the oracle's."""
@@ -750,9 +750,9 @@ def _grouped_case(Hq, Hkv, ps, dtype, seed, group_sizes, prefix_pages, n_alone, 
         tables[b] = [next(next_page) for _ in range(math.ceil(lens[b] / ps))]
     P = 20000
     g = torch.Generator().manual_seed(seed)
-    k = torch.randn(P, ps, Hkv, 128, generator=g).to(dtype)
-    v = torch.randn(P, ps, Hkv, 128, generator=g).to(dtype)
-    q = torch.randn(B, Hq, 128, generator=g).to(dtype)
+    k = torch.randn(P, ps, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(P, ps, Hkv, D, generator=g).to(dtype)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype)
     indptr, indices, lpl = O.plan_csr(tables, lens, ps)
     args = (q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV),
             torch.from_numpy(lpl).to(DEV), int(indptr[-1]))
@@ -760,25 +760,28 @@ def _grouped_case(Hq, Hkv, ps, dtype, seed, group_sizes, prefix_pages, n_alone, 
     out_g = K.paged_decode(*args, groups=groups)
     out_p = K.paged_decode(*args)
     torch.cuda.synchronize()
-    ref = O.paged_attention_ref([q[b:b + 1] for b in range(B)], k.view(-1, Hkv, 128), v.view(-1, Hkv, 128), ps,
+    ref = O.paged_attention_ref([q[b:b + 1] for b in range(B)], k.view(-1, Hkv, D), v.view(-1, Hkv, D), ps,
                                 indptr, indices, lpl, [1] * B)
     ref = torch.stack([r[0] for r in ref])
     return out_g.cpu().float(), out_p.cpu().float(), ref
 
 
-@pytest.mark.parametrize("Hq,Hkv,ps,dtype,sizes,prefix", [
-    (32, 8, 16, torch.float16, [4, 4, 3], [127, 10, 1]),
-    (8, 8, 16, torch.float16, [16, 2], [40, 3]),
-    (64, 8, 16, torch.bfloat16, [2, 2], [64, 5]),
-    (32, 8, 8, torch.float16, [4, 2], [50, 7]),
-    (16, 1, 16, torch.float16, [1, 1], [20, 2]),
+@pytest.mark.parametrize("Hq,Hkv,ps,dtype,sizes,prefix,D", [
+    (32, 8, 16, torch.float16, [4, 4, 3], [127, 10, 1], 128),
+    (32, 8, 16, torch.bfloat16, [4, 2], [12, 3], 64),
+    (32, 8, 16, torch.float16, [4, 3], [20, 2], 256),
+    (16, 8, 16, torch.bfloat16, [8, 5], [30, 4], 128),   # G = 2: 8 members
+    (8, 8, 16, torch.float16, [16, 2], [40, 3], 128),
+    (64, 8, 16, torch.bfloat16, [2, 2], [64, 5], 128),
+    (32, 8, 8, torch.float16, [4, 2], [50, 7], 128),
+    (16, 1, 16, torch.float16, [1, 1], [20, 2], 128),
 ])
-def test_decode_grouped_prefix(Hq, Hkv, ps, dtype, sizes, prefix):
+def test_decode_grouped_prefix(Hq, Hkv, ps, dtype, sizes, prefix, D):
     """Groups of sequences sharing their first pages: the grouped decode (prefix read
     once per group, members in the MFMA columns) against the oracle, and against the
     plain decode of the same batch; a member with no token past the prefix included."""
-    _log(f"decode grouped Hq={Hq} Hkv={Hkv} ps={ps} {dtype} groups={sizes} prefix={prefix}")
-    out_g, out_p, ref = _grouped_case(Hq, Hkv, ps, dtype, 7 + Hq + ps, sizes, prefix, n_alone=5)
+    _log(f"decode grouped Hq={Hq} Hkv={Hkv} ps={ps} {dtype} groups={sizes} prefix={prefix} D={D}")
+    out_g, out_p, ref = _grouped_case(Hq, Hkv, ps, dtype, 7 + Hq + ps, sizes, prefix, n_alone=5, D=D)
     torch.testing.assert_close(out_g, ref, atol=ATOL, rtol=RTOL)
     torch.testing.assert_close(out_p, ref, atol=ATOL, rtol=RTOL)
 
