@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
   const int f_key = tid / kChunks;
   const bool ps_pow2 = (ps & (ps - 1)) == 0;
   const int ps_shift = __builtin_ctz((unsigned)ps);
-  const int64_t page_bytes = (int64_t)ps * row_bytes;
+  const uint32_t page_bytes = (uint32_t)ps * (uint32_t)row_bytes;  // < 2^32 (checked by the host)
   auto fetch_half = [&](int kt, int half) {
     const int key0 = kt * kKeys + half * kHalf;
 #pragma unroll
@@ -310,8 +310,9 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
         pg = kabs / ps;
         slot = kabs - pg * ps;
       }
-      const int pid = page_lds[pg - win_base];
-      const int64_t off = (int64_t)pid * page_bytes + (slot * row_bytes + f_ch16);
+      // page ids in the window are checked (>= 0): one 32 x 32 -> 64-bit multiply-add
+      const uint32_t pid = (uint32_t)page_lds[pg - win_base];
+      const uint64_t off = (uint64_t)pid * page_bytes + (uint32_t)(slot * row_bytes + f_ch16);
       kreg[i] = *reinterpret_cast<const u32x4*>(kpool + off);
       vreg[i] = *reinterpret_cast<const u32x4*>(vpool + off);
     }
@@ -615,6 +616,8 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
     return fail(NSLG_EINVAL, "paged_prefill: q/pool/out must be 16-byte aligned");
   if (num_pages * (int64_t)page_size >= ((int64_t)1 << 31))
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: pool has >= 2^31 token slots");
+  if ((int64_t)page_size * num_kv_heads * head_dim * 2 > (int64_t)0xffffffff)
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: pages of >= 4 GiB");
   const int64_t tiles = grid_tiles(total_q, batch, group);
   if (tiles > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
 
