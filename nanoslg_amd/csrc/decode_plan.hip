@@ -19,8 +19,12 @@ namespace nslg {
 namespace {
 
 constexpr int kMaxPlanBatch = 512;
+// Batches up to this size launch with a 64-entry list in the arguments (256 bytes
+// instead of 2 KiB: measured 2.4 vs 3.2 us of host time per launch).
+constexpr int kSmallPlanBatch = 64;
 constexpr int kZeroBytes = 16 << 10;  // bytes zeroed per workgroup
 
+template <int N>
 struct PlanStepArgs {
   const int32_t* indptr_in;
   const int32_t* indices_in;
@@ -41,17 +45,19 @@ struct PlanStepArgs {
   int32_t num_layers;
   int32_t zero_parts;  // ceil(page_bytes / kZeroBytes)
   const int32_t* new_page_dev;  // nullptr: the list below; else the same list in device memory
-  int32_t new_page[kMaxPlanBatch];  // page opened by sequence b this step, or -1
+  int32_t new_page[N];  // page opened by sequence b this step, or -1
 };
 
-__device__ inline int opened_page(const PlanStepArgs& a, int b) {
+template <int N>
+__device__ inline int opened_page(const PlanStepArgs<N>& a, int b) {
   return a.new_page_dev ? a.new_page_dev[b] : a.new_page[b];
 }
 
 // Workgroup z of the zeroing part: (page, layer, K or V, 16 KiB part), where the
 // page is the j-th opened one of the list in the kernel arguments, or, with the
 // list in memory, the one sequence j opened (if any: one read of the list each).
-__device__ void zero_part(const PlanStepArgs& a, int z) {
+template <int N>
+__device__ void zero_part(const PlanStepArgs<N>& a, int z) {
   const int part = z % a.zero_parts;
   z /= a.zero_parts;
   const int kv = z & 1;
@@ -83,14 +89,16 @@ __device__ void zero_part(const PlanStepArgs& a, int z) {
 }
 
 // Pages of sequence s before the step, and whether this step opens one.
-__device__ inline void seq_step(const PlanStepArgs& a, int s, int& np_in, int& lpl_in, bool& opens) {
+template <int N>
+__device__ inline void seq_step(const PlanStepArgs<N>& a, int s, int& np_in, int& lpl_in, bool& opens) {
   np_in = a.indptr_in[s + 1] - a.indptr_in[s];
   lpl_in = np_in > 0 ? a.last_len_in[s] : a.page_size;
   lpl_in = lpl_in < 1 ? 1 : (lpl_in > a.page_size ? a.page_size : lpl_in);
   opens = lpl_in == a.page_size;
 }
 
-__global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs a) {
+template <int N>
+__global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs<N> a) {
   if ((int)blockIdx.x >= a.batch) {
     zero_part(a, blockIdx.x - a.batch);
     return;
@@ -175,52 +183,60 @@ int plan_step_impl(const int32_t* kv_indptr, const int32_t* kv_indices, const in
     return fail(NSLG_EINVAL, "decode_plan_step: null pointer");
   if (kv_indices_out == kv_indices || kv_indptr_out == kv_indptr || kv_last_page_len_out == kv_last_page_len)
     return fail(NSLG_EINVAL, "decode_plan_step: output tables must not alias the input ones");
-  PlanStepArgs a;
-  a.indptr_in = kv_indptr;
-  a.indices_in = kv_indices;
-  a.last_len_in = kv_last_page_len;
-  a.indptr_out = kv_indptr_out;
-  a.indices_out = kv_indices_out;
-  a.last_len_out = kv_last_page_len_out;
-  a.slot_out = slot_mapping_out;
-  a.pos_out = positions_out;
-  a.new_pages_out = new_pages_out;
-  a.batch = batch;
-  a.page_size = page_size;
-  a.new_page_dev = new_page_dev;
-  int opened = 0;
-  if (new_page_host) {
-    for (int b = 0; b < batch; ++b) {
-      a.new_page[b] = new_page_host[b];
-      opened += new_page_host[b] >= 0 ? 1 : 0;
+  // the same arguments at either list size
+  auto run = [&](auto& a) -> int {
+    a.indptr_in = kv_indptr;
+    a.indices_in = kv_indices;
+    a.last_len_in = kv_last_page_len;
+    a.indptr_out = kv_indptr_out;
+    a.indices_out = kv_indices_out;
+    a.last_len_out = kv_last_page_len_out;
+    a.slot_out = slot_mapping_out;
+    a.pos_out = positions_out;
+    a.new_pages_out = new_pages_out;
+    a.batch = batch;
+    a.page_size = page_size;
+    a.new_page_dev = new_page_dev;
+    int opened = 0;
+    if (new_page_host) {
+      for (int b = 0; b < batch; ++b) {
+        a.new_page[b] = new_page_host[b];
+        opened += new_page_host[b] >= 0 ? 1 : 0;
+      }
+    } else {
+      opened = batch;  // one zeroing slot per sequence: sequence j's page, if it opens one
     }
-  } else {
-    opened = batch;  // one zeroing slot per sequence: sequence j's page, if it opens one
+    a.k_pool = (char*)k_pool;
+    a.v_pool = (char*)v_pool;
+    a.num_layers = 0;
+    a.num_pages = 0;
+    a.page_bytes = 0;
+    a.zero_parts = 1;
+    int64_t zero_groups = 0;
+    if (k_pool || v_pool) {
+      if (!k_pool || !v_pool || num_layers <= 0 || num_pages <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+        return fail(NSLG_EINVAL, "decode_plan_step: bad pool for zeroing");
+      const int eb = elem_bytes(dtype);
+      if (!eb) return fail(NSLG_EINVAL, "decode_plan_step: dtype %d", dtype);
+      const int64_t pb = (int64_t)page_size * num_kv_heads * head_dim * eb;
+      if (pb % 16 || ((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)
+        return fail(NSLG_EINVAL, "decode_plan_step: pool pages must be 16-byte aligned");
+      a.num_layers = num_layers;
+      a.num_pages = num_pages;
+      a.page_bytes = pb;
+      a.zero_parts = (int32_t)((pb + kZeroBytes - 1) / kZeroBytes);
+      zero_groups = (int64_t)opened * num_layers * 2 * a.zero_parts;
+      if (batch + zero_groups > 0x7fffffff) return fail(NSLG_EINVAL, "decode_plan_step: too much to zero");
+    }
+    decode_plan_step_kernel<<<(unsigned)(batch + zero_groups), 256, 0, as_stream(stream)>>>(a);
+    return check_launch("decode_plan_step");
+  };
+  if (batch <= kSmallPlanBatch) {
+    PlanStepArgs<kSmallPlanBatch> a;
+    return run(a);
   }
-  a.k_pool = (char*)k_pool;
-  a.v_pool = (char*)v_pool;
-  a.num_layers = 0;
-  a.num_pages = 0;
-  a.page_bytes = 0;
-  a.zero_parts = 1;
-  int64_t zero_groups = 0;
-  if (k_pool || v_pool) {
-    if (!k_pool || !v_pool || num_layers <= 0 || num_pages <= 0 || num_kv_heads <= 0 || head_dim <= 0)
-      return fail(NSLG_EINVAL, "decode_plan_step: bad pool for zeroing");
-    const int eb = elem_bytes(dtype);
-    if (!eb) return fail(NSLG_EINVAL, "decode_plan_step: dtype %d", dtype);
-    const int64_t pb = (int64_t)page_size * num_kv_heads * head_dim * eb;
-    if (pb % 16 || ((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)
-      return fail(NSLG_EINVAL, "decode_plan_step: pool pages must be 16-byte aligned");
-    a.num_layers = num_layers;
-    a.num_pages = num_pages;
-    a.page_bytes = pb;
-    a.zero_parts = (int32_t)((pb + kZeroBytes - 1) / kZeroBytes);
-    zero_groups = (int64_t)opened * num_layers * 2 * a.zero_parts;
-    if (batch + zero_groups > 0x7fffffff) return fail(NSLG_EINVAL, "decode_plan_step: too much to zero");
-  }
-  decode_plan_step_kernel<<<(unsigned)(batch + zero_groups), 256, 0, as_stream(stream)>>>(a);
-  return check_launch("decode_plan_step");
+  PlanStepArgs<kMaxPlanBatch> a;
+  return run(a);
 }
 
 }  // namespace

@@ -434,17 +434,20 @@ def decode_plan_step(kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_
     return _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args)
 
 
-def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args, out=None):
+def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_size, num_new, pool_args, out=None,
+                      new_page_ptr=None):
     """decode_plan_step without the argument checks, for callers whose inputs are the
-    previous plan's outputs (the cache manager). new_page: contiguous int32 numpy;
-    pool_args: (k_pool ptr, v_pool ptr, L, P, Hkv, D, dtype code) or all-null. `out`:
-    preallocated outputs (an object with indptr, indices, lpl, slot, pos, new_pages
-    tensors, `ptrs` = their six addresses, indices with room for this step's pages),
-    else new tensors (indices exactly this step's pages)."""
+    previous plan's outputs (the cache manager). new_page: contiguous int32 numpy
+    (new_page_ptr: its address, when the caller keeps it; the values are read during
+    the call); pool_args: (k_pool ptr, v_pool ptr, L, P, Hkv, D, dtype code) or
+    all-null. `out`: preallocated outputs (an object with indptr, indices, lpl, slot,
+    pos, new_pages tensors, `ptrs` = their six addresses, indices with room for this
+    step's pages), else new tensors (indices exactly this step's pages)."""
     B = kv_indptr.numel() - 1
     if out is not None:
         rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                                              kv_last_page_len.data_ptr(), B, int(page_size), new_page.ctypes.data,
+                                              kv_last_page_len.data_ptr(), B, int(page_size),
+                                              new_page.ctypes.data if new_page_ptr is None else new_page_ptr,
                                               *out.ptrs, *pool_args, _stream(kv_indptr))
         _lib.check(rc, "nslg_decode_plan_step")
         return out.indptr, out.indices, out.lpl, out.slot, out.pos, out.new_pages

@@ -1180,6 +1180,7 @@ class PagedKVCache(KVCacheManager):
         self._pool_args = None  # the pools as the device planner takes them
         self._decode_rows: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._plan_ring = None  # [batch, capacity, buffers, last used] of device-planned decode steps
+        self._newp = None  # (batch, int32 [batch] opened-page list, -1 between steps, its address)
         # the block tables on the device (room for every pool page twice before growing)
         self._tables = _BlockTableArena(self.pool.device, 2 * cfg.max_pages + 4096)
         if self.pool.device.type == "cuda":
@@ -1369,9 +1370,10 @@ class PagedKVCache(KVCacheManager):
         new_page, n_new = step
         return self._plan_on_device(B, prev[1], new_page, n_new)
 
-    def _plan_on_device(self, B, plan, new_page, n_new) -> "_ForwardPlan":
+    def _plan_on_device(self, B, plan, new_page, n_new, new_page_ptr=None) -> "_ForwardPlan":
         """The next decode plan from `plan` on the device (kernels.decode_plan_step):
-        new_page int32 [B], the page sequence b opens this step or -1."""
+        new_page int32 [B], the page sequence b opens this step or -1 (new_page_ptr: its
+        address, if known)."""
         kern, pool, ps = self.kernels, self.pool, self.cfg.page_size
         fast = getattr(kern, "_decode_plan_step", None)
         if fast is not None:  # inputs are the previous plan's outputs: no argument checks
@@ -1380,7 +1382,7 @@ class PagedKVCache(KVCacheManager):
                 self._pool_args = (pool.k.data_ptr(), pool.v.data_ptr(), L, P, Hkv, D, kern.dtype_code(pool.k.dtype))
             dst = self._plan_buffers(B, plan.total_pages + n_new)
             indptr, indices, lpl, slot, pos, new = fast(plan.indptr, plan.indices, plan.lpl, new_page, ps, n_new,
-                                                        self._pool_args, out=dst)
+                                                        self._pool_args, out=dst, new_page_ptr=new_page_ptr)
         else:
             indptr, indices, lpl, slot, pos, new = kern.decode_plan_step(plan.indptr, plan.indices, plan.lpl,
                                                                         new_page, ps, n_new, pool.k, pool.v)
@@ -1422,7 +1424,11 @@ class PagedKVCache(KVCacheManager):
             states.append(st)
         if opening > pool.num_free:
             return None
-        new_page = [-1] * B
+        newp = self._newp
+        if newp is None or newp[0] != B:
+            buf = np.full(B, -1, np.int32)
+            newp = self._newp = (B, buf, buf.ctypes.data)
+        new_page = newp[1]  # -1 everywhere between steps
         if opening:
             pages = pool.alloc(opening, zero=False)  # zeroed by the planner, as the general path does
             it = iter(pages)
@@ -1437,7 +1443,11 @@ class PagedKVCache(KVCacheManager):
             used = n % ps + 1
             if tu[pid] < used:
                 tu[pid] = used
-        new_plan = self._plan_on_device(B, plan, np.array(new_page, np.int32), opening)
+        try:
+            new_plan = self._plan_on_device(B, plan, new_page, opening, new_page_ptr=newp[2])
+        finally:
+            if opening:
+                new_page.fill(-1)  # the planner took the list by value
         ctx = PagedCacheContext.__new__(PagedCacheContext)
         ctx.cache, ctx.seq_ids, ctx.batch_size = self, list(ids), B
         ctx.new_token_counts, ctx.input_offsets = [1] * B, [0] * B

@@ -640,7 +640,7 @@ def test_decode_append_grouped_bit_exact():
     assert torch.equal(_bits(o1), _bits(o2))
 
 
-@pytest.mark.parametrize("B,ps", [(64, 16), (1, 16), (37, 32), (512, 8)])
+@pytest.mark.parametrize("B,ps", [(64, 16), (65, 16), (1, 16), (37, 32), (512, 8)])
 def test_decode_plan_step_bit_exact(B, ps):
     """The device-built next-step plan equals the CSR the oracle builds from the
     extended block tables (kv_cache.py:598-615), with slots and positions of the new
