@@ -496,6 +496,13 @@ class PagePool:
         self._is_free[1:] = True
         self._free: List[int] = list(range(P - 1, 0, -1))
         self._lock = threading.Lock()
+        self._layers: List[Tuple[torch.Tensor, torch.Tensor]] = []
+
+    def layer(self, i: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The K and V pool views of layer i ([P, ps, Hkv, D]), made once."""
+        if not self._layers:
+            self._layers = list(zip(self.k.unbind(0), self.v.unbind(0)))
+        return self._layers[i]
 
     # -- allocation --------------------------------------------------------------------
     def alloc(self, n: int = 1, zero: bool = True) -> Optional[List[int]]:
@@ -1033,6 +1040,12 @@ class PagedCacheContext(CacheContext):
                 pidx = p0[rep] + (np.arange(tot, dtype=np.int64) - wfirst[rep])
                 last = np.where(pidx == plast[rep], (start + n - 1 - plast * ps)[rep], ps - 1)
                 pool.tokens_used[wp] = np.maximum(pool.tokens_used[wp], last + 1)
+                if zero.size:
+                    # a page this forward writes in every slot needs no zero-on-alloc: the
+                    # append leaves the same bytes (a chunked prefill's pages, but the last)
+                    full = (pidx * ps >= start[rep]) & ((pidx + 1) * ps <= (start + n)[rep])
+                    if bool(full.any()):
+                        zero = zero[~np.isin(zero, wp[full])]
             else:
                 wp = np.zeros(1, np.int64)
             T = int(ncnt.sum())
@@ -1087,7 +1100,7 @@ class PagedCacheContext(CacheContext):
                 self._plan.group_slot = views[9]
                 self._plan.groups = kern.DecodeGroups(B, groups[0], groups[1], pool.device,
                                                       seq_group_slot=views[9])
-        if zero_pages:  # zero-on-alloc of the pages this forward's extensions took
+        if zero.size:  # zero-on-alloc of the pages this forward's extensions took
             kern.zero_pages(pool.k, pool.v, self._plan.zero_ids)
         if cow_src:
             kern.copy_pages(pool.k, pool.v, self._plan.cow_src, self._plan.cow_dst)
@@ -1114,7 +1127,7 @@ class PagedCacheContext(CacheContext):
             if launch is None or launch.bound_plan is not plan:
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q, k_new, v_new)
-        k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+        k_layer, v_layer = pool.layer(layer_idx)
         kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         return self._prefill(q, k_layer, v_layer)
 
@@ -1136,7 +1149,7 @@ class PagedCacheContext(CacheContext):
             if launch is None or launch.bound_plan is not plan:
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q, k_new, v_new, rope=(cos, sin, pos))
-        k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+        k_layer, v_layer = pool.layer(layer_idx)
         q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
         return self._prefill(q_rot, k_layer, v_layer)
 
