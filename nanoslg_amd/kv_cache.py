@@ -653,11 +653,6 @@ class RadixTree:
         self._clock += 1
         return self._clock
 
-    def _keys(self, tokens):
-        ps = self.ps
-        for i in range(len(tokens) // ps):
-            yield tuple(tokens[i * ps:(i + 1) * ps])
-
     def _partials_on_path(self, node, tokens, at):
         """(length, node) of the partial children of `node` whose ids are a prefix of
         tokens[at:], shortest first (the token path passes through them in that
