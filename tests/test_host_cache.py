@@ -731,3 +731,42 @@ def test_partial_page_match_brute_force(seed):
             plen, pages = impl.tree.match(prompt)
             assert plen == f * ps + r, (impl, prompt)
             assert len(pages) == f + (1 if r else 0)
+
+
+def test_pages_written_in_full_skip_the_owed_zeroing():
+    """A multi-token forward zeroes the pages it owes zero-on-alloc (kv_cache.py:411)
+    except those its own append writes in every slot: chunks of whole pages launch no
+    zeroing, a chunk that ends inside a page zeroes that page. Every page of every
+    block table, unwritten slots included, equals the oracle's bytes."""
+    g = torch.Generator().manual_seed(21)
+    mgr, ref = make(ps=4, pages=64, prefix=False)
+    # pages written once and released, so the pages taken below hold old K/V
+    for impl in (mgr, ref):
+        impl.allocate_sequence("x")
+    forward_both(mgr, ref, ["x"], [60], [0], g)
+    for impl in (mgr, ref):
+        impl.release_sequence("x")
+    ids = ["a", "b"]
+    for impl in (mgr, ref):
+        for sid in ids:
+            impl.allocate_sequence(sid)
+
+    def zero_calls():
+        return [n for name, n in FK.CALLS if name == "zero_pages"]
+
+    FK.CALLS.clear()
+    forward_both(mgr, ref, ids, [8, 12], [0, 0], g)  # whole pages only
+    assert zero_calls() == []
+    FK.CALLS.clear()
+    forward_both(mgr, ref, ids, [6, 3], [0, 0], g)  # a: 8..13 ends inside a page; b: 12..14 too
+    assert zero_calls() == [2]
+    FK.CALLS.clear()
+    forward_both(mgr, ref, ids, [2, 8], [0, 0], g)  # a fills its page; b: 15..22, a page in full
+    assert zero_calls() == [1]  # and b's last page, slots 20..22 of 20..23
+    check_state(mgr, ref, ids)
+    for sid in ids:
+        bt1, bt2 = mgr.seqs[sid].bt[:mgr.seqs[sid].n_pages].tolist(), ref.seqs[sid].block_table
+        assert len(bt1) == len(bt2)
+        for p1, p2 in zip(bt1, bt2):
+            assert torch.equal(mgr.pool.k[:, p1], ref.pool.k[:, p2])
+            assert torch.equal(mgr.pool.v[:, p1], ref.pool.v[:, p2])
