@@ -437,6 +437,7 @@ def test_device_decode_plan_matches_host_plan(scalar_batch, monkeypatch):
     per-sequence one of small batches (begin_forward's one-pass steady step) and the
     vectorised one."""
     monkeypatch.setattr(KC.PagedKVCache, "SCALAR_PLAN_BATCH", scalar_batch)
+    monkeypatch.setattr(KC.PagedKVCache, "ONE_PASS_BATCH", scalar_batch)
     g = torch.Generator().manual_seed(11)
     fast, _ = make(ps=4, pages=96, prefix=False)
     slow, _ = make(ps=4, pages=96, prefix=False)
