@@ -984,7 +984,7 @@ class PagedCacheContext(CacheContext):
             pi = npg - 1
             sl = start - pi * ps
             ok = pi < have
-            pids = np.fromiter((int(st.bt[p]) if o else 0 for st, p, o in zip(states, pi.tolist(), ok.tolist())),
+            pids = np.fromiter((st.bt.item(p) if o else 0 for st, p, o in zip(states, pi.tolist(), ok.tolist())),
                                np.int64, B)
             cand = np.nonzero(ok & (pool.ref_count[pids] > 1))[0]
             for b in cand.tolist():
@@ -993,8 +993,9 @@ class PagedCacheContext(CacheContext):
                     _cow(st, int(pi[b]))
                     pids[b] = st.bt[pi[b]]
             slot = np.where(ok, pids * ps + sl, 0).astype(np.int32)
-            if ok.any():
-                np.maximum.at(pool.tokens_used, pids[ok], sl[ok] + 1)
+            if ok.any():  # the written pages are distinct after copy-on-write
+                w = pids[ok]
+                pool.tokens_used[w] = np.maximum(pool.tokens_used[w], sl[ok] + 1)
             lpl = lens - pi * ps
             pos = start.astype(np.int32)
             q_rows = np.arange(B, dtype=np.int32)
