@@ -27,6 +27,23 @@ def test_random_serving_traffic_on_gpu(seed, ps, pages):
     R.run_traffic(seed, ps, pages, GPU)
 
 
+@pytest.mark.parametrize("seed,ps,pages,HQ,HKV,D,dtype", [
+    (501, 16, 40, 32, 8, 128, torch.float16),   # the Llama-3 layer shape
+    (502, 8, 60, 32, 8, 128, torch.bfloat16),
+    (503, 32, 30, 16, 8, 128, torch.float16),   # G = 2
+    (504, 4, 50, 8, 8, 64, torch.bfloat16),     # G = 1
+    (505, 1, 70, 16, 2, 64, torch.float16),     # G = 8, one-token pages
+    (506, 16, 24, 32, 8, 128, torch.bfloat16),
+])
+def test_random_serving_traffic_shapes_on_gpu(seed, ps, pages, HQ, HKV, D, dtype):
+    """The same traffic at other head shapes and in bf16, on the same bar."""
+    import test_host_random as R
+    print(f"random traffic seed={seed} ps={ps} pages={pages} {HQ}/{HKV}x{D} {dtype}", flush=True)
+    sys.stdout.flush()
+    env = dict(GPU, HQ=HQ, HKV=HKV, D=D, dtype=dtype)
+    R.run_traffic(seed, ps, pages, env)
+
+
 @pytest.mark.parametrize("seed", [1, 2, 3, 4, 5])
 def test_random_contiguous_traffic_on_gpu(seed):
     import test_host_random as R
