@@ -255,28 +255,25 @@ class EventTimedKernels:
         return _TimedLaunch(self, real)
 
     def paged_decode(self, *args, **kw):
+        return self._timed(self._k.paged_decode, *args, **kw)
+
+    def _timed(self, fn, *args, **kw):
         if not self.recording:
-            return self._k.paged_decode(*args, **kw)
+            return fn(*args, **kw)
         torch = self._torch
         stream = torch.cuda.current_stream()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        out = self._k.paged_decode(*args, **kw)
+        out = fn(*args, **kw)
         b.record(stream)
         self.events.append((a, b))
         return out
 
     def paged_prefill(self, *args, **kw):
-        if not self.recording:
-            return self._k.paged_prefill(*args, **kw)
-        torch = self._torch
-        stream = torch.cuda.current_stream()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        out = self._k.paged_prefill(*args, **kw)
-        b.record(stream)
-        self.events.append((a, b))
-        return out
+        return self._timed(self._k.paged_prefill, *args, **kw)
+
+    def _paged_prefill_layer(self, *args, **kw):  # the cache manager's prefill launch
+        return self._timed(self._k._paged_prefill_layer, *args, **kw)
 
     def mean_ms(self):
         return float(np.mean([a.elapsed_time(b) for a, b in self.events]))

@@ -103,6 +103,29 @@ def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: torch.Tens
     _lib.check(rc, "nslg_append_kv")
 
 
+def _append_kv_layer(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: torch.Tensor,
+                     k_layer: torch.Tensor, v_layer: torch.Tensor) -> None:
+    """append_kv for the cache manager: its pool layer (contiguous [P, page_size, Hkv,
+    D], K and V alike) and slot mapping (int32 on the pool's device) are taken as they
+    are; the caller's k_new and v_new get append_kv's checks (a tensor that fails one
+    goes through append_kv, which raises its error)."""
+    dev, dt = k_layer.get_device(), k_layer.dtype
+    Hkv, D = k_layer.shape[2], k_layer.shape[3]
+    if (k_new.get_device() != dev or v_new.get_device() != dev or k_new.dtype != dt or v_new.dtype != dt
+            or k_new.dim() < 2 or v_new.dim() < 2 or k_new.shape[-1] != D or v_new.shape[-1] != D
+            or k_new.shape[-2] != Hkv or v_new.shape[-2] != Hkv):
+        return append_kv(k_new, v_new, slot_mapping, k_layer, v_layer)
+    nk, ks, _ = _rows(k_new, "k_new")
+    nv, vs, _ = _rows(v_new, "v_new")
+    T = slot_mapping.numel()
+    if nk != T or nv != T:
+        raise ValueError(f"append_kv: {T} slots for {nk} k rows / {nv} v rows")
+    rc = _lib.load().nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(),
+                                    T, k_layer.data_ptr(), v_layer.data_ptr(), k_layer.shape[0] * k_layer.shape[1],
+                                    Hkv, D, _DTYPE_CODE[dt], _stream(k_layer))
+    _lib.check(rc, "nslg_append_kv")
+
+
 def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, D: int):
     """fp32 [R, >=D] tables with unit inner stride and a common row stride (a
     16-bit table is widened exactly; the kernel rounds it back)."""
@@ -531,11 +554,16 @@ def _decode_plan_step_device(kv_indptr, kv_indices, kv_last_page_len, new_page, 
     _lib.check(rc, "nslg_decode_plan_step_device")
 
 
-def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
-    """forward_plan without the argument checks (the cache manager's own tables)."""
+def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T,
+                  out=None):
+    """forward_plan without the argument checks (the cache manager's own tables). The
+    outputs (slots, positions, rows, qo_indptr) are consecutive views of `out` (int32,
+    at least 2*B*iw + T + B + 1 entries on the device) or of a new buffer."""
     sizes = [B * iw, B * iw, T, B + 1]
-    buf = torch.empty(sum(sizes) + 1, dtype=torch.int32, device=kv_indptr.device)
-    slot, pos, rows, qo, _ = buf.split(sizes + [1])
+    buf = torch.empty(sum(sizes) + 1, dtype=torch.int32, device=kv_indptr.device) if out is None else out
+    if buf.numel() < sum(sizes) or buf.dtype != torch.int32:
+        raise ValueError("forward_plan: the output buffer is too small or not int32")
+    slot, pos, rows, qo = buf[:sum(sizes)].split(sizes)
     base = buf.data_ptr()
     o1, o2 = 4 * B * iw, 8 * B * iw
     o3 = o2 + 4 * T
@@ -720,6 +748,44 @@ class DecodeLaunch:
                                                out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
             _lib.check(rc, "nslg_paged_decode_grouped")
         return out
+
+
+def _paged_prefill_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
+                         k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
+                         kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, workspace: Workspace,
+                         q_rows: Optional[torch.Tensor] = None, grid_width: int = 0) -> torch.Tensor:
+    """paged_prefill for the cache manager: its pool layer, plan (int32 arrays on the
+    pool's device, qo_indptr and kv_indptr of B + 1 entries) and workspace are taken
+    as they are; the caller's q gets paged_prefill's checks (a q that fails one goes
+    through paged_prefill, which raises its error). Default scale 1/sqrt(D)."""
+    dev, dt = k_layer.get_device(), k_layer.dtype
+    P, ps, Hkv, D = k_layer.shape
+    B = kv_indptr.numel() - 1
+    if (q.get_device() != dev or q.dtype != dt or q.dim() != 3 or q.shape[2] != D or q.stride(2) != 1
+            or q.stride(1) != D or q.shape[0] < total_q
+            or (q_rows is not None and (grid_width < 1 or q.shape[0] != B * grid_width))):
+        return paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices,
+                             kv_last_page_len, workspace=workspace, q_rows=q_rows, grid_width=grid_width)
+    T, Hq = q.shape[0], q.shape[1]
+    out = torch.empty((T, Hq, D), dtype=dt, device=q.device)
+    lib = _lib.load()
+    ws = workspace.get(int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q))))
+    stream = _stream(k_layer)
+    scale = 1.0 / math.sqrt(D)
+    if q_rows is not None:
+        rc = lib.nslg_paged_prefill_grid(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), q_rows.data_ptr(),
+                                         int(grid_width), int(total_q), int(max_q), k_layer.data_ptr(),
+                                         v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                         kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale, _DTYPE_CODE[dt],
+                                         out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "nslg_paged_prefill_grid")
+        return out
+    rc = lib.nslg_paged_prefill(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), int(total_q), int(max_q),
+                                k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                                kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale,
+                                _DTYPE_CODE[dt], out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "nslg_paged_prefill")
+    return out
 
 
 def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,

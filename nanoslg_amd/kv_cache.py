@@ -279,12 +279,8 @@ class _PlanStaging:
         if buf is None or buf.numel() < total:
             buf = torch.empty(max(total, 1 << 12) * 2, dtype=torch.int32, pin_memory=True)
             self.host[k], self.host_np[k] = buf, buf.numpy()
-        host = self.host_np[k]
-        off = 0
-        for a in parts:
-            n = a.size
-            host[off:off + n] = a.reshape(-1)
-            off += n
+        if total:  # one pass over every part (each cast to int32 as it is written)
+            np.concatenate(parts, out=self.host_np[k][:total], casting="unsafe")
         self.pending[k] = True
         size = max(total + extra, 1)
         if 4 * total <= self.SIDE_STREAM_BYTES:
@@ -320,10 +316,11 @@ def _upload_i32(parts: List[np.ndarray], device: torch.device, extra: int = 0) -
     per part; with extra > 0, one more view of `extra` uninitialised entries in the
     same buffer, for a device output). On a GPU this goes through the device's
     _PlanStaging."""
-    sizes = [int(a.size) for a in parts]
+    parts = [a if isinstance(a, np.ndarray) and a.ndim == 1 else np.asarray(a).reshape(-1) for a in parts]
+    sizes = [a.size for a in parts]
     total = sum(sizes)
     if device.type == "cuda":
-        dev = _staging(device).upload([np.asarray(a) for a in parts], total, extra)
+        dev = _staging(device).upload(parts, total, extra)
     else:
         dev = torch.from_numpy(np.concatenate([np.asarray(a, dtype=np.int32).reshape(-1) for a in parts]
                                               + [np.zeros(extra, np.int32)])).clone()
@@ -495,6 +492,7 @@ class PagePool:
         self._is_free = np.zeros(P, bool)
         self._is_free[1:] = True
         self._free: List[int] = list(range(P - 1, 0, -1))
+        self._mark = np.zeros(P, bool)  # scratch page set for mark_filter, all False between calls
         self._lock = threading.Lock()
         self._layers: List[Tuple[torch.Tensor, torch.Tensor]] = []
 
@@ -509,6 +507,11 @@ class PagePool:
         """All-or-nothing allocation of n pages (refcount 1, tokens_used 0).
         Returns None when fewer than n are free. zero=True zeroes them on the device
         (all layers, K and V) in one launch."""
+        got = self.alloc_ids(n, zero)
+        return None if got is None else got[0]
+
+    def alloc_ids(self, n: int, zero: bool = True) -> Optional[Tuple[List[int], np.ndarray]]:
+        """alloc(n, zero), the pages also as an int64 array."""
         with self._lock:
             if len(self._free) < n:
                 return None
@@ -521,7 +524,16 @@ class PagePool:
             self._is_free[idx] = False
         if zero and out:
             self.zero(out)
-        return out
+        return out, idx
+
+    def mark_filter(self, ids: np.ndarray, drop: np.ndarray) -> np.ndarray:
+        """The entries of ids that are not in drop, in order (np.isin's result, through
+        a page-indexed mark: a few fancy-index passes instead of a sort)."""
+        mark = self._mark
+        mark[drop] = True
+        keep = ids[~mark[ids]]
+        mark[drop] = False
+        return keep
 
     def zero(self, page_ids: List[int]) -> None:
         if not page_ids:
@@ -1041,7 +1053,7 @@ class PagedCacheContext(CacheContext):
                     # append leaves the same bytes (a chunked prefill's pages, but the last)
                     full = (pidx * ps >= start[rep]) & ((pidx + 1) * ps <= (start + n)[rep])
                     if bool(full.any()):
-                        zero = zero[~np.isin(zero, wp[full])]
+                        zero = pool.mark_filter(zero, wp[full])
             else:
                 wp = np.zeros(1, np.int64)
             T = int(ncnt.sum())
@@ -1076,10 +1088,12 @@ class PagedCacheContext(CacheContext):
         if device_plan:
             # per-token slots, positions and the ragged layout expanded on the device
             offs = np.fromiter(self.input_offsets, np.int64, B)
-            views, d_idx = cache._plan_upload(states, indptr, [lpl, cs, cd, zero, start, ncnt, offs, have])
+            fp_sizes = [B * iw, B * iw, T, B + 1]  # forward_plan's outputs, after the CSR indices
+            views, d_idx, fp_out = cache._plan_upload(states, indptr, [lpl, cs, cd, zero, start, ncnt, offs, have],
+                                                      tail=sum(fp_sizes))
             d_indptr, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have = views
             slot_t, pos_t, rows_t, qo_t = kern._forward_plan(d_indptr, d_idx, d_start, d_n, d_off, d_have, B, iw,
-                                                             ps, T)
+                                                             ps, T, out=fp_out)
             self._uniform_rows = T == B * iw
             self._plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t,
                                                    d_cs, d_cd, d_zero, total_pages, T)
@@ -1124,7 +1138,7 @@ class PagedCacheContext(CacheContext):
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q, k_new, v_new)
         k_layer, v_layer = pool.layer(layer_idx)
-        kern.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
+        kern._append_kv_layer(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         return self._prefill(q, k_layer, v_layer)
 
     def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
@@ -1157,12 +1171,12 @@ class PagedCacheContext(CacheContext):
         Hq, D = q.shape[2], q.shape[3]
         q_grid = q.reshape(B * S, Hq, D)
         if self._uniform_rows and S == self._iw:  # every grid row is a token: the ragged rows themselves
-            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
-                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace)
+            o = kern._paged_prefill_layer(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                          plan.indptr, plan.indices, plan.lpl, cache.workspace)
         else:  # padded or ragged: the kernel reads and writes the grid rows (pad rows zero)
-            o = kern.paged_prefill(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
-                                   plan.indptr, plan.indices, plan.lpl, workspace=cache.workspace,
-                                   q_rows=plan.rows_for(S), grid_width=S)
+            o = kern._paged_prefill_layer(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
+                                          plan.indptr, plan.indices, plan.lpl, cache.workspace,
+                                          q_rows=plan.rows_for(S), grid_width=S)
         return o.view(B, S, Hq * D)
 
     # ---- introspection used by tests and the bench -------------------------------------
@@ -1197,13 +1211,14 @@ class PagedKVCache(KVCacheManager):
 
     STAGING_INTS = 1 << 16  # pinned plan-upload buffers (int32 each) set up with the cache
 
-    def _plan_upload(self, states, indptr, parts):
+    def _plan_upload(self, states, indptr, parts, tail=0):
         """One upload of a forward's host-built plan arrays (`parts`, after the CSR
         pointers `indptr`) together with the block-table entries its sequences gained
         or changed since their device rows were last used; then the forward's CSR
         indices built on the device from those rows (nslg_block_table_csr), which
         also brings the rows up to date. Returns ([indptr] + views of parts,
-        kv_indices) on the device."""
+        kv_indices) on the device; with tail > 0, also a third item: `tail` more
+        entries of the same device buffer, left for other device outputs."""
         tables = self._tables
         B = len(states)
         for st in states:
@@ -1218,13 +1233,16 @@ class PagedKVCache(KVCacheManager):
                  if npatch else np.zeros(1, np.int32))
         total = int(indptr[-1])
         up = _upload_i32([indptr] + list(parts) + [row, have, syn, pip, patch], self.pool.device,
-                         extra=max(total, 1))
+                         extra=max(total, 1) + tail)
         k = len(parts) + 1
-        d_row, d_have, d_syn, d_pip, d_patch, d_idx = up[k:k + 6]
+        d_row, d_have, d_syn, d_pip, d_patch, d_ext = up[k:k + 6]
+        d_idx = d_ext[:max(total, 1)] if tail else d_ext
         self.kernels._block_table_csr(tables.dev, d_row, d_have, d_syn, d_pip, d_patch, npatch, up[0], d_idx,
                                       total, B)
         for st in states:
             st.synced = st.n_pages
+        if tail:
+            return up[:k], d_idx, d_ext[max(total, 1):]
         return up[:k], d_idx
 
     # ---- decode plans built on the device ---------------------------------------------
@@ -1539,10 +1557,10 @@ class PagedKVCache(KVCacheManager):
             if need > 0:
                 grow.append((st, need))
         if len(grow) > 1 and self.pool.num_free >= sum(k for _, k in grow):
-            pages = self._alloc(sum(k for _, k in grow), defer_zero=True)
+            ids = self._alloc(sum(k for _, k in grow), defer_zero=True, as_array=True)
             o = 0
             for st, k in grow:
-                st.extend(pages[o:o + k])
+                st.extend(ids[o:o + k])
                 o += k
         else:
             for st, k in grow:
@@ -1591,16 +1609,18 @@ class PagedKVCache(KVCacheManager):
         for s in list(self.seqs):
             self.release_sequence(s)
 
-    def _alloc(self, n, defer_zero=False):
-        """kv_cache.py:760-768: pool, else LRU-evict from the tree and retry, else OOM."""
-        pages = self.pool.alloc(n, zero=not defer_zero)
-        if pages is None and self.tree and self.tree.evict_lru(n) > 0:
-            pages = self.pool.alloc(n, zero=not defer_zero)
-        if pages is None:
+    def _alloc(self, n, defer_zero=False, as_array=False):
+        """kv_cache.py:760-768: pool, else LRU-evict from the tree and retry, else OOM.
+        The pages as a list, or (as_array) as an int64 array."""
+        got = self.pool.alloc_ids(n, zero=not defer_zero)
+        if got is None and self.tree and self.tree.evict_lru(n) > 0:
+            got = self.pool.alloc_ids(n, zero=not defer_zero)
+        if got is None:
             raise RuntimeError(f"KV OOM: need {n}, free {self.pool.num_free}")
+        pages, ids = got
         if defer_zero:
             self._pending_zero.extend(pages)
-        return pages
+        return ids if as_array else pages
 
     @property
     def stats(self):

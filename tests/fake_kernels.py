@@ -110,6 +110,16 @@ def paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_
     return res
 
 
+def _append_kv_layer(k_new, v_new, slot_mapping, k_layer, v_layer):
+    append_kv(k_new, v_new, slot_mapping, k_layer, v_layer)
+
+
+def _paged_prefill_layer(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,
+                         workspace, q_rows=None, grid_width=0):
+    return paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,
+                         workspace=workspace, q_rows=q_rows, grid_width=grid_width)
+
+
 class DecodeLaunch:
     """Per-forward append + decode, as nanoslg_amd.kernels.DecodeLaunch, from the
     functions above."""
@@ -230,7 +240,8 @@ def _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch
                 kv_indices[ip[b] + i] = pid
 
 
-def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T):
+def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_allocated, B, iw, page_size, T,
+                  out=None):
     """As nanoslg_amd.kernels._forward_plan, in plain Python on the CPU."""
     CALLS.append(("forward_plan", T))
     ip, idx = kv_indptr.tolist(), kv_indices.tolist()
@@ -245,5 +256,9 @@ def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages
             pos[r] = ap
             rows[qo[-1] + t] = r
         qo.append(qo[-1] + max(n[b], 0))
-    t = lambda x: torch.tensor(x, dtype=torch.int32)  # noqa: E731
-    return t(slot), t(pos), t(rows), t(qo)
+    flat = torch.tensor(slot + pos + rows + qo, dtype=torch.int32)
+    if out is not None:  # the outputs are consecutive views of the caller's buffer
+        assert out.dtype == torch.int32 and out.numel() >= flat.numel()
+        out[:flat.numel()].copy_(flat)
+        flat = out[:flat.numel()]
+    return tuple(flat.split([B * iw, B * iw, T, B + 1]))
