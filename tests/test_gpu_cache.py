@@ -76,6 +76,45 @@ def check_state(mgr, ref, ids):
             assert torch.equal(k1.float(), k2) and torch.equal(v1.float(), v2)
 
 
+def test_prefill_attend_checks_the_callers_tensors():
+    """The cache's prefill calls take its own pool and plan as they are and check the
+    caller's q, k_new and v_new as the public kernel calls do: a CPU tensor, another
+    dtype, other head counts or too few rows raise before any launch, and the same
+    forward then runs as usual (outputs and pool bytes against the oracle)."""
+    _log("cache: prefill attend argument checks")
+    mgr, ref = make(prefix=False)
+    g = torch.Generator().manual_seed(11)
+    for sid in ("a", "b"):
+        mgr.allocate_sequence(sid)
+        ref.allocate_sequence(sid)
+    ids, ntok, S = ["a", "b"], [20, 20], 20
+    q = torch.randn(2, S, HQ, D, generator=g).half()
+    k = torch.randn(2, S, HKV, D, generator=g).half()
+    v = torch.randn(2, S, HKV, D, generator=g).half()
+    c1 = mgr.begin_forward(ids, ntok)
+    c2 = ref.begin_forward(ids, ntok)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    with pytest.raises(ValueError):
+        c1.attend(0, qd, k, vd, HQ, HKV)  # k_new on the host
+    with pytest.raises(TypeError):
+        c1.attend(0, qd, kd.bfloat16(), vd, HQ, HKV)
+    with pytest.raises(ValueError):
+        c1.attend(0, qd, kd[:, :, :4], vd[:, :, :4], HQ, HKV)  # 4 KV heads for a pool of 8
+    with pytest.raises(ValueError):
+        c1.attend(0, qd, kd[:, :10], vd[:, :10], HQ, HKV)  # 20 rows of slots, 10 rows given
+    with pytest.raises(ValueError):
+        c1.attend(0, q, kd, vd, HQ, HKV)  # q on the host
+    with pytest.raises(TypeError):
+        c1.attend(0, qd.bfloat16(), kd, vd, HQ, HKV)
+    for layer in range(L):
+        o1 = c1.attend(layer, qd, kd, vd, HQ, HKV).float().cpu()
+        o2 = c2.attend(layer, q.float(), k.float(), v.float(), HQ, HKV)
+        torch.testing.assert_close(o1, o2, atol=ATOL, rtol=RTOL)
+    mgr.end_forward(c1)
+    ref.end_forward(c2)
+    check_state(mgr, ref, ids)
+
+
 def test_paged_prefill_then_decode():
     _log("cache: prefill + decode")
     g = torch.Generator().manual_seed(0)
