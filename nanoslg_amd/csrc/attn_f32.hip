@@ -1,7 +1,9 @@
-// Paged attention over fp32 pools (decode and causal chunked prefill alike), for
-// gfx950. The 16-bit paths run on MFMA; this one serves caches kept in fp32 (the
-// contiguous backend of an fp32 model, kv_cache.py:227-322, whose attention is
-// torch SDPA in the model's dtype). It computes in fp32 on the VALU with its
+// Paged attention on the VALU (decode and causal chunked prefill alike), for gfx950.
+// The 16-bit paths run on MFMA; this one serves caches kept in fp32 (the contiguous
+// backend of an fp32 model, kv_cache.py:227-322, whose attention is torch SDPA in the
+// model's dtype), and the prefill of 16-bit pools at a head dim the MFMA prefill
+// kernel does not take (256): their elements are widened to fp32 as they are loaded
+// and the output rounded once when it is stored. It computes in fp32 with its
 // operands staged in LDS.
 //
 // A workgroup (256 threads) owns 16 query rows of one (sequence, KV head); rows are
@@ -24,6 +26,32 @@ namespace {
 constexpr int kRowsF = 16;
 constexpr int kKeysF = 32;
 constexpr int kThreadsF = 256;
+
+// Four consecutive elements of a pool, q or out row as fp32: T = float (fp32 pools,
+// 16-byte accesses) or a 16-bit tag (F16, BF16: 8-byte accesses, exact widening,
+// round-to-nearest-even narrowing).
+template <typename T>
+struct Vec4 {
+  using E = uint16_t;
+  __device__ static inline f32x4 load(const E* p) {
+    const u16x4 w = *reinterpret_cast<const u16x4*>(p);
+    return f32x4{T::to_f32(w[0]), T::to_f32(w[1]), T::to_f32(w[2]), T::to_f32(w[3])};
+  }
+  __device__ static inline void store(E* p, f32x4 v) {
+    u16x4 w;
+    w[0] = T::from_f32(v[0]);
+    w[1] = T::from_f32(v[1]);
+    w[2] = T::from_f32(v[2]);
+    w[3] = T::from_f32(v[3]);
+    *reinterpret_cast<u16x4*>(p) = w;
+  }
+};
+template <>
+struct Vec4<float> {
+  using E = float;
+  __device__ static inline f32x4 load(const E* p) { return *reinterpret_cast<const f32x4*>(p); }
+  __device__ static inline void store(E* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+};
 
 // Row of q / out holding new token t (-1: a grid row out of range, not read or written).
 __device__ inline int64_t f32_grid_row(const AttnF32Args& p, int t) {
@@ -74,8 +102,14 @@ __device__ inline bool locate_f32(const AttnF32Args& p, int g, int& b, int& tile
   return false;
 }
 
-template <int D>
+template <typename T, int D>
 __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p) {
+  using VE = Vec4<T>;
+  using E = typename VE::E;
+  const E* q_src = reinterpret_cast<const E*>(p.q);
+  const E* k_src = reinterpret_cast<const E*>(p.k_pool);
+  const E* v_src = reinterpret_cast<const E*>(p.v_pool);
+  E* out = reinterpret_cast<E*>(p.out);
   constexpr int kPitch = D + 4;     // floats; 16 B row padding against bank conflicts
   constexpr int kCols = D / 16;     // output columns per thread
   __shared__ __attribute__((aligned(16))) float q_lds[kRowsF * kPitch];
@@ -87,7 +121,7 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
   const int64_t work = (int64_t)p.row_tiles * p.num_kv_heads;
   if ((int64_t)blockIdx.x >= work) {  // a padded grid's pad rows: one workgroup per sequence
     if (p.q_rows && blockIdx.y == 0)
-      zero_pad_rows(p.qo_indptr, p.q_rows, p.grid_width, (int)(blockIdx.x - work), p.out, p.out_stride,
+      zero_pad_rows(p.qo_indptr, p.q_rows, p.grid_width, (int)(blockIdx.x - work), out, p.out_stride,
                     (int64_t)p.num_qo_heads * D, (int64_t)p.batch * p.grid_width);
     return;
   }
@@ -123,7 +157,7 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
     if (row < nrows) {
       const int t = row / G, g = row % G;
       const int64_t qr = f32_grid_row(p, q0 + t);
-      if (qr >= 0) v = *reinterpret_cast<const f32x4*>(p.q + qr * p.q_stride + (int64_t)(h * G + g) * D + 4 * c);
+      if (qr >= 0) v = VE::load(q_src + qr * p.q_stride + (int64_t)(h * G + g) * D + 4 * c);
     }
     *reinterpret_cast<f32x4*>(&q_lds[i * kPitch + 4 * c]) = v;
   }
@@ -148,8 +182,8 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
       int pid = idx[key / ps];
       pid = (pid < 0 || (int64_t)pid >= p.num_pages) ? 0 : pid;
       const int64_t off = ((int64_t)pid * ps + key % ps) * row_elems + (int64_t)h * D + 4 * c;
-      *reinterpret_cast<f32x4*>(&k_lds[j * kPitch + 4 * c]) = *reinterpret_cast<const f32x4*>(p.k_pool + off);
-      *reinterpret_cast<f32x4*>(&v_lds[j * kPitch + 4 * c]) = *reinterpret_cast<const f32x4*>(p.v_pool + off);
+      *reinterpret_cast<f32x4*>(&k_lds[j * kPitch + 4 * c]) = VE::load(k_src + off);
+      *reinterpret_cast<f32x4*>(&v_lds[j * kPitch + 4 * c]) = VE::load(v_src + off);
     }
     __syncthreads();
     // scores of keys key0 + rj and key0 + rj + 16 for row ri
@@ -219,10 +253,9 @@ __global__ void __launch_bounds__(kThreadsF) attention_f32_kernel(AttnF32Args p)
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   const int64_t orr = f32_grid_row(p, q0 + t);
   if (orr < 0) return;
-  float* orow = p.out + orr * p.out_stride + (int64_t)(h * G + g) * D + rj * kCols;
+  E* orow = out + orr * p.out_stride + (int64_t)(h * G + g) * D + rj * kCols;
 #pragma unroll
-  for (int c = 0; c < kCols; c += 4)
-    *reinterpret_cast<f32x4*>(orow + c) = f32x4{o[c] * inv, o[c + 1] * inv, o[c + 2] * inv, o[c + 3] * inv};
+  for (int c = 0; c < kCols; c += 4) VE::store(orow + c, f32x4{o[c] * inv, o[c + 1] * inv, o[c + 2] * inv, o[c + 3] * inv});
 }
 
 // Merge of the splits of one (query token, query head) row: one wave, lanes over D.
@@ -289,15 +322,28 @@ int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipSt
   if (a.splits > 1 && (!a.part_o || !a.part_ml)) return fail(NSLG_EWORKSPACE, "attention_f32: no workspace");
   if (a.q_rows && (a.splits != 1 || !a.qo_indptr || a.grid_width < 1))
     return fail(NSLG_EINVAL, "attention_f32: a padded grid needs ragged rows, a width and one split");
+  if (a.dtype != NSLG_F32 && a.dtype != NSLG_F16 && a.dtype != NSLG_BF16)
+    return fail(NSLG_EUNSUPPORTED, "attention_f32: dtype %d", a.dtype);
+  if (a.dtype != NSLG_F32 && a.splits != 1)
+    return fail(NSLG_EINVAL, "attention_f32: 16-bit pools take one split (prefill)");
   AttnF32Args p = a;
   p.row_tiles = (int32_t)tiles;
   const int64_t pad_wgs = a.q_rows ? a.batch : 0;
   if (tiles * a.num_kv_heads + pad_wgs > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "attention_f32: too many rows");
   const dim3 grid((unsigned)(tiles * a.num_kv_heads + pad_wgs), (unsigned)a.splits);
-  switch (head_dim) {
-    case 64: attention_f32_kernel<64><<<grid, kThreadsF, 0, s>>>(p); break;
-    case 128: attention_f32_kernel<128><<<grid, kThreadsF, 0, s>>>(p); break;
-    default: attention_f32_kernel<256><<<grid, kThreadsF, 0, s>>>(p); break;
+  if (a.dtype == NSLG_F32) {
+    switch (head_dim) {
+      case 64: attention_f32_kernel<float, 64><<<grid, kThreadsF, 0, s>>>(p); break;
+      case 128: attention_f32_kernel<float, 128><<<grid, kThreadsF, 0, s>>>(p); break;
+      default: attention_f32_kernel<float, 256><<<grid, kThreadsF, 0, s>>>(p); break;
+    }
+  } else if (head_dim != 256) {
+    return fail(NSLG_EUNSUPPORTED, "attention_f32: 16-bit pools at head_dim 256 only (the MFMA kernels take %d)",
+                head_dim);
+  } else if (a.dtype == NSLG_F16) {
+    attention_f32_kernel<F16, 256><<<grid, kThreadsF, 0, s>>>(p);
+  } else {
+    attention_f32_kernel<BF16, 256><<<grid, kThreadsF, 0, s>>>(p);
   }
   int rc = check_launch("attention_f32");
   if (rc || a.splits == 1) return rc;

@@ -574,11 +574,14 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
     return fail(NSLG_EINVAL, "paged_prefill: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_prefill: GQA group %d > 16", group);
-  if (dtype == NSLG_F32) {
-    // fp32 pools: the fp32 attention kernel, ragged rows, bottom-right causal
+  if (dtype == NSLG_F32 || ((dtype == NSLG_F16 || dtype == NSLG_BF16) && head_dim == 256)) {
+    // fp32 pools, and 16-bit pools at D = 256 (two stages of 128-key K/V tiles and two
+    // 16-row column blocks per wave do not fit a CU there): the VALU attention kernel,
+    // ragged rows, bottom-right causal
     if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
       return fail(NSLG_EINVAL, "paged_prefill: row stride smaller than Hq*D");
     AttnF32Args a;
+    a.dtype = dtype;
     a.q = (const float*)q;
     a.q_stride = q_stride;
     a.qo_indptr = qo_indptr;
@@ -607,7 +610,7 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   if (dtype != NSLG_F16 && dtype != NSLG_BF16)
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: dtype %d", dtype);
   if (head_dim != 64 && head_dim != 128)
-    return fail(NSLG_EUNSUPPORTED, "paged_prefill: head_dim %d (64 or 128)", head_dim);
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill: head_dim %d (64, 128 or 256)", head_dim);
   if (num_kv_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many KV heads");
   if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
     return fail(NSLG_EINVAL, "paged_prefill: row stride smaller than Hq*D");

@@ -19,10 +19,11 @@ _DTYPE_CODE = {torch.float16: _lib.NSLG_F16, torch.bfloat16: _lib.NSLG_BF16, tor
 # decode batches of other pools are decoded per sequence.
 GROUPED_DECODE_DTYPES = (torch.float16, torch.bfloat16)
 # head dims each pool dtype supports on every entry point a cache uses: decode,
-# RoPE append and fp32 attention take 64, 128 and 256; the 16-bit prefill kernel
-# 64 and 128 (at 256 its two 16-row column blocks per wave and the 128-key LDS
-# tiles do not fit one CU)
-HEAD_DIMS = {torch.float16: (64, 128), torch.bfloat16: (64, 128), torch.float32: (64, 128, 256)}
+# RoPE append and the VALU attention kernel take 64, 128 and 256; the 16-bit MFMA
+# prefill kernel 64 and 128 (at 256 its two 16-row column blocks per wave and the
+# 128-key LDS tiles do not fit one CU), and 16-bit prefill at 256 runs on the VALU
+# kernel
+HEAD_DIMS = {torch.float16: (64, 128, 256), torch.bfloat16: (64, 128, 256), torch.float32: (64, 128, 256)}
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -115,6 +115,48 @@ def test_prefill_attend_checks_the_callers_tensors():
     check_state(mgr, ref, ids)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_head_dim_256_prefill_then_decode(dtype):
+    """A 16-bit cache at head_dim 256: a ragged prefill and a chunk over cached
+    context (the VALU attention kernel), then decode steps (the MFMA decode), against
+    the oracle: outputs within the tolerance, pad rows zero, pool bytes equal."""
+    _log(f"cache: head_dim 256 {dtype}")
+    from nanoslg_amd import kv_cache as KC
+    Dh, Hq, Hkv, ps, pages = 256, 16, 4, 16, 64
+    cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=Hkv, num_qo_heads=Hq, head_dim=Dh, page_size=ps,
+                           max_pages=pages, dtype=dtype, device=DEV, enable_prefix_caching=False, backend="paged")
+    mgr = KC.PagedKVCache(cfg)
+    ref = O.PagedRef(1, pages, ps, Hkv, Dh, torch.float32, enable_prefix_caching=False)
+    g = torch.Generator().manual_seed(256)
+    ids = ["a", "b"]
+    for sid in ids:
+        mgr.allocate_sequence(sid)
+        ref.allocate_sequence(sid)
+    for ntok in ([37, 100], [20, 5], [1, 1], [1, 1], [1, 1]):
+        S = max(ntok)
+        q = torch.randn(2, S, Hq, Dh, generator=g).to(dtype)
+        k = torch.randn(2, S, Hkv, Dh, generator=g).to(dtype)
+        v = torch.randn(2, S, Hkv, Dh, generator=g).to(dtype)
+        c1 = mgr.begin_forward(ids, ntok)
+        c2 = ref.begin_forward(ids, ntok)
+        o1 = c1.attend(0, q.to(DEV), k.to(DEV), v.to(DEV), Hq, Hkv).float().cpu()
+        o2 = c2.attend(0, q.float(), k.float(), v.float(), Hq, Hkv)
+        for b in range(2):
+            torch.testing.assert_close(o1[b, :ntok[b]], o2[b, :ntok[b]], atol=ATOL, rtol=RTOL)
+            assert not o1[b, ntok[b]:].any()
+        mgr.end_forward(c1)
+        ref.end_forward(c2)
+    torch.cuda.synchronize()
+    kpool, vpool = mgr.pool.k.cpu(), mgr.pool.v.cpu()
+    for sid in ids:
+        st = mgr.seqs[sid]
+        bt, n = st.block_table, st.num_tokens
+        k1 = torch.stack([kpool[0, bt[t // ps], t % ps] for t in range(n)])
+        v1 = torch.stack([vpool[0, bt[t // ps], t % ps] for t in range(n)])
+        k2, v2 = ref.logical_kv(sid, 0)
+        assert torch.equal(k1.float(), k2) and torch.equal(v1.float(), v2)
+
+
 def test_paged_prefill_then_decode():
     _log("cache: prefill + decode")
     g = torch.Generator().manual_seed(0)

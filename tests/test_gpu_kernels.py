@@ -250,7 +250,7 @@ def _prefill_case(lens, news, Hq, Hkv, D, ps, dtype, seed, scale=None, max_q=Non
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 def test_prefill_from_zero(dtype, D):
     _log(f"prefill from zero dtype={dtype} D={D}")
     out, ref = _prefill_case([37, 100, 1], [37, 100, 1], 32, 8, D, 16, dtype, seed=31 + D)
@@ -295,6 +295,17 @@ def test_prefill_row_tile_orders():
         torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_head_dim_256_chunk_over_cached_context(dtype):
+    """16-bit pools at head_dim 256 (the VALU kernel): chunks over cached context,
+    GQA 4, page sizes 16 and 1, against the oracle."""
+    _log(f"prefill D=256 {dtype}")
+    out, ref = _prefill_case([300, 1000, 64, 17], [64, 200, 64, 3], 32, 8, 256, 16, dtype, seed=61)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    out, ref = _prefill_case([90, 40], [30, 40], 16, 4, 256, 1, dtype, seed=62)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+
+
 def test_prefill_sequence_without_new_tokens():
     _log("prefill n=0 rows")
     out, ref = _prefill_case([50, 20, 33], [5, 0, 33], 32, 8, 128, 16, torch.float16, seed=52, scale=0.1)
@@ -302,7 +313,7 @@ def test_prefill_sequence_without_new_tokens():
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64), (torch.float32, 128),
-                                     (torch.float32, 256)])
+                                     (torch.float32, 256), (torch.bfloat16, 256)])
 def test_prefill_grid_rows_bit_exact(dtype, D):
     """nslg_paged_prefill_grid on a padded [B, S] grid (left and right padding, a
     sequence without new tokens, a full row) against nslg_paged_prefill on the ragged

@@ -402,11 +402,12 @@ def test_release_many_equals_one_release_per_page():
 
 
 def test_unsupported_head_dim_is_rejected_at_construction():
-    """A GPU cache whose dtype and head_dim some kernel it uses does not support (the
-    16-bit prefill: head_dim 64 or 128) is refused when it is built, not at its first
-    prefill; fp32 pools take 256."""
+    """A GPU cache whose dtype and head_dim some kernel it uses does not support (64,
+    128 and 256 for every pool dtype) is refused when it is built, not at its first
+    prefill."""
     from nanoslg_amd import kernels as K
-    for dt, hd, ok in ((torch.float16, 256, False), (torch.bfloat16, 96, False), (torch.float16, 128, True),
+    for dt, hd, ok in ((torch.float16, 96, False), (torch.bfloat16, 96, False), (torch.float32, 32, False),
+                       (torch.float16, 128, True), (torch.float16, 256, True), (torch.bfloat16, 256, True),
                        (torch.float32, 256, True), (torch.bfloat16, 64, True)):
         cfg = KC.KVCacheConfig(1, 2, 4, hd, page_size=16, max_pages=8, dtype=dt, device=None)
         cfg.device = torch.device("cuda", 0)  # the check only; nothing is allocated here
