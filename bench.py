@@ -41,6 +41,12 @@ HBM_PEAK_GBS = 8000.0
 # (profiles/paged_decode_hbm_traffic_kv_pressure_b64.md). `traffic` in the JSON line is
 # this ratio times the algorithmic bytes of the run being reported.
 TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0113}
+# The same for the chunked-prefill kernel over the 8 chunks of a batch (q, out, the
+# K/V of every visible key once and the page ids): FETCH_SIZE and WRITE_SIZE of
+# `bench.py --workload prefill --steps 4 --warmup 8`, scaled as above
+# (profiles/paged_prefill_chunked_b8x4096.md). Above 1 because the row tiles of one
+# KV head re-fetch its K/V once it leaves the XCD's L2.
+PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE = 1.472
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -834,6 +840,17 @@ def prefill_flops(B, L, Hq, D, start=0, n=None):
     return 4 * Hq * D * B * keys
 
 
+def prefill_bytes(B, L, CH, Hq, Hkv, D, ps):
+    """Algorithmic HBM bytes of the prefill kernel over the L // CH chunks of a batch
+    (fp16): per chunk q read and out written once, the K and V of every key the chunk
+    sees (its own and the earlier chunks') read once, and their page ids."""
+    total = 0
+    for c in range(L // CH):
+        keys = (c + 1) * CH
+        total += 2 * B * CH * Hq * D * 2 + B * keys * Hkv * D * 2 * 2 + 4 * B * (keys // ps)
+    return total
+
+
 def run_prefill(args):
     """Chunked prefill: 8 sequences x 4096 tokens, each fed as 8 chunks of 512 through
     the drop-in API (begin_forward -> attend -> end_forward): every chunk appends its
@@ -901,6 +918,7 @@ def run_prefill(args):
     timed.recording = False
     kernel_ms = timed.total_ms() / steps
     achieved = flops / (kernel_ms * 1e-3) / 1e12
+    alg_per_launch = prefill_bytes(B, L, CH, HQ, HKV, D, PS) / nchunks
     _log(f"prefill kernel: {kernel_ms:.3f} ms per 8 chunks ({len(timed.events)} launches), {achieved:.1f} TFLOP/s")
     res = {
         "metric": "chunked prefill attention: TFLOP/s (causal, algorithmic) and prefill tok/s/layer",
@@ -927,7 +945,8 @@ def run_prefill(args):
             "peak": MFMA_F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": int(round(PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE * alg_per_launch)),
+            "algorithmic_bytes_per_launch": int(alg_per_launch),
             "avg_launch_us": round(timed.mean_ms() * 1e3, 2),
         },
     }
