@@ -41,7 +41,11 @@ enum nslg_status {
   NSLG_EINVAL = -1,      /* bad pointer / size / stride */
   NSLG_EUNSUPPORTED = -2,/* shape or dtype this build has no kernel for */
   NSLG_ELAUNCH = -3,     /* the HIP launch itself failed */
-  NSLG_EWORKSPACE = -4   /* workspace too small */
+  NSLG_EWORKSPACE = -4,  /* workspace too small */
+  NSLG_ECAPTURE = -5     /* the call's first use of a kernel variant on a device would
+                            query the device while its stream is being captured into a
+                            graph: make one call (or a workspace-size query) outside
+                            the capture first */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -133,6 +137,10 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
  * KV head and key split, then an fp32 merge, for caches kept in fp32 such as the
  * contiguous backend of an fp32 model, kv_cache.py:227-322); D in {64, 128, 256};
  * 1 <= Hq/Hkv <= 16. A sequence with no tokens gets zeros.
+ * The first f16/bf16 call of a (dtype, head_dim, page_size) variant on a device
+ * (or the first workspace-size query for it) queries the device's occupancy
+ * once; a decode call that would do so while its stream is being captured into
+ * a graph returns NSLG_ECAPTURE and launches nothing.
  */
 size_t nslg_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads,
                                         int32_t num_kv_heads, int32_t head_dim,

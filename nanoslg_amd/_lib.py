@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libnslg_kv.so"
 
 NSLG_F16, NSLG_BF16, NSLG_F32 = 0, 1, 2
 NSLG_EWORKSPACE = -4
+NSLG_ECAPTURE = -5  # a variant's first use on a device inside a stream capture
 NSLG_NOALLOC_SCRATCH_BYTES = 16 << 20  # the static scratch of nslg_paged_decode_noalloc
 
 _I32P = POINTER(c_int32)

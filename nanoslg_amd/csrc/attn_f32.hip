@@ -307,9 +307,11 @@ size_t attention_f32_workspace(int64_t total_q, int32_t num_qo_heads, int32_t he
 
 int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipStream_t s) {
   if (a.group > kRowsF * 64) return fail(NSLG_EUNSUPPORTED, "attention_f32: GQA group %d", a.group);
+  // 16-byte rows: the kernel's vector accesses and the pad-row zeroing (16-byte stores)
+  const int64_t esize = a.dtype == NSLG_F32 ? 4 : 2;
   if (((uintptr_t)a.q | (uintptr_t)a.k_pool | (uintptr_t)a.v_pool | (uintptr_t)a.out) & 15 ||
-      a.q_stride % 4 || a.out_stride % 4)
-    return fail(NSLG_EINVAL, "attention_f32: q/pool/out must be 16-byte aligned with row strides of 4k floats");
+      (a.q_stride * esize) % 16 || (a.out_stride * esize) % 16)
+    return fail(NSLG_EINVAL, "attention_f32: q/pool/out must be 16-byte aligned with row strides of 16 bytes");
   if (a.num_pages * (int64_t)a.page_size >= ((int64_t)1 << 31))
     return fail(NSLG_EUNSUPPORTED, "attention_f32: pool has >= 2^31 token slots");
   // row-tile slots per KV head: an upper bound over the batch (every sequence may

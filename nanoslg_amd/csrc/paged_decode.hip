@@ -818,12 +818,30 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(MergeParams p, GroupA
 constexpr int kMaxDevices = 64;
 constexpr int kDefaultSlots = 768;
 
+// Whether a call may be inside a stream capture (a launch on `stream`), and the stream.
+struct CaptureCheck {
+  bool check = false;
+  hipStream_t stream = nullptr;
+};
+
+inline bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
 // Calls whose K/V (both, all KV heads) exceed this stream them with non-temporal
 // loads; smaller ones are left in the caches (MI355X: 256 MB of memory-side cache).
 constexpr int64_t kStreamBytes = (int64_t)128 << 20;
 
+// The first call of a variant on a device queries the device (attribute and
+// occupancy); a call whose stream is being captured into a graph must not make
+// those queries, so it returns 0 (refused) when the figure is not cached yet.
 template <typename T, int D, bool kTileInPage, bool kGrouped>
-int decode_wg_slots(int waves) {
+int decode_wg_slots(int waves, const CaptureCheck& cc) {
   static std::atomic<int> cache[kMaxDevices][kMaxWaves + 1];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
@@ -832,6 +850,7 @@ int decode_wg_slots(int waves) {
   }
   int v = cache[dev][waves].load(std::memory_order_relaxed);
   if (v > 0) return v;
+  if (cc.check && stream_capturing(cc.stream)) return 0;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, kTileInPage, 2, kGrouped>,
@@ -846,6 +865,7 @@ int decode_wg_slots(int waves) {
 }
 
 struct DecodeShape {
+  bool refused = false;  // the variant's first use happened inside a stream capture
   int waves;         // waves (KV heads) per workgroup
   int head_groups;   // workgroups per chunk
   int chunk_tokens;  // upper bound passed to the kernel
@@ -863,12 +883,17 @@ struct DecodeShape {
 // length. Lengths are multiples of 16 (tiles never straddle a chunk) and at
 // least 64.
 template <typename T, int D, bool kGrouped>
-DecodeShape decode_shape(int32_t units, int32_t num_kv_heads, int64_t total_tokens, int page_size) {
+DecodeShape decode_shape(int32_t units, int32_t num_kv_heads, int64_t total_tokens, int page_size,
+                         const CaptureCheck& cc) {
   DecodeShape sh;
   sh.waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
   sh.head_groups = (num_kv_heads + sh.waves - 1) / sh.waves;
-  const int slots = page_size % 16 == 0 ? decode_wg_slots<T, D, true, kGrouped>(sh.waves)
-                                        : decode_wg_slots<T, D, false, kGrouped>(sh.waves);
+  const int slots = page_size % 16 == 0 ? decode_wg_slots<T, D, true, kGrouped>(sh.waves, cc)
+                                        : decode_wg_slots<T, D, false, kGrouped>(sh.waves, cc);
+  if (slots <= 0) {  // refused: first use of the variant inside a stream capture
+    sh.refused = true;
+    return sh;
+  }
   int64_t capacity = slots / sh.head_groups;
   if (capacity < 1) capacity = 1;
   const bool fit = capacity > 2 * (int64_t)units;
@@ -885,20 +910,20 @@ DecodeShape decode_shape(int32_t units, int32_t num_kv_heads, int64_t total_toke
 
 template <typename T, bool kGrouped>
 DecodeShape decode_shape_for(int32_t head_dim, int32_t units, int32_t num_kv_heads, int64_t total_tokens,
-                             int page_size) {
+                             int page_size, const CaptureCheck& cc) {
   switch (head_dim) {
-    case 64: return decode_shape<T, 64, kGrouped>(units, num_kv_heads, total_tokens, page_size);
-    case 128: return decode_shape<T, 128, kGrouped>(units, num_kv_heads, total_tokens, page_size);
-    default: return decode_shape<T, 256, kGrouped>(units, num_kv_heads, total_tokens, page_size);
+    case 64: return decode_shape<T, 64, kGrouped>(units, num_kv_heads, total_tokens, page_size, cc);
+    case 128: return decode_shape<T, 128, kGrouped>(units, num_kv_heads, total_tokens, page_size, cc);
+    default: return decode_shape<T, 256, kGrouped>(units, num_kv_heads, total_tokens, page_size, cc);
   }
 }
 
 template <bool kGrouped>
 DecodeShape shape_of(int32_t dtype, int32_t head_dim, int32_t units, int32_t num_kv_heads, int64_t total_tokens,
-                     int page_size) {
+                     int page_size, const CaptureCheck& cc = CaptureCheck{}) {
   return dtype == NSLG_BF16
-             ? decode_shape_for<BF16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size)
-             : decode_shape_for<F16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size);
+             ? decode_shape_for<BF16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size, cc)
+             : decode_shape_for<F16, kGrouped>(head_dim, units, num_kv_heads, total_tokens, page_size, cc);
 }
 
 template <typename T, int D, bool kGrouped>
@@ -1057,8 +1082,16 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     return fail(NSLG_EINVAL, "paged_decode: q/pool/out must be 16-byte aligned");
   const int64_t total_tokens = total_pages * page_size;
   if (total_tokens >= (int64_t)1 << 31) return fail(NSLG_EUNSUPPORTED, "paged_decode: >2^31 tokens");
+  CaptureCheck cc;
+  cc.check = true;
+  cc.stream = as_stream(stream);
   const DecodeShape sh =
-      shape_of<kGrouped>(dtype, head_dim, batch + num_groups, num_kv_heads, total_tokens, page_size);
+      shape_of<kGrouped>(dtype, head_dim, batch + num_groups, num_kv_heads, total_tokens, page_size, cc);
+  if (sh.refused)
+    return fail(NSLG_ECAPTURE,
+                "paged_decode: first call of this variant (dtype %d, head_dim %d, page_size %d) is inside a "
+                "stream capture; make one call, or a workspace-size query, outside the capture first",
+                dtype, head_dim, page_size);
   const int64_t mc = sh.max_chunks;
   const size_t need = workspace_bytes_for(sh, batch, num_qo_heads, head_dim, slot_members, num_groups);
   if (!workspace || workspace_bytes < need)

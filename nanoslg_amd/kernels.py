@@ -24,6 +24,9 @@ GROUPED_DECODE_DTYPES = (torch.float16, torch.bfloat16)
 # 128-key LDS tiles do not fit one CU), and 16-bit prefill at 256 runs on the VALU
 # kernel
 HEAD_DIMS = {torch.float16: (64, 128, 256), torch.bfloat16: (64, 128, 256), torch.float32: (64, 128, 256)}
+# (dtype, head_dim) pairs whose prefill runs on the VALU attention kernel although the
+# dtype has an MFMA prefill at other head dims: tens of times slower per token
+VALU_PREFILL = {(torch.float16, 256), (torch.bfloat16, 256)}
 
 
 def dtype_code(dt: torch.dtype) -> int:

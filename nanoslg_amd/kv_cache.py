@@ -24,8 +24,11 @@ host-to-device copy. There is no CPU attention path.
 """
 from __future__ import annotations
 
+import gc
 import math
 import threading
+import warnings
+import weakref
 from abc import ABC, abstractmethod
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -44,6 +47,11 @@ def _check_head_dim(cfg: "KVCacheConfig", kernels) -> None:
     if dims is not None and dev is not None and dev.type == "cuda" and cfg.head_dim not in dims.get(cfg.dtype, ()):
         raise ValueError(f"KV cache: head_dim {cfg.head_dim} is not supported for {cfg.dtype} "
                          f"(supported: {dims.get(cfg.dtype, ())})")
+    slow = getattr(kernels, "VALU_PREFILL", ())
+    if dev is not None and dev.type == "cuda" and (cfg.dtype, cfg.head_dim) in slow:
+        warnings.warn(f"KV cache: prefill at head_dim {cfg.head_dim} in {cfg.dtype} runs on the VALU attention "
+                      f"kernel (no MFMA prefill for this head_dim), tens of times slower per token than at "
+                      f"head_dim 128; decode is unaffected", RuntimeWarning, stacklevel=3)
 
 
 def _default_kernels():
@@ -1865,10 +1873,16 @@ class _GraphPlan:
 
 class _GraphDecodeContext(CacheContext):
     """The context a captured decode step's attend calls run on: its plan tensors
-    are static (the graph's), its host attributes are refreshed every step."""
+    are static (the graph's), its host attributes are refreshed every step.
+
+    It refers to its graph weakly: the graph holds its contexts, and a strong
+    reference back would make every DecodeGraph a reference cycle, destroyed only
+    by Python's cyclic collector at an arbitrary later time, possibly while another
+    graph is being captured, when the HIP calls its destruction makes (graph
+    teardown, the pinned page-list buffers' stream events) are not allowed."""
 
     def __init__(self, graph: "DecodeGraph", plan: _GraphPlan, launch):
-        self._graph, self._plan_t, self._launch = graph, plan, launch
+        self._graph, self._plan_t, self._launch = weakref.ref(graph), plan, launch
         self.seq_ids = list(graph.seq_ids)
         self.batch_size = len(self.seq_ids)
         self.new_token_counts = [1] * self.batch_size
@@ -1890,7 +1904,7 @@ class _GraphDecodeContext(CacheContext):
     def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):
         B = q.shape[0]
         # replays rotate at positions the captured tables must hold (step() checks)
-        g = self._graph
+        g = self._graph()
         g.rope_rows = cos.shape[0] if g.rope_rows is None else min(g.rope_rows, cos.shape[0])
         if self.seq_lens and max(self.seq_lens) > cos.shape[0]:
             raise IndexError(f"position {max(self.seq_lens) - 1} is outside the rope tables ({cos.shape[0]} rows)")
@@ -1967,19 +1981,30 @@ class DecodeGraph:
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         torch.cuda.synchronize(dev)
-        with torch.cuda.stream(side):
-            for i in range(2):  # graph i: plan i -> plan 1-i, then the forward on plan 1-i
-                src, dst = self.plans[i], self.plans[1 - i]
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=side):
-                    # this step's page list: pinned host memory -> device (a copy node of
-                    # the graph; measured faster than the planner reading host memory)
-                    self.new_dev[i].copy_(self.new_host[i], non_blocking=True)
-                    kern._decode_plan_step_device(src.indptr, src.indices, src.lpl, self.new_dev[i], B, ps, dst,
-                                                  self.pool_args)
-                    out = forward(self.ctxs[i])
-                self.graphs.append(g)
-                self.outputs.append(out)
+        # No object may be destroyed by the cyclic collector while a graph is being
+        # captured: unreachable cycles holding graphs, pinned buffers or events (an
+        # earlier DecodeGraph of the caller's, say) are collected now, and the
+        # collector stays off until both captures have ended.
+        gc.collect()
+        gc_was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.stream(side):
+                for i in range(2):  # graph i: plan i -> plan 1-i, then the forward on plan 1-i
+                    src, dst = self.plans[i], self.plans[1 - i]
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=side):
+                        # this step's page list: pinned host memory -> device (a copy node of
+                        # the graph; measured faster than the planner reading host memory)
+                        self.new_dev[i].copy_(self.new_host[i], non_blocking=True)
+                        kern._decode_plan_step_device(src.indptr, src.indices, src.lpl, self.new_dev[i], B, ps,
+                                                      dst, self.pool_args)
+                        out = forward(self.ctxs[i])
+                    self.graphs.append(g)
+                    self.outputs.append(out)
+        finally:
+            if gc_was_enabled:
+                gc.enable()
         torch.cuda.current_stream(dev).wait_stream(side)
         self.parity = 0
         self.steps = 0

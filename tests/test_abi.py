@@ -180,3 +180,17 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
     with pytest.raises(_lib.KernelLibraryError):
         _lib.load()
+
+
+def test_attention_kernel_rejects_rows_not_16_byte_aligned():
+    """The VALU attention path (fp32 pools, 16-bit prefill at head_dim 256) takes only
+    row strides of whole 16-byte units for q and out: its vector accesses and the
+    padded grid's pad-row zeroing store 16 bytes at a time."""
+    from nanoslg_amd import _lib
+    lib = _lib.load()
+    A = 4096
+    for dt, D, q_stride, out_stride in ((0, 256, 512, 516), (0, 256, 516, 512), (2, 128, 256, 258)):
+        rc = lib.nslg_paged_prefill_grid(A, q_stride, A, A, 8, 10, 8, A, A, 100, 16, A, A, A, 2, 2, 1, D, 0.1,
+                                         dt, A, out_stride, None, 0, None)
+        assert rc == -1 and "16-byte" in _lib.last_error(), (dt, q_stride, out_stride, _lib.last_error())
+    assert _lib.NSLG_ECAPTURE == -5

@@ -772,3 +772,44 @@ def test_pages_written_in_full_skip_the_owed_zeroing():
         for p1, p2 in zip(bt1, bt2):
             assert torch.equal(mgr.pool.k[:, p1], ref.pool.k[:, p2])
             assert torch.equal(mgr.pool.v[:, p1], ref.pool.v[:, p2])
+
+
+def test_graph_context_refers_to_its_graph_weakly():
+    """A DecodeGraph holds its step contexts and the contexts refer back to it weakly:
+    a graph is freed by reference counting when its caller drops it, never later by
+    the cyclic collector, which could run while another graph is being captured."""
+    import gc
+    import weakref
+
+    class Holder:  # holds its contexts as DecodeGraph does
+        seq_ids = ["a", "b"]
+        rope_rows = None
+
+    h = Holder()
+    h.ctxs = [KC._GraphDecodeContext(h, None, None) for _ in range(2)]
+    assert h.ctxs[0]._graph() is h
+    wr = weakref.ref(h)
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        del h
+        assert wr() is None
+    finally:
+        if was:
+            gc.enable()
+
+
+def test_valu_prefill_head_dims_warn_at_construction(monkeypatch):
+    """A 16-bit cache at head_dim 256 on a device warns once at construction that its
+    prefill runs on the VALU attention kernel; head_dim 128 builds silently."""
+    import warnings
+
+    from nanoslg_amd import kernels as K
+    kern = types.SimpleNamespace(HEAD_DIMS=K.HEAD_DIMS, VALU_PREFILL=K.VALU_PREFILL)
+    for D, warns in ((256, True), (128, False)):
+        cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=8, num_qo_heads=32, head_dim=D, page_size=16,
+                               max_pages=64, dtype=torch.float16, device="cuda:0")
+        with warnings.catch_warnings(record=True) as w:
+            warnings.simplefilter("always")
+            KC._check_head_dim(cfg, kern)
+        assert any("VALU" in str(x.message) for x in w) == warns, D
