@@ -61,6 +61,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true",
                     help="decode workloads: replay each step from captured HIP graphs (DecodeGraph)")
+    ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128, 256],
+                    help="prefill workload: head dim (heads scaled to keep Hq*D = 4096, Hkv*D = 1024)")
     return ap.parse_args()
 
 
@@ -861,6 +863,9 @@ def run_prefill(args):
     from nanoslg_amd import kernels
     from nanoslg_amd.kv_cache import KVCacheConfig, PagedKVCache
     B, L, CH = PREFILL_B, PREFILL_LEN, PREFILL_CHUNK
+    # the layer's width stays Llama-3.1-8B's (Hq*D = 4096, Hkv*D = 1024, GQA 4) at other head dims
+    D = args.head_dim
+    HQ, HKV = 4096 // D, 1024 // D
     nchunks = L // CH
     dev = torch.device("cuda:0")
     cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
@@ -945,7 +950,7 @@ def run_prefill(args):
             "peak": MFMA_F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-            "traffic": int(round(PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE * alg_per_launch)),
+            "traffic": (int(round(PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE * alg_per_launch)) if D == 128 else None),
             "algorithmic_bytes_per_launch": int(alg_per_launch),
             "avg_launch_us": round(timed.mean_ms() * 1e3, 2),
         },

@@ -1,10 +1,7 @@
 // Paged attention on the VALU (decode and causal chunked prefill alike), for gfx950.
 // The 16-bit paths run on MFMA; this one serves caches kept in fp32 (the contiguous
 // backend of an fp32 model, kv_cache.py:227-322, whose attention is torch SDPA in the
-// model's dtype), and the prefill of 16-bit pools at a head dim the MFMA prefill
-// kernel does not take (256): their elements are widened to fp32 as they are loaded
-// and the output rounded once when it is stored. It computes in fp32 with its
-// operands staged in LDS.
+// model's dtype). It computes in fp32 with its operands staged in LDS.
 //
 // A workgroup (256 threads) owns 16 query rows of one (sequence, KV head); rows are
 // packed GQA-style, row = token * G + g, so one K/V tile serves all G query heads of
@@ -27,25 +24,9 @@ constexpr int kRowsF = 16;
 constexpr int kKeysF = 32;
 constexpr int kThreadsF = 256;
 
-// Four consecutive elements of a pool, q or out row as fp32: T = float (fp32 pools,
-// 16-byte accesses) or a 16-bit tag (F16, BF16: 8-byte accesses, exact widening,
-// round-to-nearest-even narrowing).
+// Four consecutive elements of a pool, q or out row (fp32, 16-byte accesses).
 template <typename T>
-struct Vec4 {
-  using E = uint16_t;
-  __device__ static inline f32x4 load(const E* p) {
-    const u16x4 w = *reinterpret_cast<const u16x4*>(p);
-    return f32x4{T::to_f32(w[0]), T::to_f32(w[1]), T::to_f32(w[2]), T::to_f32(w[3])};
-  }
-  __device__ static inline void store(E* p, f32x4 v) {
-    u16x4 w;
-    w[0] = T::from_f32(v[0]);
-    w[1] = T::from_f32(v[1]);
-    w[2] = T::from_f32(v[2]);
-    w[3] = T::from_f32(v[3]);
-    *reinterpret_cast<u16x4*>(p) = w;
-  }
-};
+struct Vec4;
 template <>
 struct Vec4<float> {
   using E = float;
@@ -307,10 +288,11 @@ size_t attention_f32_workspace(int64_t total_q, int32_t num_qo_heads, int32_t he
 
 int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipStream_t s) {
   if (a.group > kRowsF * 64) return fail(NSLG_EUNSUPPORTED, "attention_f32: GQA group %d", a.group);
+  if (a.dtype != NSLG_F32)
+    return fail(NSLG_EUNSUPPORTED, "attention_f32: dtype %d (16-bit pools run on the MFMA kernels)", a.dtype);
   // 16-byte rows: the kernel's vector accesses and the pad-row zeroing (16-byte stores)
-  const int64_t esize = a.dtype == NSLG_F32 ? 4 : 2;
   if (((uintptr_t)a.q | (uintptr_t)a.k_pool | (uintptr_t)a.v_pool | (uintptr_t)a.out) & 15 ||
-      (a.q_stride * esize) % 16 || (a.out_stride * esize) % 16)
+      (a.q_stride * 4) % 16 || (a.out_stride * 4) % 16)
     return fail(NSLG_EINVAL, "attention_f32: q/pool/out must be 16-byte aligned with row strides of 16 bytes");
   if (a.num_pages * (int64_t)a.page_size >= ((int64_t)1 << 31))
     return fail(NSLG_EUNSUPPORTED, "attention_f32: pool has >= 2^31 token slots");
@@ -324,28 +306,15 @@ int attention_f32(const AttnF32Args& a, int64_t total_q, int32_t head_dim, hipSt
   if (a.splits > 1 && (!a.part_o || !a.part_ml)) return fail(NSLG_EWORKSPACE, "attention_f32: no workspace");
   if (a.q_rows && (a.splits != 1 || !a.qo_indptr || a.grid_width < 1))
     return fail(NSLG_EINVAL, "attention_f32: a padded grid needs ragged rows, a width and one split");
-  if (a.dtype != NSLG_F32 && a.dtype != NSLG_F16 && a.dtype != NSLG_BF16)
-    return fail(NSLG_EUNSUPPORTED, "attention_f32: dtype %d", a.dtype);
-  if (a.dtype != NSLG_F32 && a.splits != 1)
-    return fail(NSLG_EINVAL, "attention_f32: 16-bit pools take one split (prefill)");
   AttnF32Args p = a;
   p.row_tiles = (int32_t)tiles;
   const int64_t pad_wgs = a.q_rows ? a.batch : 0;
   if (tiles * a.num_kv_heads + pad_wgs > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "attention_f32: too many rows");
   const dim3 grid((unsigned)(tiles * a.num_kv_heads + pad_wgs), (unsigned)a.splits);
-  if (a.dtype == NSLG_F32) {
-    switch (head_dim) {
-      case 64: attention_f32_kernel<float, 64><<<grid, kThreadsF, 0, s>>>(p); break;
-      case 128: attention_f32_kernel<float, 128><<<grid, kThreadsF, 0, s>>>(p); break;
-      default: attention_f32_kernel<float, 256><<<grid, kThreadsF, 0, s>>>(p); break;
-    }
-  } else if (head_dim != 256) {
-    return fail(NSLG_EUNSUPPORTED, "attention_f32: 16-bit pools at head_dim 256 only (the MFMA kernels take %d)",
-                head_dim);
-  } else if (a.dtype == NSLG_F16) {
-    attention_f32_kernel<F16, 256><<<grid, kThreadsF, 0, s>>>(p);
-  } else {
-    attention_f32_kernel<BF16, 256><<<grid, kThreadsF, 0, s>>>(p);
+  switch (head_dim) {
+    case 64: attention_f32_kernel<float, 64><<<grid, kThreadsF, 0, s>>>(p); break;
+    case 128: attention_f32_kernel<float, 128><<<grid, kThreadsF, 0, s>>>(p); break;
+    default: attention_f32_kernel<float, 256><<<grid, kThreadsF, 0, s>>>(p); break;
   }
   int rc = check_launch("attention_f32");
   if (rc || a.splits == 1) return rc;

@@ -145,7 +145,7 @@ __device__ inline void zero_pad_rows(const int32_t* qo, const int32_t* q_rows, i
 
 // ---- fp32 attention (attn_f32.hip), shared by the decode and prefill entries ----
 struct AttnF32Args {
-  int32_t dtype = NSLG_F32;    // element type of q, the pools and out (16-bit: prefill at D = 256 only)
+  int32_t dtype = NSLG_F32;    // element type of q, the pools and out (fp32 only)
   const float* q;
   int64_t q_stride;            // elements between query tokens
   const int32_t* qo_indptr;    // [B+1] new-token offsets; null: one token per sequence

@@ -35,11 +35,26 @@
 namespace nslg {
 namespace {
 
-constexpr int kRowsPerWG = 256;  // query rows of a workgroup: 16 x kCB per wave
-constexpr int kKeys = 128;
 constexpr int kPageWin = 2048;                     // page ids per LDS window
 constexpr float kRescaleSlack = 8.0f;
-constexpr int kBlocks = kKeys / 32;                // 32-key blocks per tile
+
+// Tile shape per head dim: column blocks of 16 query rows per wave, keys per LDS
+// tile, waves per workgroup. D = 64, 128: two column blocks per wave and 128-key
+// tiles (256 rows per workgroup, two 128-key stages of K and V in LDS). D = 256:
+// one column block per wave (its Q, O, K and V operands fill the 256 registers of
+// 2 waves per SIMD) and 64-key tiles (two stages of 256-wide rows fit the LDS);
+// 128 rows per workgroup.
+template <int D>
+struct PrefillTile {
+  static constexpr int kCB = D == 256 ? 1 : 2;
+  static constexpr int kKeys = D == 256 ? 64 : 128;
+  static constexpr int kWaves = 8;
+  static constexpr int kRowsPerWG = 16 * kCB * kWaves;
+};
+
+inline int rows_per_wg(int head_dim) {
+  return head_dim == 256 ? PrefillTile<256>::kRowsPerWG : PrefillTile<128>::kRowsPerWG;
+}
 
 struct PrefillParams {
   const uint16_t* q;
@@ -70,6 +85,7 @@ struct PrefillParams {
   int32_t grid_width;
   int32_t pad_work;
   int32_t by_round;   // > 0: longest-first rounds of this many tiles per sequence (see below)
+  int32_t rows_wg;    // query rows per workgroup (the kernel's tile shape)
 };
 
 template <int N>
@@ -100,7 +116,7 @@ __device__ inline bool locate_tile_by_round(const PrefillParams& p, int g, int& 
   b = g % p.batch;
   const int r = g / p.batch;
   const int n = p.qo_indptr[b + 1] - p.qo_indptr[b];
-  const int nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+  const int nt = n > 0 ? (n * p.group + p.rows_wg - 1) / p.rows_wg : 0;
   if (r >= nt) return false;
   tile = nt - 1 - r;
   return true;
@@ -115,7 +131,7 @@ __device__ inline int most_tiles(const PrefillParams& p) {
     int nt = 0;
     if (s < p.batch) {
       const int n = p.qo_indptr[s + 1] - p.qo_indptr[s];
-      nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+      nt = n > 0 ? (n * p.group + p.rows_wg - 1) / p.rows_wg : 0;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) nt = max(nt, __shfl_xor(nt, off, 64));
@@ -133,7 +149,7 @@ __device__ inline bool locate_tile(const PrefillParams& p, int g, int& b, int& t
     int nt = 0;
     if (s < p.batch) {
       const int n = p.qo_indptr[s + 1] - p.qo_indptr[s];
-      nt = n > 0 ? (n * p.group + kRowsPerWG - 1) / kRowsPerWG : 0;
+      nt = n > 0 ? (n * p.group + p.rows_wg - 1) / p.rows_wg : 0;
     }
     int incl = nt;
 #pragma unroll
@@ -154,10 +170,14 @@ __device__ inline bool locate_tile(const PrefillParams& p, int g, int& b, int& t
   return false;
 }
 
-template <typename T, int D, int kCB>
-__global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_kernel(PrefillParams p) {
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_kernel(PrefillParams p) {
+  constexpr int kCB = PrefillTile<D>::kCB;
+  constexpr int kKeys = PrefillTile<D>::kKeys;
+  constexpr int kWaves = PrefillTile<D>::kWaves;
+  constexpr int kRowsPerWG = PrefillTile<D>::kRowsPerWG;
   constexpr int kRowsPerWave = 16 * kCB;  // kCB column blocks of 16 rows
-  constexpr int kWaves = kRowsPerWG / kRowsPerWave;
+  constexpr int kBlocks = kKeys / 32;     // 32-key blocks per tile
   constexpr int kThreads = 64 * kWaves;
   constexpr int kSteps = D / 32;
   constexpr int NT = D / 16;
@@ -168,6 +188,7 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
   constexpr int kPitch = D + 16;
   constexpr int kVPitch = D + 16;
   constexpr bool kSplitP = T::kDtype == NSLG_BF16;
+  constexpr bool kLean = D == 256;
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKeys * kPitch];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kVPitch];
@@ -428,6 +449,53 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
 
   };
 
+  // D = 256 (lean): scores of one 16-key half at a time, P.V over half the output
+  // tiles at a time, each with its operands read from LDS just before
+  auto qk_lean = [&](int stage, int kb, f32x4 (&sacc)[kCB][2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      u16x8 kh[kSteps];
+      const uint16_t* krow = &k_lds[stage][(32 * kb + 16 * t + r) * kPitch + 8 * gq];
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) kh[s] = *reinterpret_cast<const u16x8*>(krow + 32 * s);
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        sacc[cb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) sacc[cb][t] = T::mma_k32(kh[s], qb[cb][s], sacc[cb][t]);
+      }
+    }
+  };
+  auto pv_lean = [&](int stage, int kb, const u16x8 (&pb)[kCB], const u16x8 (&pb_lo)[kCB]) {
+    const uint16_t* vsrc = &v_lds[stage][(32 * kb + 4 * gq + (r >> 2)) * kVPitch + 4 * (r & 3)];
+    constexpr int kHalfNT = NT / 2;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      u16x8 va[kHalfNT];
+#pragma unroll
+      for (int n = 0; n < kHalfNT; ++n) {
+        typedef short i16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) i16x4* lds_i16x4;
+        const uint16_t* vp = vsrc + 16 * (hh * kHalfNT + n);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)vp);
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(vp + 16 * kVPitch));
+        va[n] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+        for (int n = 0; n < kHalfNT; ++n) {
+          o[cb][hh * kHalfNT + n] = T::mma_k32(va[n], pb[cb], o[cb][hh * kHalfNT + n]);
+          if constexpr (kSplitP) o[cb][hh * kHalfNT + n] = T::mma_k32(va[n], pb_lo[cb], o[cb][hh * kHalfNT + n]);
+        }
+    }
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) {
+      lsum[cb] = T::mma_k32(ones, pb[cb], lsum[cb]);
+      if constexpr (kSplitP) lsum[cb] = T::mma_k32(ones, pb_lo[cb], lsum[cb]);
+    }
+  };
+
   if (n_kt > 0) {
     load_pages(0);
     __syncthreads();
@@ -448,7 +516,31 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
     int nb = (min(wave_kv_end, key0 + kKeys) - key0 + 31) / 32;
     nb = nb < 0 ? 0 : (nb > kBlocks ? kBlocks : nb);
     bool half1_done = false;
-    if (nb > 0) {
+    if constexpr (kLean) {
+      // D = 256: the same order without holding a whole block's K or V operands at
+      // once (64 registers each): the K operands of each 16-key half and the V
+      // operands of each half of the output tiles are read from LDS right before
+      // their MFMAs.
+      if (nb > 0) {
+        f32x4 sacc[2][kCB][2];
+        qk_lean(stage, 0, sacc[0]);
+#pragma unroll
+        for (int kb = 0; kb < kBlocks; ++kb) {
+          if (kb >= nb) break;
+          const int cur = kb & 1;
+          mask_and_rescale(key0 + 32 * kb, sacc[cur]);
+          u16x8 pb[kCB], pb_lo[kCB];
+          if (kb + 1 < nb) qk_lean(stage, kb + 1, sacc[cur ^ 1]);
+          probs(sacc[cur], pb, pb_lo);
+          pv_lean(stage, kb, pb, pb_lo);
+          if (kb == 1 && staged) {
+            stash_half(stage ^ 1, 0);
+            fetch_half(kt + 1, 1);
+            half1_done = true;
+          }
+        }
+      }
+    } else if (nb > 0) {
       // Software pipeline over the tile's blocks: the scores of block kb + 1 are
       // computed (MFMA) while the probabilities of block kb are (VALU), and P.V of
       // block kb runs while the K operands of block kb + 2 are read from LDS.
@@ -521,16 +613,15 @@ __global__ void __launch_bounds__(64 * (kRowsPerWG / (16 * kCB))) paged_prefill_
 // Rows of every sequence with no key to attend (n_new > 0 but L = 0 cannot occur
 // with a consistent plan; sequences with n_new = 0 have no rows) need no pass.
 
-inline int64_t grid_tiles(int64_t total_q, int32_t batch, int group) {
-  return (total_q * group + kRowsPerWG - 1) / kRowsPerWG + batch;
+inline int64_t grid_tiles(int64_t total_q, int32_t batch, int group, int rows_wg) {
+  return (total_q * group + rows_wg - 1) / rows_wg + batch;
 }
 
 template <typename T, int D>
-int launch_prefill(const PrefillParams& p, int64_t tiles, hipStream_t s) {
-  // two column blocks (32 rows) per wave, 8 waves: measured faster than four per
-  // wave at one wave per SIMD (chunk 3584..4095 of 8 x 4096: 276 vs 338 us)
-  constexpr int kCB = 2;
-  paged_prefill_kernel<T, D, kCB><<<dim3((unsigned)(8 * p.per_xcd)), 64 * (kRowsPerWG / (16 * kCB)), 0, s>>>(p);
+int launch_prefill(const PrefillParams& p, hipStream_t s) {
+  // D = 64, 128: two column blocks (32 rows) per wave, 8 waves: measured faster than
+  // four per wave at one wave per SIMD (chunk 3584..4095 of 8 x 4096: 276 vs 338 us)
+  paged_prefill_kernel<T, D><<<dim3((unsigned)(8 * p.per_xcd)), 64 * PrefillTile<D>::kWaves, 0, s>>>(p);
   return check_launch("paged_prefill");
 }
 
@@ -574,10 +665,8 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
     return fail(NSLG_EINVAL, "paged_prefill: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_prefill: GQA group %d > 16", group);
-  if (dtype == NSLG_F32 || ((dtype == NSLG_F16 || dtype == NSLG_BF16) && head_dim == 256)) {
-    // fp32 pools, and 16-bit pools at D = 256 (two stages of 128-key K/V tiles and two
-    // 16-row column blocks per wave do not fit a CU there): the VALU attention kernel,
-    // ragged rows, bottom-right causal
+  if (dtype == NSLG_F32) {
+    // fp32 pools: the VALU attention kernel, ragged rows, bottom-right causal
     if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
       return fail(NSLG_EINVAL, "paged_prefill: row stride smaller than Hq*D");
     AttnF32Args a;
@@ -609,7 +698,7 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   }
   if (dtype != NSLG_F16 && dtype != NSLG_BF16)
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: dtype %d", dtype);
-  if (head_dim != 64 && head_dim != 128)
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: head_dim %d (64, 128 or 256)", head_dim);
   if (num_kv_heads > 65535) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many KV heads");
   if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
@@ -621,7 +710,8 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: pool has >= 2^31 token slots");
   if ((int64_t)page_size * num_kv_heads * head_dim * 2 > (int64_t)0xffffffff)
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: pages of >= 4 GiB");
-  const int64_t tiles = grid_tiles(total_q, batch, group);
+  const int rows_wg = rows_per_wg(head_dim);
+  const int64_t tiles = grid_tiles(total_q, batch, group, rows_wg);
   if (tiles > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
 
   PrefillParams p;
@@ -647,10 +737,11 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   // that is at most 5/4 of the slots of the packed order (near-uniform batches,
   // such as the chunks of a batch of prompts), so few slots are empty.
   // The grid fits both orders; the kernel checks the rounds against the batch.
-  const int64_t most = max_q > 0 ? ((int64_t)max_q * group + kRowsPerWG - 1) / kRowsPerWG : 0;
+  const int64_t most = max_q > 0 ? ((int64_t)max_q * group + rows_wg - 1) / rows_wg : 0;
   const int64_t round_slots = (int64_t)batch * most;
   const bool by_round = most > 0 && most <= 0x7fffffff && 4 * round_slots <= 5 * tiles;
   p.by_round = by_round ? (int32_t)most : 0;
+  p.rows_wg = rows_wg;
   const int64_t slots = by_round && round_slots > tiles ? round_slots : tiles;
   if (slots * num_kv_heads > 0x7fffffff) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
   p.row_tiles = (int32_t)slots;
@@ -661,8 +752,18 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   if ((int64_t)p.num_work + p.pad_work > 0x7fffffff - 8) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
   p.per_xcd = (p.num_work + p.pad_work + 7) / 8;
   hipStream_t s = as_stream(stream);
-  if (dtype == NSLG_F16) return head_dim == 64 ? launch_prefill<F16, 64>(p, tiles, s) : launch_prefill<F16, 128>(p, tiles, s);
-  return head_dim == 64 ? launch_prefill<BF16, 64>(p, tiles, s) : launch_prefill<BF16, 128>(p, tiles, s);
+  if (dtype == NSLG_F16) {
+    switch (head_dim) {
+      case 64: return launch_prefill<F16, 64>(p, s);
+      case 128: return launch_prefill<F16, 128>(p, s);
+      default: return launch_prefill<F16, 256>(p, s);
+    }
+  }
+  switch (head_dim) {
+    case 64: return launch_prefill<BF16, 64>(p, s);
+    case 128: return launch_prefill<BF16, 128>(p, s);
+    default: return launch_prefill<BF16, 256>(p, s);
+  }
 }
 
 }  // namespace

@@ -18,15 +18,10 @@ _DTYPE_CODE = {torch.float16: _lib.NSLG_F16, torch.bfloat16: _lib.NSLG_BF16, tor
 # Pool dtypes nslg_paged_decode_grouped serves (its work units are 16-bit MFMA tiles);
 # decode batches of other pools are decoded per sequence.
 GROUPED_DECODE_DTYPES = (torch.float16, torch.bfloat16)
-# head dims each pool dtype supports on every entry point a cache uses: decode,
-# RoPE append and the VALU attention kernel take 64, 128 and 256; the 16-bit MFMA
-# prefill kernel 64 and 128 (at 256 its two 16-row column blocks per wave and the
-# 128-key LDS tiles do not fit one CU), and 16-bit prefill at 256 runs on the VALU
-# kernel
+# head dims each pool dtype supports on every entry point a cache uses: decode, RoPE
+# append and prefill take 64, 128 and 256 (16-bit pools on the MFMA kernels, fp32
+# pools on the VALU attention kernel)
 HEAD_DIMS = {torch.float16: (64, 128, 256), torch.bfloat16: (64, 128, 256), torch.float32: (64, 128, 256)}
-# (dtype, head_dim) pairs whose prefill runs on the VALU attention kernel although the
-# dtype has an MFMA prefill at other head dims: tens of times slower per token
-VALU_PREFILL = {(torch.float16, 256), (torch.bfloat16, 256)}
 
 
 def dtype_code(dt: torch.dtype) -> int:

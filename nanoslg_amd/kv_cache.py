@@ -27,7 +27,6 @@ from __future__ import annotations
 import gc
 import math
 import threading
-import warnings
 import weakref
 from abc import ABC, abstractmethod
 from dataclasses import dataclass
@@ -47,11 +46,6 @@ def _check_head_dim(cfg: "KVCacheConfig", kernels) -> None:
     if dims is not None and dev is not None and dev.type == "cuda" and cfg.head_dim not in dims.get(cfg.dtype, ()):
         raise ValueError(f"KV cache: head_dim {cfg.head_dim} is not supported for {cfg.dtype} "
                          f"(supported: {dims.get(cfg.dtype, ())})")
-    slow = getattr(kernels, "VALU_PREFILL", ())
-    if dev is not None and dev.type == "cuda" and (cfg.dtype, cfg.head_dim) in slow:
-        warnings.warn(f"KV cache: prefill at head_dim {cfg.head_dim} in {cfg.dtype} runs on the VALU attention "
-                      f"kernel (no MFMA prefill for this head_dim), tens of times slower per token than at "
-                      f"head_dim 128; decode is unaffected", RuntimeWarning, stacklevel=3)
 
 
 def _default_kernels():

@@ -183,9 +183,10 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 
 
 def test_attention_kernel_rejects_rows_not_16_byte_aligned():
-    """The VALU attention path (fp32 pools, 16-bit prefill at head_dim 256) takes only
-    row strides of whole 16-byte units for q and out: its vector accesses and the
-    padded grid's pad-row zeroing store 16 bytes at a time."""
+    """Prefill on a padded grid takes only row strides of whole 16-byte units for q and
+    out, on the MFMA kernel (16-bit pools, here at head_dim 256) and on the VALU kernel
+    (fp32 pools) alike: their vector accesses and the pad-row zeroing store 16 bytes at
+    a time."""
     from nanoslg_amd import _lib
     lib = _lib.load()
     A = 4096

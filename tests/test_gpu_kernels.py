@@ -297,12 +297,20 @@ def test_prefill_row_tile_orders():
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_prefill_head_dim_256_chunk_over_cached_context(dtype):
-    """16-bit pools at head_dim 256 (the VALU kernel): chunks over cached context,
-    GQA 4, page sizes 16 and 1, against the oracle."""
+    """16-bit pools at head_dim 256 (the MFMA kernel's shape for it: one 16-row column
+    block per wave, 64-key tiles, 128 rows per workgroup): chunks over cached context,
+    GQA 4, 1 and 8, a 512-token chunk over 3584 cached tokens, page sizes 16 and 1 (a
+    sequence whose page ids span more than one 2048-entry window), against the oracle."""
     _log(f"prefill D=256 {dtype}")
     out, ref = _prefill_case([300, 1000, 64, 17], [64, 200, 64, 3], 32, 8, 256, 16, dtype, seed=61)
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
     out, ref = _prefill_case([90, 40], [30, 40], 16, 4, 256, 1, dtype, seed=62)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    out, ref = _prefill_case([4096, 2500], [512, 300], 16, 4, 256, 16, dtype, seed=63)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    out, ref = _prefill_case([4500, 33], [70, 33], 8, 8, 256, 1, dtype, seed=64)
+    torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
+    out, ref = _prefill_case([1500, 1400, 1300], [512, 500, 480], 64, 8, 256, 16, dtype, seed=65)
     torch.testing.assert_close(out, ref, atol=ATOL, rtol=RTOL)
 
 

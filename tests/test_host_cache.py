@@ -798,18 +798,3 @@ def test_graph_context_refers_to_its_graph_weakly():
         if was:
             gc.enable()
 
-
-def test_valu_prefill_head_dims_warn_at_construction(monkeypatch):
-    """A 16-bit cache at head_dim 256 on a device warns once at construction that its
-    prefill runs on the VALU attention kernel; head_dim 128 builds silently."""
-    import warnings
-
-    from nanoslg_amd import kernels as K
-    kern = types.SimpleNamespace(HEAD_DIMS=K.HEAD_DIMS, VALU_PREFILL=K.VALU_PREFILL)
-    for D, warns in ((256, True), (128, False)):
-        cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=8, num_qo_heads=32, head_dim=D, page_size=16,
-                               max_pages=64, dtype=torch.float16, device="cuda:0")
-        with warnings.catch_warnings(record=True) as w:
-            warnings.simplefilter("always")
-            KC._check_head_dim(cfg, kern)
-        assert any("VALU" in str(x.message) for x in w) == warns, D
