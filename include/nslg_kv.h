@@ -293,9 +293,8 @@ int nslg_paged_decode_grouped_append(const void* q, int64_t q_stride,
  *               the true max only costs that order, never correctness)
  *   out         [T] rows of Hq*D elements at stride out_stride
  *   sm_scale    positive and finite (EINVAL otherwise)
- * Supported: f16, bf16 with D in {64, 128} (MFMA) or 256 (the VALU kernel, inputs
- * widened to fp32, the output rounded once); f32 with D in {64, 128, 256} (the VALU
- * kernel of nslg_paged_decode's f32 path); 1 <= Hq/Hkv <= 16.
+ * Supported: f16, bf16 with D in {64, 128, 256} (MFMA); f32 with D in {64, 128,
+ * 256} (the VALU kernel of nslg_paged_decode's f32 path); 1 <= Hq/Hkv <= 16.
  */
 size_t nslg_paged_prefill_workspace_size(int32_t batch, int32_t num_qo_heads,
                                          int32_t head_dim, int64_t total_q,
