@@ -61,6 +61,9 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true",
                     help="decode workloads: replay each step from captured HIP graphs (DecodeGraph)")
+    ap.add_argument("--layers", type=int, default=1,
+                    help="small_batch workload: layers per decode step (each with its own pool layer; "
+                         "one forward attends every layer, as a model's decode step does)")
     ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128, 256],
                     help="prefill workload: head dim (heads scaled to keep Hq*D = 4096, Hkv*D = 1024)")
     return ap.parse_args()
@@ -104,17 +107,18 @@ def _log(msg):
 class DecodeWorkload:
     """A batch of sequences with random K/V already resident in a paged pool."""
 
-    def __init__(self, name, lens, pool_pages, seed, churn_frac=0.0, shuffle=True):
+    def __init__(self, name, lens, pool_pages, seed, churn_frac=0.0, shuffle=True, layers=1):
         import torch
         from nanoslg_amd.kv_cache import KVCacheConfig, PagedKVCache
         self.torch = torch
         self.name = name
+        self.layers = layers
         self.lens0 = list(lens)
         self.B = len(lens)
         self.seed = seed
         self.churn_frac = churn_frac
         self.rng = np.random.default_rng(seed)
-        cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
+        cfg = KVCacheConfig(num_layers=layers, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
                             max_pages=pool_pages, dtype=torch.float16, device=torch.device("cuda:0"),
                             enable_prefix_caching=False, backend="paged")
         self.mgr = PagedKVCache(cfg)
@@ -204,10 +208,16 @@ class DecodeWorkload:
         q, kn, vn = self.inputs[self.step_idx % len(self.inputs)]
         self.step_idx += 1
         ctx = self.mgr.begin_forward(self.ids, [1] * self.B)
-        out = ctx.attend(0, q, kn, vn, HQ, HKV)
+        for layer in range(self.layers):
+            out = ctx.attend(layer, q, kn, vn, HQ, HKV)
         self.mgr.end_forward(ctx)
         self.last_ctx = ctx
         return out
+
+    def forward(self, ctx):
+        """The attend calls of one decode forward on the ring's first inputs (what a
+        captured step replays)."""
+        return [ctx.attend(layer, self.q[0], self.kn[0], self.vn[0], HQ, HKV) for layer in range(self.layers)]
 
 
 def step_bytes(lens_after, B, total_pages):
@@ -418,10 +428,10 @@ def run_decode(args):
     else:  # small_batch
         rng = np.random.default_rng(args.seed)
         lens = [int(x) for x in rng.integers(1024, 4097, size=4)]
-        w = DecodeWorkload("small_batch", lens, 65536, args.seed)
+        w = DecodeWorkload("small_batch", lens, 65536, args.seed, layers=args.layers)
         cfg = {"workload": "small_batch_decode_append", "batch": 4, "ctx": "uniform[1024,4096]",
                "pool_pages": 65536, "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D,
-               "layers": 1, "seed": args.seed}
+               "layers": args.layers, "seed": args.seed}
     cfg["step"] = "graph replay (DecodeGraph)" if args.graph else "eager (begin_forward / attend / end_forward)"
     _log(f"workload {w.name}: B={w.B} pages={w.mgr.cfg.max_pages} sum(L)={sum(lens)}")
     from nanoslg_amd import kernels
@@ -436,7 +446,7 @@ def run_decode(args):
         from nanoslg_amd.kv_cache import DecodeGraph
 
         def make_graph(warm):
-            g = DecodeGraph(w.mgr, w.ids, lambda ctx: ctx.attend(0, w.q[0], w.kn[0], w.vn[0], HQ, HKV))
+            g = DecodeGraph(w.mgr, w.ids, w.forward)
             for _ in range(warm):
                 g.step()
             torch.cuda.synchronize()
@@ -453,7 +463,7 @@ def run_decode(args):
         lens_i = [L + 1 + i for L in lens_before]
         tp = sum(math.ceil(L / PS) for L in lens_i)
         for j, x in enumerate(step_bytes(lens_i, w.B, tp)):
-            nbytes[j] += x
+            nbytes[j] += x * w.layers
     kbytes = 0
     churn_s = 0.0
     with _GcPaused():
@@ -486,12 +496,12 @@ def run_decode(args):
     with _GcPaused():
         for _ in range(args.steps):
             lens_i = [L + 1 for L in w.seq_lens()]
-            kbytes += decode_call_bytes(lens_i, w.B, sum(math.ceil(L / PS) for L in lens_i))
+            kbytes += w.layers * decode_call_bytes(lens_i, w.B, sum(math.ceil(L / PS) for L in lens_i))
             w.step()
         torch.cuda.synchronize()
     timed.recording = False
     mean_ms = timed.mean_ms()
-    kbytes /= args.steps
+    kbytes /= args.steps * w.layers
     achieved = kbytes / (mean_ms * 1e-3) / 1e9
     _log(f"decode call: mean {mean_ms*1e3:.1f} us over {len(timed.events)} launches, {achieved:.1f} GB/s")
     ratio = TRAFFIC_PER_ALGORITHMIC_BYTE.get(w.name)
@@ -563,7 +573,7 @@ def run_decode(args):
         "data": "synthetic: K/V/Q ~ N(0,1), seeded",
         "config": cfg,
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "decode_tok_s_layer": round(w.B * args.steps / wall, 1),
+        "decode_tok_s_layer": round(w.B * args.steps * w.layers / wall, 1),
         "bytes_per_step": {k: int(v / args.steps) for k, v in zip(["kv_read", "append", "q_out", "csr"], nbytes)},
         "roofline": {
             "bound": "hbm",

@@ -132,6 +132,16 @@ int nslg_gather_kv(const void* k_pool, const void* v_pool, int64_t num_pages,
  *   workspace         caller-owned device scratch of at least
  *                     nslg_paged_decode_workspace_size(...) bytes, 256-byte aligned;
  *                     one call at a time per workspace
+ *   layout            0: the call cuts its sequences into chunks from their lengths
+ *                     (every wave reads the lengths and searches the chunk length);
+ *                     t > 0: the same, and the chunks' work is recorded in the
+ *                     workspace under tag t; -t: a later call of the same forward
+ *                     (another layer: same batch, block table, lengths, sizes and
+ *                     workspace) reads the record instead, when the workspace still
+ *                     holds tag t (else it cuts the chunks itself). Results are
+ *                     bit-identical in all three modes; a tag must not be reused for
+ *                     another forward (a wrong record gives wrong results, though
+ *                     every access stays inside the block table and the pool).
  * Query head h reads KV head h / (Hq/Hkv). Supported: f16, bf16 (MFMA, split-K as
  * above) and f32 (a VALU kernel, one workgroup per 16 query rows of a sequence and
  * KV head and key split, then an fp32 merge, for caches kept in fp32 such as the
@@ -155,7 +165,7 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
                       int32_t num_kv_heads, int32_t head_dim, float sm_scale,
                       int32_t dtype, void* out, int64_t out_stride,
                       void* workspace, size_t workspace_bytes,
-                      nslg_stream_t stream);
+                      int64_t layout, nslg_stream_t stream);
 
 /*
  * The decode step of one layer: each sequence's new token written into the pool,
@@ -168,7 +178,7 @@ int nslg_paged_decode(const void* q, int64_t q_stride,
  *   k_new, v_new   [batch] rows of Hkv*D elements at element strides k_new_stride,
  *                  v_new_stride (device, the pool's dtype; f16/bf16: 16-byte aligned
  *                  rows, f32: 4-byte)
- *   other arguments as nslg_paged_decode
+ *   other arguments as nslg_paged_decode (layout included)
  * Row b is sequence b's token L_b - 1 (the last token its block table covers, the
  * reference's slot for the decode write): the slot is found through the block
  * table, so no slot mapping is passed. The chunk that reads that token writes it
@@ -187,7 +197,7 @@ int nslg_paged_decode_append(const void* q, int64_t q_stride,
                              int32_t num_kv_heads, int32_t head_dim, float sm_scale,
                              int32_t dtype, void* out, int64_t out_stride,
                              void* workspace, size_t workspace_bytes,
-                             nslg_stream_t stream);
+                             int64_t layout, nslg_stream_t stream);
 
 /*
  * nslg_paged_decode without a caller workspace: the split-K partials live in a
@@ -236,7 +246,7 @@ int nslg_paged_decode_noalloc(const void* q, int64_t q_stride,
  *                       [16 g, 16 g + n_g), -1 after them; 1 <= n_g <= 16 / G;
  *                       a sequence is in at most one group
  * The workspace holds 16 / G partial slots per chunk:
- * nslg_paged_decode_grouped_workspace_size(...) bytes. f16/bf16 only (the size
+ * nslg_paged_decode_grouped_workspace_size(...) bytes. layout as nslg_paged_decode. f16/bf16 only (the size
  * query returns 0 for f32; decode f32 batches with nslg_paged_decode).
  */
 size_t nslg_paged_decode_grouped_workspace_size(int32_t batch, int32_t num_qo_heads,
@@ -254,7 +264,7 @@ int nslg_paged_decode_grouped(const void* q, int64_t q_stride,
                               const int32_t* group_prefix_pages, const int32_t* group_members,
                               void* out, int64_t out_stride,
                               void* workspace, size_t workspace_bytes,
-                              nslg_stream_t stream);
+                              int64_t layout, nslg_stream_t stream);
 
 /*
  * nslg_paged_decode_grouped with each sequence's new token written first, as
@@ -274,7 +284,7 @@ int nslg_paged_decode_grouped_append(const void* q, int64_t q_stride,
                                      int32_t num_groups, const int32_t* group_prefix_pages,
                                      const int32_t* group_members, void* out, int64_t out_stride,
                                      void* workspace, size_t workspace_bytes,
-                                     nslg_stream_t stream);
+                                     int64_t layout, nslg_stream_t stream);
 
 /*
  * Paged causal prefill attention over a ragged batch of new tokens whose K/V

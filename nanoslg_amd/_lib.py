@@ -40,18 +40,18 @@ SIGNATURES = {
     "nslg_paged_decode": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                     c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,
-                                    c_void_p]),
+                                    c_int64, c_void_p]),
     "nslg_paged_decode_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                            c_void_p, c_void_p, c_int64, c_int32,
                                            c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                            c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p, c_size_t,
-                                           c_void_p]),
+                                           c_int64, c_void_p]),
     "nslg_paged_decode_grouped_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                                    c_void_p, c_void_p, c_int64, c_int32,
                                                    c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32,
                                                    c_int32, c_int32, c_float, c_int32, c_void_p, c_int32,
                                                    c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_size_t,
-                                                   c_void_p]),
+                                                   c_int64, c_void_p]),
     "nslg_paged_decode_noalloc": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                             c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                             c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p]),
@@ -60,7 +60,7 @@ SIGNATURES = {
     "nslg_paged_decode_grouped": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                             c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                             c_int32, c_float, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
-                                            c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+                                            c_void_p, c_int64, c_void_p, c_size_t, c_int64, c_void_p]),
     "nslg_decode_plan_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p]),

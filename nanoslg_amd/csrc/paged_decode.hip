@@ -62,6 +62,15 @@ struct DecodeParams {
   int32_t max_chunks;
   int32_t head_groups;   // workgroups per chunk (grid y)
   int2* meta;            // per sequence: first chunk, chunk count (for the merge launch)
+  // Layout of the call's chunks, kept in the workspace for the other layers of a
+  // forward (same batch and plan): layout_mode 0: found from the lengths; > 0: found,
+  // and recorded under layout_tag; < 0: read from the record when *layout_tag_ptr is
+  // layout_tag, found otherwise. Two int4 per chunk (see the kernel).
+  int32_t layout_mode;
+  int64_t total_pages;  // entries of indices (kv_indptr[batch])
+  uint64_t layout_tag;
+  uint64_t* layout_tag_ptr;
+  int4* layout_map;
   uint16_t* out;
   int64_t out_stride;
   float* part_o;   // [max_chunks, slot_members, Hq, D]
@@ -337,59 +346,112 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
   const int h = blockIdx.y * (blockDim.x >> 6) + wave;
   if (h >= p.num_kv_heads) return;
 
-  int units = p.batch;
-  if constexpr (kGrouped) units += ga.num_groups;
-  const LaneLens<kGrouped> lens(p, ga, units);
-  int ct = p.chunk_tokens;
-  if (p.chunk_budget > 0) {
-    // An upper bound that fits, from the lengths themselves: with T tokens over U
-    // units, length ceil(T / (budget - U)) gives at most T / len + U <= budget
-    // chunks. (It is at most the host's bound, which came from an upper bound of T,
-    // so the search finds the same length; and a launch captured once stays right
-    // while the lengths grow.)
-    int tot = 0;
-    const int groups = (lens.units + 63) >> 6;
-    for (int i = 0; i < groups; ++i) tot += lens.at(p, ga, i);
-    const int64_t t_all = (int64_t)__builtin_amdgcn_readfirstlane(wave_sum_i32(tot));
-    const int64_t usable = (int64_t)p.chunk_budget - lens.units;
-    int64_t hi = (t_all + usable - 1) / usable;
-    hi = ((hi + 15) / 16) * 16;
-    // Shortest chunk: a chunk costs a fixed set-up and a partial to merge, so small
-    // batches (where the slots are not the limit) take fewer, longer chunks: about
-    // t_all / 96 tokens, between 64 and 256 (measured best at 4 sequences of 1k-4k
-    // tokens and at 16-64 sequences of 1k-2k; large batches are bounded by `hi`).
-    int64_t lo = ((t_all / 96 + 15) / 16) * 16;
-    lo = lo < 64 ? 64 : (lo > 256 ? 256 : lo);
-    hi = hi < lo ? lo : (hi > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : hi);
-    ct = fit_chunk_tokens<kGrouped>(p, ga, lens, (int)lo, (int)hi, p.chunk_budget);
+  // The chunk's work: unit u (sequence b's own tokens, or group g's prefix read
+  // through member b's table), its chunk range [cstart, cstart + nchunks), the
+  // chunk's tokens [t_begin, t_end), b's block-table offset and page count, and
+  // whether b's result also takes its group's prefix. Either read from the layout
+  // an earlier call of the same forward recorded in the workspace (layout < 0, when
+  // the workspace holds its tag), or found from the lengths.
+  int u = 0, cstart = 0, nchunks = 0, b = 0, g = -1, t_begin = 0, t_end = 0, idx_off = 0, np_seq = 0;
+  bool merged = false;
+  bool mapped = false;
+  if (p.layout_mode < 0 && *p.layout_tag_ptr == p.layout_tag) {
+    const int4 e0 = p.layout_map[2 * chunk];
+    const int4 e1 = p.layout_map[2 * chunk + 1];
+    u = __builtin_amdgcn_readfirstlane(e0.x);
+    if (u < 0) return;  // no unit: past the forward's chunks
+    cstart = __builtin_amdgcn_readfirstlane(e0.y);
+    nchunks = __builtin_amdgcn_readfirstlane(e0.z);
+    idx_off = __builtin_amdgcn_readfirstlane(e0.w);
+    b = __builtin_amdgcn_readfirstlane(e1.x);
+    t_begin = __builtin_amdgcn_readfirstlane(e1.y);
+    t_end = __builtin_amdgcn_readfirstlane(e1.z);
+    const int w1 = __builtin_amdgcn_readfirstlane(e1.w);
+    np_seq = w1 & 0x3fffffff;
+    merged = (w1 >> 30) & 1;
+    if constexpr (kGrouped) g = u >= p.batch ? u - p.batch : -1;
+    // a record of another batch (a caller's mistake) must not send a wave outside
+    // the block table: such an entry is found from the lengths instead
+    int units = p.batch;
+    if constexpr (kGrouped) units += ga.num_groups;
+    mapped = u < units && b >= 0 && b < p.batch && nchunks > 0 && cstart >= 0 && cstart <= chunk &&
+             chunk < cstart + nchunks && idx_off >= 0 && (int64_t)idx_off + np_seq <= p.total_pages &&
+             t_begin >= 0 && t_begin < t_end && t_end <= np_seq * p.page_size;
   }
-  int u = 0, cstart = 0, nchunks = 0;
-  if (!locate_chunk<kGrouped>(p, ga, lens, ct, chunk, u, cstart, nchunks)) return;
-  u = __builtin_amdgcn_readfirstlane(u);
-  cstart = __builtin_amdgcn_readfirstlane(cstart);
-  nchunks = __builtin_amdgcn_readfirstlane(nchunks);
-  // The unit: sequence b's tokens [base, base + len) (all of them, or those after its
-  // group's prefix), or group g's prefix [0, len), read through member 0's table.
-  int b = u, g = -1, base = 0, len = 0;
-  bool merged = false;  // the sequence's result also takes its group's prefix
-  if constexpr (kGrouped) {
-    if (u >= p.batch) {
-      g = u - p.batch;
-      b = ga.member_seq[g * kGroupCols];
-      len = group_prefix_tokens(p, ga, g);
-    } else {
-      const int L = seq_len_of(p.indptr, p.last_len, b, p.page_size);
-      base = seq_prefix_tokens(p, ga, b, L);
-      len = L - base;
-      merged = ga.seq_group_slot[b] >= 0 && (ga.seq_group_slot[b] >> 4) < ga.num_groups;
+  const bool record = p.layout_mode > 0 && blockIdx.y == 0 && threadIdx.x == 0;
+  if (!mapped) {
+    g = -1;
+    merged = false;
+    if (record && chunk == 0) *p.layout_tag_ptr = p.layout_tag;
+    int units = p.batch;
+    if constexpr (kGrouped) units += ga.num_groups;
+    const LaneLens<kGrouped> lens(p, ga, units);
+    int ct = p.chunk_tokens;
+    if (p.chunk_budget > 0) {
+      // An upper bound that fits, from the lengths themselves: with T tokens over U
+      // units, length ceil(T / (budget - U)) gives at most T / len + U <= budget
+      // chunks. (It is at most the host's bound, which came from an upper bound of T,
+      // so the search finds the same length; and a launch captured once stays right
+      // while the lengths grow.)
+      int tot = 0;
+      const int groups = (lens.units + 63) >> 6;
+      for (int i = 0; i < groups; ++i) tot += lens.at(p, ga, i);
+      const int64_t t_all = (int64_t)__builtin_amdgcn_readfirstlane(wave_sum_i32(tot));
+      const int64_t usable = (int64_t)p.chunk_budget - lens.units;
+      int64_t hi = (t_all + usable - 1) / usable;
+      hi = ((hi + 15) / 16) * 16;
+      // Shortest chunk: a chunk costs a fixed set-up and a partial to merge, so small
+      // batches (where the slots are not the limit) take fewer, longer chunks: about
+      // t_all / 96 tokens, between 64 and 256 (measured best at 4 sequences of 1k-4k
+      // tokens and at 16-64 sequences of 1k-2k; large batches are bounded by `hi`).
+      int64_t lo = ((t_all / 96 + 15) / 16) * 16;
+      lo = lo < 64 ? 64 : (lo > 256 ? 256 : lo);
+      hi = hi < lo ? lo : (hi > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : hi);
+      ct = fit_chunk_tokens<kGrouped>(p, ga, lens, (int)lo, (int)hi, p.chunk_budget);
     }
-    b = __builtin_amdgcn_readfirstlane(b);
-    g = __builtin_amdgcn_readfirstlane(g);
-    base = __builtin_amdgcn_readfirstlane(base);
-    len = __builtin_amdgcn_readfirstlane(len);
-  } else {
-    len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+    if (!locate_chunk<kGrouped>(p, ga, lens, ct, chunk, u, cstart, nchunks)) {
+      if (record) p.layout_map[2 * chunk] = make_int4(-1, 0, 0, 0);
+      return;
+    }
+    u = __builtin_amdgcn_readfirstlane(u);
+    cstart = __builtin_amdgcn_readfirstlane(cstart);
+    nchunks = __builtin_amdgcn_readfirstlane(nchunks);
+    // sequence b's tokens [base, base + len) (all of them, or those after its group's
+    // prefix), or group g's prefix [0, len), read through member 0's table
+    b = u;
+    int base = 0, len = 0;
+    if constexpr (kGrouped) {
+      if (u >= p.batch) {
+        g = u - p.batch;
+        b = ga.member_seq[g * kGroupCols];
+        len = group_prefix_tokens(p, ga, g);
+      } else {
+        const int L = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+        base = seq_prefix_tokens(p, ga, b, L);
+        len = L - base;
+        merged = ga.seq_group_slot[b] >= 0 && (ga.seq_group_slot[b] >> 4) < ga.num_groups;
+      }
+      b = __builtin_amdgcn_readfirstlane(b);
+      g = __builtin_amdgcn_readfirstlane(g);
+      base = __builtin_amdgcn_readfirstlane(base);
+      len = __builtin_amdgcn_readfirstlane(len);
+    } else {
+      len = seq_len_of(p.indptr, p.last_len, b, p.page_size);
+    }
+    // chunk c of the unit's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
+    const int ntiles_seq = (len + 15) >> 4;
+    const int c_local = chunk - cstart;
+    t_begin = base + 16 * (int)((int64_t)c_local * ntiles_seq / nchunks);
+    t_end = base + min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
+    idx_off = p.indptr[b];
+    np_seq = p.indptr[b + 1] - idx_off;
+    if (record) {
+      p.layout_map[2 * chunk] = make_int4(u, cstart, nchunks, idx_off);
+      p.layout_map[2 * chunk + 1] = make_int4(b, t_begin, t_end, np_seq | (merged ? 1 << 30 : 0));
+    }
   }
+  // the chunk ranges of the merge (written by every call: a call between two calls
+  // of one forward may have used the workspace)
   if (chunk == cstart && blockIdx.y == 0 && threadIdx.x == 0) {
     if constexpr (kGrouped) {
       if (g >= 0)
@@ -400,13 +462,9 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
       p.meta[b] = make_int2(cstart, nchunks);
     }
   }
-  // chunk c of the unit's nchunks covers tiles [c*ntiles/nchunks, (c+1)*ntiles/nchunks)
-  const int ntiles_seq = (len + 15) >> 4;
   const int c_local = chunk - cstart;
-  const int t_begin = base + 16 * (int)((int64_t)c_local * ntiles_seq / nchunks);
-  const int t_end = base + min(16 * (int)((int64_t)(c_local + 1) * ntiles_seq / nchunks), len);
   const int t_last = t_end - 1;
-  const int32_t* idx = p.indices + p.indptr[b];
+  const int32_t* idx = p.indices + idx_off;
 
   // The new row of sequence b (its last token, in its last page) is written by its
   // last chunk, this wave for its own KV head, before any of the chunk's loads: the
@@ -525,7 +583,6 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
       const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
       const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
       const int first_page = t_begin / ps;
-      const int np_seq = p.indptr[b + 1] - p.indptr[b];
       int win_lo = 0, win_hi = 0;  // window = pages [first_page + win_base, +128)
       int win_base = 0;
       auto load_window = [&]() {
@@ -968,12 +1025,14 @@ write_last_rows_kernel(const uint32_t* __restrict__ k_new, const uint32_t* __res
 inline size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace: partials [max_chunks, slot_members, Hq, D] and [..., 2] fp32, then each
-// sequence's chunk range, then each group prefix's chunk range (int32 pairs), each
-// region rounded up to 256 bytes.
+// sequence's chunk range, then each group prefix's chunk range (int32 pairs), then
+// the recorded chunk layout (a 16-byte tag, then two int4 per chunk), each region
+// rounded up to 256 bytes.
 size_t workspace_bytes_for(const DecodeShape& sh, int32_t batch, int32_t num_qo_heads, int32_t head_dim,
                            int32_t slot_members, int32_t num_groups) {
   return (size_t)(sh.max_chunks * slot_members * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float)) +
-         round256((size_t)batch * 8) + (num_groups > 0 ? round256((size_t)num_groups * 8) : 0);
+         round256((size_t)batch * 8) + (num_groups > 0 ? round256((size_t)num_groups * 8) : 0) +
+         round256(16 + (size_t)sh.max_chunks * 32);
 }
 
 bool shape_ok(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int64_t total_pages,
@@ -996,7 +1055,8 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
                 const int32_t* kv_last_page_len, int64_t total_pages, int32_t batch, int32_t num_qo_heads,
                 int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype, void* out,
                 int64_t out_stride, GroupArgs<kGrouped>& ga, int32_t num_groups, int32_t slot_members,
-                void* workspace, size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr = NewRows{}) {
+                void* workspace, size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr = NewRows{},
+                int64_t layout = 0) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_pages < 0)
     return fail(NSLG_EINVAL, "paged_decode: bad sizes");
@@ -1145,6 +1205,12 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
   char* meta = ws + (size_t)(mc * slot_members * num_qo_heads * (head_dim + 2) * (int64_t)sizeof(float));
   p.meta = reinterpret_cast<int2*>(meta);
   if constexpr (kGrouped) ga.group_meta = reinterpret_cast<int2*>(meta + round256((size_t)batch * 8));
+  char* lay = meta + round256((size_t)batch * 8) + (num_groups > 0 ? round256((size_t)num_groups * 8) : 0);
+  p.layout_mode = layout > 0 ? 1 : (layout < 0 ? -1 : 0);
+  p.layout_tag = (uint64_t)(layout > 0 ? layout : -layout);
+  p.layout_tag_ptr = reinterpret_cast<uint64_t*>(lay);
+  p.layout_map = reinterpret_cast<int4*>(lay + 16);
+  p.total_pages = total_pages;
 
   MergeParams mp;
   mp.indptr = kv_indptr;
@@ -1213,11 +1279,12 @@ extern "C" int nslg_paged_decode(const void* q, int64_t q_stride, const void* k_
                                  int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                                  int32_t head_dim, float sm_scale, int32_t dtype, void* out,
                                  int64_t out_stride, void* workspace, size_t workspace_bytes,
-                                 nslg_stream_t stream) {
+                                 int64_t layout, nslg_stream_t stream) {
   GroupArgs<false> ga;
   return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
                             kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
-                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream);
+                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, NewRows{},
+                            layout);
 }
 
 // ---- decode without a caller workspace ---------------------------------------------
@@ -1291,7 +1358,7 @@ extern "C" int nslg_paged_decode_append(const void* q, int64_t q_stride, const v
                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                                         int32_t head_dim, float sm_scale, int32_t dtype, void* out,
                                         int64_t out_stride, void* workspace, size_t workspace_bytes,
-                                        nslg_stream_t stream) {
+                                        int64_t layout, nslg_stream_t stream) {
   if (batch > 0 && (!k_new || !v_new)) return fail(NSLG_EINVAL, "paged_decode_append: null k_new or v_new");
   NewRows nr;
   nr.k = k_new;
@@ -1301,7 +1368,7 @@ extern "C" int nslg_paged_decode_append(const void* q, int64_t q_stride, const v
   GroupArgs<false> ga;
   return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
                             kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
-                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, nr);
+                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, nr, layout);
 }
 
 namespace {
@@ -1312,7 +1379,7 @@ int grouped_impl(const void* q, int64_t q_stride, const void* k_pool, const void
                  int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
                  const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
                  const int32_t* group_members, void* out, int64_t out_stride, void* workspace,
-                 size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr) {
+                 size_t workspace_bytes, nslg_stream_t stream, const NewRows& nr, int64_t layout) {
   if (num_groups < 1 || num_groups > kMaxGroups)
     return fail(NSLG_EUNSUPPORTED, "paged_decode_grouped: %d groups (1..%d)", num_groups, kMaxGroups);
   if (!seq_group_slot || !group_prefix_pages || !group_members)
@@ -1359,7 +1426,7 @@ int grouped_impl(const void* q, int64_t q_stride, const void* k_pool, const void
   return decode_impl<true>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
                            dtype, out, out_stride, ga, num_groups, max_members, workspace, workspace_bytes, stream,
-                           nr);
+                           nr, layout);
 }
 
 }  // namespace
@@ -1373,11 +1440,11 @@ extern "C" int nslg_paged_decode_grouped(const void* q, int64_t q_stride, const 
                                          const int32_t* seq_group_slot, int32_t num_groups,
                                          const int32_t* group_prefix_pages, const int32_t* group_members,
                                          void* out, int64_t out_stride, void* workspace,
-                                         size_t workspace_bytes, nslg_stream_t stream) {
+                                         size_t workspace_bytes, int64_t layout, nslg_stream_t stream) {
   return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
                       total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
                       num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,
-                      stream, NewRows{});
+                      stream, NewRows{}, layout);
 }
 
 extern "C" int nslg_paged_decode_grouped_append(
@@ -1387,7 +1454,7 @@ extern "C" int nslg_paged_decode_grouped_append(
     int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
     const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
     const int32_t* group_members, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
-    nslg_stream_t stream) {
+    int64_t layout, nslg_stream_t stream) {
   if (batch > 0 && (!k_new || !v_new)) return fail(NSLG_EINVAL, "paged_decode_grouped_append: null k_new or v_new");
   NewRows nr;
   nr.k = k_new;
@@ -1397,5 +1464,5 @@ extern "C" int nslg_paged_decode_grouped_append(
   return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
                       total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
                       num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,
-                      stream, nr);
+                      stream, nr, layout);
 }

@@ -6,6 +6,7 @@ here computes on the CPU: a missing library or a non-HIP tensor raises.
 """
 from __future__ import annotations
 
+import itertools
 import math
 from typing import Optional, Tuple
 
@@ -32,6 +33,10 @@ def dtype_code(dt: torch.dtype) -> int:
 
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+# tags of the chunk layouts decode launchers record in their workspaces (one per
+# recorded plan; never reused within the process)
+_LAYOUT_TAGS = itertools.count(1)
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -299,30 +304,32 @@ def paged_decode(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
                  total_pages: int, sm_scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
-                 groups: Optional[DecodeGroups] = None) -> torch.Tensor:
+                 groups: Optional[DecodeGroups] = None, layout: int = 0) -> torch.Tensor:
     """Decode attention. q: [B, Hq, D] (rows may be strided); returns [B, Hq, D].
     With `groups`, the shared prefix pages of each group are read once for all its
-    members (nslg_paged_decode_grouped)."""
+    members (nslg_paged_decode_grouped). `layout`: the chunk-layout record of the
+    C entry point (0: none; t > 0: record under tag t in the workspace; -t: a later
+    layer of the same forward reads it)."""
     return _decode(q, None, None, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
-                   sm_scale, out, workspace, groups)
+                   sm_scale, out, workspace, groups, layout)
 
 
 def paged_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_layer: torch.Tensor,
                         v_layer: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
                         kv_last_page_len: torch.Tensor, total_pages: int, sm_scale: Optional[float] = None,
                         out: Optional[torch.Tensor] = None, workspace: Optional[Workspace] = None,
-                        groups: Optional[DecodeGroups] = None) -> torch.Tensor:
+                        groups: Optional[DecodeGroups] = None, layout: int = 0) -> torch.Tensor:
     """One decode step of a layer (nslg_paged_decode_append / _grouped_append): row b
     of k_new / v_new ([B, ..., Hkv, D], one token per sequence, rows may be strided)
     is written into the pool as sequence b's last token (the slot its block table
     gives for token L_b - 1), then decode attention as paged_decode. Same result as
-    append_kv of those rows followed by paged_decode."""
+    append_kv of those rows followed by paged_decode. `layout` as in paged_decode."""
     return _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
-                   sm_scale, out, workspace, groups)
+                   sm_scale, out, workspace, groups, layout)
 
 
 def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages, sm_scale,
-            out, workspace, groups):
+            out, workspace, groups, layout=0):
     _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
         _i32(t, n)
@@ -361,13 +368,13 @@ def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
                                               v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
                                               kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
                                               dtype_code(q.dtype), out.data_ptr(), out.stride(0), ws.data_ptr(),
-                                              ws.numel(), _stream(q))
+                                              ws.numel(), layout, _stream(q))
             _lib.check(rc, "nslg_paged_decode_append")
             return out
         rc = lib.nslg_paged_decode(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
                                    kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
                                    int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
-                                   out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+                                   out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), layout, _stream(q))
         _lib.check(rc, "nslg_paged_decode")
         return out
     _require_gpu(q, groups.seq_group_slot)
@@ -385,7 +392,7 @@ def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
             kv_indices.data_ptr(), kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
             dtype_code(q.dtype), groups.seq_group_slot.data_ptr(), groups.num_groups,
             groups.prefix_pages_np.ctypes.data, groups.members_np.ctypes.data, out.data_ptr(), out.stride(0),
-            ws.data_ptr(), ws.numel(), _stream(q))
+            ws.data_ptr(), ws.numel(), layout, _stream(q))
         _lib.check(rc, "nslg_paged_decode_grouped_append")
         return out
     rc = lib.nslg_paged_decode_grouped(q.data_ptr(), q.stride(0), k_layer.data_ptr(), v_layer.data_ptr(), P, ps,
@@ -393,7 +400,7 @@ def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
                                        int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
                                        groups.seq_group_slot.data_ptr(), groups.num_groups,
                                        groups.prefix_pages_np.ctypes.data, groups.members_np.ctypes.data,
-                                       out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream(q))
+                                       out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), layout, _stream(q))
     _lib.check(rc, "nslg_paged_decode_grouped")
     return out
 
@@ -585,7 +592,11 @@ class DecodeLaunch:
     results as append_kv followed by paged_decode on the layer's pool slices.
 
     A launcher can be re-bound to the next forward's plan (rebind) when the pools,
-    batch size and head count stay: the pool geometry is then not checked again."""
+    batch size and head count stay: the pool geometry is then not checked again.
+
+    The first decode call after a (re)bind records the chunk layout of the plan in
+    the workspace under a fresh tag; the later calls of the same plan (the other
+    layers of the forward) read it instead of cutting the chunks again."""
 
     def __init__(self, k_pool: torch.Tensor, v_pool: torch.Tensor, slot_mapping: torch.Tensor,
                  kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
@@ -618,6 +629,7 @@ class DecodeLaunch:
                check: bool = True) -> "DecodeLaunch":
         """Point the launcher at another forward's plan of the same batch size."""
         B = self.B
+        self._layout = 0  # the next call records the new plan's chunk layout
         if check:
             _require_gpu(self.pools[0], slot_mapping, kv_indptr, kv_indices, kv_last_page_len)
             for t, n in ((slot_mapping, "slot_mapping"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
@@ -696,6 +708,10 @@ class DecodeLaunch:
         lib = self.lib
         out = torch.empty(out_shape, dtype=self.dtype, device=self.device)
         grp = self.groups
+        lay = self._layout  # < 0: read the layout recorded under tag -lay
+        if lay == 0:  # the first call on this plan records its chunk layout
+            lay = next(_LAYOUT_TAGS)
+            self._layout = -lay
         if rope is None:
             kn, vn = k_new.data_ptr(), v_new.data_ptr()
             if not (kn | vn | (ks | vs) * self.esize) & self.row_align:
@@ -705,7 +721,7 @@ class DecodeLaunch:
                     rc = lib.nslg_paged_decode_append(q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps,
                                                       self.indptr, self.indices, self.lpl, self.total_pages, B, Hq,
                                                       self.Hkv, D, self.scale, self.code, out.data_ptr(), Hq * D,
-                                                      self.ws.data_ptr(), self.ws.numel(), stream)
+                                                      self.ws.data_ptr(), self.ws.numel(), lay, stream)
                     _lib.check(rc, "nslg_paged_decode_append")
                 else:
                     rc = lib.nslg_paged_decode_grouped_append(
@@ -713,7 +729,7 @@ class DecodeLaunch:
                         self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
                         grp.seq_group_slot.data_ptr(), grp.num_groups, grp.prefix_pages_np.ctypes.data,
                         grp.members_np.ctypes.data, out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(),
-                        stream)
+                        lay, stream)
                     _lib.check(rc, "nslg_paged_decode_grouped_append")
                 return out
             rc = lib.nslg_append_kv(kn, vn, ks, vs, self.slots, B, kp, vp, self.P * self.ps, self.Hkv, D,
@@ -737,14 +753,15 @@ class DecodeLaunch:
         if grp is None:
             rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
                                        self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
-                                       out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
+                                       out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), lay, stream)
             _lib.check(rc, "nslg_paged_decode")
         else:
             rc = lib.nslg_paged_decode_grouped(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
                                                self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale,
                                                self.code, grp.seq_group_slot.data_ptr(), grp.num_groups,
                                                grp.prefix_pages_np.ctypes.data, grp.members_np.ctypes.data,
-                                               out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), stream)
+                                               out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), lay,
+                                               stream)
             _lib.check(rc, "nslg_paged_decode_grouped")
         return out
 

@@ -45,18 +45,18 @@ def test_host_side_argument_checks():
     assert lib.nslg_copy_pages(None, None, 0, 4, 16, 8, 128, 0, None, None, 1, None) == -1
     assert "copy_pages" in _lib.last_error()
     rc = lib.nslg_paged_decode(1, 4096, 1, 1, 100, 16, 1, 1, 1, 10, 2, 32, 8, 100, 0.1, 0, 1, 4096,
-                               None, 0, None)
+                               None, 0, 0, None)
     assert rc == -2  # head_dim 100 unsupported
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 32, 8, 128, 0.1, 0, 256, 4096,
-                               None, 0, None)
+                               None, 0, 0, None)
     assert rc == -4  # no workspace
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 100, 16, 1, 1, 1, 10, 2, 34, 8, 128, 0.1, 0, 256, 4096,
-                               None, 0, None)
+                               None, 0, 0, None)
     assert rc == -1  # Hq not a multiple of Hkv
     # an fp32 decode long enough to be split over keys needs its workspace
     assert lib.nslg_paged_decode_workspace_size(1, 32, 8, 128, 2048, 16, 2) > (1 << 20)
     rc = lib.nslg_paged_decode(256, 4096, 256, 256, 4096, 16, 256, 256, 256, 2048, 1, 32, 8, 128, 0.1, 2, 256,
-                               4096, None, 0, None)
+                               4096, None, 0, 0, None)
     assert rc == -4 and "workspace" in _lib.last_error()
     # prefill: the softmax scale must be positive and finite (the lazy running max
     # compares raw scores against a threshold divided by the scale)
@@ -82,7 +82,7 @@ def test_decode_append_argument_checks():
     from nanoslg_amd import _lib
     lib = _lib.load()
     geo = (256, 256, 100, 16, 256, 256, 256, 10, 2, 32, 8, 128, 0.1)  # pools .. sm_scale
-    tail = (256, 4096, None, 0, None)  # out, out_stride, workspace, bytes, stream
+    tail = (256, 4096, None, 0, 0, None)  # out, out_stride, workspace, bytes, layout, stream
     # f16: k_new missing; rows overlapping (stride < Hkv*D); unaligned row stride / pointer
     assert lib.nslg_paged_decode_append(256, 4096, None, 1024, 256, 1024, *geo, 0, *tail) == -1
     assert "k_new" in _lib.last_error()

@@ -487,7 +487,7 @@ def test_decode_writes_stay_inside_workspace_and_out(lens, Hq, Hkv, D, ps):
     ip, ix, lp = (torch.from_numpy(a).to(DEV) for a in (indptr, indices, lpl))
     rc = lib.nslg_paged_decode(qd.data_ptr(), Hq * D, kd.data_ptr(), vd.data_ptr(), P, ps, ip.data_ptr(),
                                ix.data_ptr(), lp.data_ptr(), int(indptr[-1]), B, Hq, Hkv, D,
-                               1.0 / math.sqrt(D), 0, out.data_ptr(), Hq * D, ws.data_ptr(), need,
+                               1.0 / math.sqrt(D), 0, out.data_ptr(), Hq * D, ws.data_ptr(), need, 0,
                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0, _lib.last_error()
     torch.cuda.synchronize()
@@ -805,6 +805,77 @@ def test_decode_grouped_prefix(Hq, Hkv, ps, dtype, sizes, prefix, D):
     torch.testing.assert_close(out_p, ref, atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("grouped,n_alone,own_max", [(False, 3, 4000), (True, 2, 600), (False, 40, 2500),
+                                                      (True, 30, 900)])
+def test_decode_layout_record_and_reuse_bit_exact(grouped, n_alone, own_max):
+    """The later layers of a forward read the chunk layout the first layer's call
+    recorded in the workspace (layout -t) instead of cutting the chunks again; a call
+    whose tag the workspace no longer holds (another call recorded in between) cuts
+    them itself. Outputs bit-identical to calls that always cut the chunks (layout 0),
+    plain and grouped, at a small batch (many chunks per sequence) and a larger one;
+    the first layer also against the oracle."""
+    _log(f"decode layout record/reuse grouped={grouped} alone={n_alone}")
+    K = _k()
+    rng = np.random.default_rng(90 + n_alone)
+    L, ps, Hq, Hkv, D = 3, 16, 32, 8, 128
+    sizes, prefix = ([4, 3], [40, 9]) if grouped else ([], [])
+    B = sum(sizes) + n_alone
+    order = rng.permutation(B).tolist()
+    next_page = iter(rng.permutation(np.arange(1, 12000)).tolist())
+    lens, tables, members, pos = [0] * B, [None] * B, [], 0
+    for gsz, pp in zip(sizes, prefix):
+        shared = [next(next_page) for _ in range(pp)]
+        ms = order[pos:pos + gsz]
+        pos += gsz
+        members.append(ms)
+        for b in ms:
+            own = int(rng.integers(1, own_max))
+            lens[b] = pp * ps + own
+            tables[b] = shared + [next(next_page) for _ in range(math.ceil(own / ps))]
+    for b in order[pos:]:
+        lens[b] = int(rng.integers(1, own_max))
+        tables[b] = [next(next_page) for _ in range(math.ceil(lens[b] / ps))]
+    P = 12000
+    g = torch.Generator().manual_seed(91)
+    gd = torch.Generator(device=DEV).manual_seed(91)
+    kd = torch.randn(L, P, ps, Hkv, D, generator=gd, device=DEV, dtype=torch.float16)
+    vd = torch.randn(L, P, ps, Hkv, D, generator=gd, device=DEV, dtype=torch.float16)
+    k0, v0 = kd[0].cpu(), vd[0].cpu()
+    indptr, indices, lpl = O.plan_csr(tables, lens, ps)
+    plan = (torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV), torch.from_numpy(lpl).to(DEV),
+            int(indptr[-1]))
+    groups = K.DecodeGroups(B, members, prefix, DEV) if grouped else None
+    ws_fresh, ws_rec = K.Workspace(DEV), K.Workspace(DEV)
+    # another forward's plan: the first half of the batch, no groups
+    h = max(1, B // 2)
+    ip2, ix2, lp2 = O.plan_csr(tables[:h], lens[:h], ps)
+    plan2 = (torch.from_numpy(ip2).to(DEV), torch.from_numpy(ix2).to(DEV), torch.from_numpy(lp2).to(DEV),
+             int(ip2[-1]))
+    tag = 1000 + n_alone
+    for step in range(2):
+        for layer in range(L):
+            q = torch.randn(B, Hq, D, generator=g).half().to(DEV)
+            want = K.paged_decode(q, kd[layer], vd[layer], *plan, workspace=ws_fresh, groups=groups, layout=0)
+            lay = tag if layer == 0 else -tag
+            got = K.paged_decode(q, kd[layer], vd[layer], *plan, workspace=ws_rec, groups=groups, layout=lay)
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(got), _bits(want)), (step, layer)
+            if step == 0 and layer == 0:
+                ref = O.paged_attention_ref([q[b:b + 1].cpu() for b in range(B)], k0.view(-1, Hkv, D),
+                                            v0.view(-1, Hkv, D), ps, indptr, indices, lpl, [1] * B)
+                torch.testing.assert_close(got.cpu().float(), torch.stack([r[0] for r in ref]), atol=ATOL,
+                                           rtol=RTOL)
+        tag += 1
+    # a record of another plan in between: the reusing call no longer finds its tag
+    q = torch.randn(B, Hq, D, generator=g).half().to(DEV)
+    K.paged_decode(q, kd[0], vd[0], *plan, workspace=ws_rec, groups=groups, layout=tag)
+    K.paged_decode(q[:h], kd[0], vd[0], *plan2, workspace=ws_rec, layout=tag + 1)
+    got = K.paged_decode(q, kd[1], vd[1], *plan, workspace=ws_rec, groups=groups, layout=-tag)
+    want = K.paged_decode(q, kd[1], vd[1], *plan, workspace=ws_fresh, groups=groups, layout=0)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
 def test_decode_grouped_rejects_bad_groups():
     K = _k()
     lib = __import__("nanoslg_amd._lib", fromlist=["load"]).load()
@@ -826,7 +897,7 @@ def test_decode_grouped_rejects_bad_groups():
         return lib.nslg_paged_decode_grouped(q.data_ptr(), Hq * D, pool.data_ptr(), pool.data_ptr(), 8, ps,
                                              ip.data_ptr(), ix.data_ptr(), lp.data_ptr(), B, B, Hq, Hkv, D, 0.1, 0,
                                              slot.data_ptr(), num_groups, pp, mm, q.data_ptr(), Hq * D,
-                                             ws.data_ptr(), ws.numel(), None)
+                                             ws.data_ptr(), ws.numel(), 0, None)
     assert call(0, [], []) == -2               # no group
     assert call(33, [1] * 33, [0]) == -2       # too many groups
     assert call(1, [0], [0, 1]) == -1          # empty prefix
