@@ -376,7 +376,7 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
     if constexpr (kGrouped) units += ga.num_groups;
     mapped = u < units && b >= 0 && b < p.batch && nchunks > 0 && cstart >= 0 && cstart <= chunk &&
              chunk < cstart + nchunks && idx_off >= 0 && (int64_t)idx_off + np_seq <= p.total_pages &&
-             t_begin >= 0 && t_begin < t_end && t_end <= np_seq * p.page_size;
+             t_begin >= 0 && t_begin < t_end && (int64_t)t_end <= (int64_t)np_seq * p.page_size;
   }
   const bool record = p.layout_mode > 0 && blockIdx.y == 0 && threadIdx.x == 0;
   if (!mapped) {
