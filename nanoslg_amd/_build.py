@@ -12,12 +12,16 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 OBJ_DIR = CSRC / "_obj"
 LIB_PATH = PKG_DIR / "libnslg_kv.so"
+# the CPython fast-call binding of the per-step entry points (links libnslg_kv.so)
+FAST_SRC = CSRC / "fastcall.c"
+FAST_PATH = PKG_DIR / ("_nslg_fast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -78,9 +82,25 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    _build_fast()
     if verbose:
-        print(f"[nanoslg_amd] built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+        print(f"[nanoslg_amd] built {LIB_PATH} from {len(srcs)} sources and {FAST_PATH.name}", file=sys.stderr)
     return LIB_PATH
+
+
+def _build_fast() -> None:
+    """Compile the fast-call binding (host C, the system compiler) against the
+    library just linked; it finds the library next to itself at run time."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler (gcc) for the fast-call binding")
+    tmp = FAST_PATH.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Wno-unused-parameter", f"-I{sysconfig.get_paths()['include']}",
+           str(FAST_SRC), "-o", str(tmp), f"-L{PKG_DIR}", "-lnslg_kv", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"fast-call binding failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, FAST_PATH)
 
 
 if __name__ == "__main__":

@@ -87,6 +87,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_fast = None
 _lock = threading.Lock()
 
 
@@ -116,6 +117,23 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = lib
         return lib
+
+
+def fast():
+    """The CPython fast-call binding of the per-step entry points (built with the
+    library): the same C functions as the ctypes ones of `load()`, called with the
+    same Python arguments in a fraction of ctypes' conversion time."""
+    global _fast
+    if _fast is not None:
+        return _fast
+    load()
+    try:
+        from . import _nslg_fast
+    except ImportError as e:
+        raise KernelLibraryError(f"the fast-call binding of {LIB_PATH} is not built or does not load ({e}); "
+                                 "run `python -m nanoslg_amd._build` (or __graft_entry__.build()) first") from e
+    _fast = _nslg_fast
+    return _fast
 
 
 def last_error() -> str:

@@ -474,10 +474,10 @@ def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_si
     step's pages), else new tensors (indices exactly this step's pages)."""
     B = kv_indptr.numel() - 1
     if out is not None:
-        rc = _lib.load().nslg_decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                                              kv_last_page_len.data_ptr(), B, int(page_size),
-                                              new_page.ctypes.data if new_page_ptr is None else new_page_ptr,
-                                              *out.ptrs, *pool_args, _stream(kv_indptr))
+        rc = _lib.fast().decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                          kv_last_page_len.data_ptr(), B, int(page_size),
+                                          new_page.ctypes.data if new_page_ptr is None else new_page_ptr,
+                                          *out.ptrs, *pool_args, _stream(kv_indptr))
         _lib.check(rc, "nslg_decode_plan_step")
         return out.indptr, out.indices, out.lpl, out.slot, out.pos, out.new_pages
     cap = kv_indices.numel() + num_new
@@ -607,6 +607,10 @@ class DecodeLaunch:
         if num_qo_heads % Hkv:
             raise ValueError(f"DecodeLaunch: Hq={num_qo_heads} is not a multiple of Hkv={Hkv}")
         self.lib = _lib.load()
+        # the per-layer calls go through the fast-call binding (same entry points)
+        fast = _lib.fast()
+        self._f_decode_append, self._f_grouped_append = fast.paged_decode_append, fast.paged_decode_grouped_append
+        self._f_decode, self._f_grouped, self._f_rope = fast.paged_decode, fast.paged_decode_grouped, fast.rope_append
         self.device, self.dtype = k_pool.device, k_pool.dtype
         self.dev_index = k_pool.get_device()
         self.code = dtype_code(k_pool.dtype)
@@ -718,13 +722,13 @@ class DecodeLaunch:
                 # one launch: each sequence's new row is written by the chunk that reads it
                 q_ptr, q_stride = q.data_ptr(), qst[0]
                 if grp is None:
-                    rc = lib.nslg_paged_decode_append(q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps,
-                                                      self.indptr, self.indices, self.lpl, self.total_pages, B, Hq,
-                                                      self.Hkv, D, self.scale, self.code, out.data_ptr(), Hq * D,
-                                                      self.ws.data_ptr(), self.ws.numel(), lay, stream)
+                    rc = self._f_decode_append(q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps, self.indptr,
+                                               self.indices, self.lpl, self.total_pages, B, Hq, self.Hkv, D,
+                                               self.scale, self.code, out.data_ptr(), Hq * D, self.ws.data_ptr(),
+                                               self.ws.numel(), lay, stream)
                     _lib.check(rc, "nslg_paged_decode_append")
                 else:
-                    rc = lib.nslg_paged_decode_grouped_append(
+                    rc = self._f_grouped_append(
                         q_ptr, q_stride, kn, ks, vn, vs, kp, vp, self.P, self.ps, self.indptr, self.indices,
                         self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
                         grp.seq_group_slot.data_ptr(), grp.num_groups, grp.prefix_pages_np.ctypes.data,
@@ -744,24 +748,23 @@ class DecodeLaunch:
             if cos.get_device() != di:
                 raise ValueError(f"DecodeLaunch: rope tables must be on {self.device}")
             q_rot = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
-            rc = lib.nslg_rope_append(q.data_ptr(), q.stride(0), q_rot.data_ptr(), Hq * D, k_new.data_ptr(), ks,
-                                      v_new.data_ptr(), vs, pos.data_ptr(), self.slots, B, cos.data_ptr(),
-                                      sin.data_ptr(), cos.stride(0), cos.shape[0], Hq, self.Hkv, D, kp, vp,
-                                      self.P * self.ps, self.code, stream)
+            rc = self._f_rope(q.data_ptr(), q.stride(0), q_rot.data_ptr(), Hq * D, k_new.data_ptr(), ks,
+                              v_new.data_ptr(), vs, pos.data_ptr(), self.slots, B, cos.data_ptr(), sin.data_ptr(),
+                              cos.stride(0), cos.shape[0], Hq, self.Hkv, D, kp, vp, self.P * self.ps, self.code,
+                              stream)
             _lib.check(rc, "nslg_rope_append")
             q_ptr, q_stride = q_rot.data_ptr(), Hq * D
         if grp is None:
-            rc = lib.nslg_paged_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
-                                       self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
-                                       out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), lay, stream)
+            rc = self._f_decode(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices, self.lpl,
+                                self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code, out.data_ptr(), Hq * D,
+                                self.ws.data_ptr(), self.ws.numel(), lay, stream)
             _lib.check(rc, "nslg_paged_decode")
         else:
-            rc = lib.nslg_paged_decode_grouped(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices,
-                                               self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale,
-                                               self.code, grp.seq_group_slot.data_ptr(), grp.num_groups,
-                                               grp.prefix_pages_np.ctypes.data, grp.members_np.ctypes.data,
-                                               out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), lay,
-                                               stream)
+            rc = self._f_grouped(q_ptr, q_stride, kp, vp, self.P, self.ps, self.indptr, self.indices, self.lpl,
+                                 self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
+                                 grp.seq_group_slot.data_ptr(), grp.num_groups, grp.prefix_pages_np.ctypes.data,
+                                 grp.members_np.ctypes.data, out.data_ptr(), Hq * D, self.ws.data_ptr(),
+                                 self.ws.numel(), lay, stream)
             _lib.check(rc, "nslg_paged_decode_grouped")
         return out
 

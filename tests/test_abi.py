@@ -195,3 +195,52 @@ def test_attention_kernel_rejects_rows_not_16_byte_aligned():
                                          dt, A, out_stride, None, 0, None)
         assert rc == -1 and "16-byte" in _lib.last_error(), (dt, q_stride, out_stride, _lib.last_error())
     assert _lib.NSLG_ECAPTURE == -5
+
+
+def test_fast_binding_calls_the_same_entry_points():
+    """The fast-call binding of the per-step entry points (_nslg_fast) calls the same C
+    functions as ctypes: the same statuses and error text from the host-side checks
+    (no device work), and it refuses a wrong argument count or an int32 out of range."""
+    from nanoslg_amd import _lib
+    lib, fast = _lib.load(), _lib.fast()
+    A = 4096
+    dec = (A, 4096, A, A, 100, 16, A, A, A, 10, 2, 32, 8, 100, 0.1, 0, A, 4096, None, 0, 0, None)
+    assert fast.paged_decode(*dec) == lib.nslg_paged_decode(*dec) == -2
+    assert "head_dim" in _lib.last_error()
+    app = (A, 4096, None, 1024, A, 1024, A, A, 100, 16, A, A, A, 10, 2, 32, 8, 128, 0.1, 0, A, 4096, None, 0, 0, None)
+    assert fast.paged_decode_append(*app) == lib.nslg_paged_decode_append(*app) == -1
+    assert "k_new" in _lib.last_error()
+    zero = (None, 0, None, 0, None, 0, A, A, 100, 16, A, A, A, 0, 0, 32, 8, 128, 0.1, 0, None, 4096, None, 0, 0, None)
+    assert fast.paged_decode_append(*zero) == 0
+    members = (ctypes.c_int32 * 16)(0, 1, *([-1] * 14))
+    prefix = (ctypes.c_int32 * 1)(4)
+    mp, pp = ctypes.addressof(members), ctypes.addressof(prefix)
+    grp = (A, 4096, A, A, 100, 16, A, A, A, 10, 2, 32, 8, 128, 0.1, 0, A, 0, pp, mp, A, 4096, None, 0, 0, None)
+    assert fast.paged_decode_grouped(*grp) == lib.nslg_paged_decode_grouped(*grp) == -2  # no group
+    gap = (A, 4096, None, 1024, A, 1024, A, A, 100, 16, A, A, A, 10, 2, 32, 8, 128, 0.1, 0, A, 1, pp, mp, A, 4096,
+           None, 0, 0, None)
+    assert fast.paged_decode_grouped_append(*gap) == lib.nslg_paged_decode_grouped_append(*gap) == -1
+    z = (None, None, 0, 0, 0, 0, 0)
+    plan = (1, 1, 1, 513, 16, 1, 2, 2, 2, 2, 2, 2, *z, None)
+    assert fast.decode_plan_step(*plan) == lib.nslg_decode_plan_step(*plan) == -2
+    rope = (A, 4096, A, 4096, A, 1024, A, 1024, A, A, 4, A, A, 96, 100, 32, 8, 96, A, A, 64, 0, None)
+    assert fast.rope_append(*rope) == lib.nslg_rope_append(*rope) == -2
+    with pytest.raises(TypeError):
+        fast.paged_decode(*dec[:-1])
+    with pytest.raises(OverflowError):
+        fast.paged_decode(*dec[:10], 1 << 40, *dec[11:])  # batch is an int32
+
+
+def test_fast_binding_signatures_match_the_header():
+    """Each function of the fast-call binding converts its arguments by the same types
+    as the ctypes declaration of its entry point (which test_library_exports_every_
+    declared_symbol ties to include/nslg_kv.h)."""
+    import re
+    from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
+    from nanoslg_amd import _lib
+    code = {c_void_p: "p", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
+    src = (ROOT / "nanoslg_amd" / "csrc" / "fastcall.c").read_text()
+    found = re.findall(r'parse\("(\w+)", "(\w+)"', src)
+    assert len(found) == 6
+    for fn, sig in found:
+        assert sig == "".join(code[t] for t in _lib.SIGNATURES["nslg_" + fn][1]), fn
