@@ -1,7 +1,8 @@
 /*
- * _nslg_fast: a CPython binding of the C-ABI entry points a decode step calls every
- * layer or every step (nslg_kv.h), for the host path of small batches, where the
- * Python of a step, not the GPU, sets the pace. Each function takes the entry
+ * _nslg_fast: a CPython binding of the C-ABI entry points a forward calls every
+ * layer or every step (nslg_kv.h): decode, the planners, append, prefill, page
+ * zeroing and copies. Small decode batches and the first chunks of a chunked
+ * prefill are paced by the host's Python, not the GPU. Each function takes the entry
  * point's arguments in order, as Python ints (pointers, sizes) and a float (the
  * softmax scale), converts them with the C API's fast-call convention and calls
  * the entry point; it returns the entry point's status. ctypes converts the same
@@ -144,6 +145,71 @@ static PyObject* rope_append(PyObject* self, PyObject* const* args, Py_ssize_t n
   return PyLong_FromLong(rc);
 }
 
+static PyObject* append_kv(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("append_kv", "ppqqpippqiiip", args, n, a)) return NULL;
+  const int rc = nslg_append_kv(a[0].p, a[1].p, a[2].q, a[3].q, a[4].p, a[5].i, a[6].p, a[7].p, a[8].q, a[9].i,
+                                a[10].i, a[11].i, a[12].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* block_table_csr(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("block_table_csr", "pqpppppqppqip", args, n, a)) return NULL;
+  const int rc = nslg_block_table_csr(a[0].p, a[1].q, a[2].p, a[3].p, a[4].p, a[5].p, a[6].p, a[7].q, a[8].p, a[9].p,
+                                      a[10].q, a[11].i, a[12].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* forward_plan(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("forward_plan", "ppppppiiippppp", args, n, a)) return NULL;
+  const int rc = nslg_forward_plan(a[0].p, a[1].p, a[2].p, a[3].p, a[4].p, a[5].p, a[6].i, a[7].i, a[8].i, a[9].p,
+                                   a[10].p, a[11].p, a[12].p, a[13].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* paged_prefill(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("paged_prefill", "pqpqippqipppiiiifipqpzp", args, n, a)) return NULL;
+  const int rc = nslg_paged_prefill(a[0].p, a[1].q, a[2].p, a[3].q, a[4].i, a[5].p, a[6].p, a[7].q, a[8].i, a[9].p,
+                                    a[10].p, a[11].p, a[12].i, a[13].i, a[14].i, a[15].i, a[16].f, a[17].i, a[18].p,
+                                    a[19].q, a[20].p, a[21].z, a[22].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* paged_prefill_grid(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("paged_prefill_grid", "pqppiqippqipppiiiifipqpzp", args, n, a)) return NULL;
+  const int rc = nslg_paged_prefill_grid(a[0].p, a[1].q, a[2].p, a[3].p, a[4].i, a[5].q, a[6].i, a[7].p, a[8].p,
+                                         a[9].q, a[10].i, a[11].p, a[12].p, a[13].p, a[14].i, a[15].i, a[16].i,
+                                         a[17].i, a[18].f, a[19].i, a[20].p, a[21].q, a[22].p, a[23].z, a[24].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* zero_pages(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("zero_pages", "ppiqiiiipip", args, n, a)) return NULL;
+  const int rc = nslg_zero_pages(a[0].p, a[1].p, a[2].i, a[3].q, a[4].i, a[5].i, a[6].i, a[7].i, a[8].p, a[9].i,
+                                 a[10].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* copy_pages(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("copy_pages", "ppiqiiiippip", args, n, a)) return NULL;
+  const int rc = nslg_copy_pages(a[0].p, a[1].p, a[2].i, a[3].q, a[4].i, a[5].i, a[6].i, a[7].i, a[8].p, a[9].p,
+                                 a[10].i, a[11].p);
+  return PyLong_FromLong(rc);
+}
+
 static PyMethodDef methods[] = {
     {"paged_decode_append", (PyCFunction)(void (*)(void))paged_decode_append, METH_FASTCALL,
      "nslg_paged_decode_append: the entry point's arguments in order; returns its status"},
@@ -157,6 +223,20 @@ static PyMethodDef methods[] = {
      "nslg_decode_plan_step: the entry point's arguments in order; returns its status"},
     {"rope_append", (PyCFunction)(void (*)(void))rope_append, METH_FASTCALL,
      "nslg_rope_append: the entry point's arguments in order; returns its status"},
+    {"append_kv", (PyCFunction)(void (*)(void))append_kv, METH_FASTCALL,
+     "nslg_append_kv: the entry point's arguments in order; returns its status"},
+    {"block_table_csr", (PyCFunction)(void (*)(void))block_table_csr, METH_FASTCALL,
+     "nslg_block_table_csr: the entry point's arguments in order; returns its status"},
+    {"forward_plan", (PyCFunction)(void (*)(void))forward_plan, METH_FASTCALL,
+     "nslg_forward_plan: the entry point's arguments in order; returns its status"},
+    {"paged_prefill", (PyCFunction)(void (*)(void))paged_prefill, METH_FASTCALL,
+     "nslg_paged_prefill: the entry point's arguments in order; returns its status"},
+    {"paged_prefill_grid", (PyCFunction)(void (*)(void))paged_prefill_grid, METH_FASTCALL,
+     "nslg_paged_prefill_grid: the entry point's arguments in order; returns its status"},
+    {"zero_pages", (PyCFunction)(void (*)(void))zero_pages, METH_FASTCALL,
+     "nslg_zero_pages: the entry point's arguments in order; returns its status"},
+    {"copy_pages", (PyCFunction)(void (*)(void))copy_pages, METH_FASTCALL,
+     "nslg_copy_pages: the entry point's arguments in order; returns its status"},
     {NULL, NULL, 0, NULL}};
 
 static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_nslg_fast",

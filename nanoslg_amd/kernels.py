@@ -101,9 +101,9 @@ def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: torch.Tens
     if nk != T or nv != T:
         raise ValueError(f"append_kv: {T} slots for {nk} k rows / {nv} v rows")
     slots = k_pool.numel() // (Hkv * D)
-    rc = _lib.load().nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(),
-                                    T, k_pool.data_ptr(), v_pool.data_ptr(), slots, Hkv, D,
-                                    dtype_code(k_pool.dtype), _stream(k_pool))
+    rc = _lib.fast().append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(), T,
+                               k_pool.data_ptr(), v_pool.data_ptr(), slots, Hkv, D, dtype_code(k_pool.dtype),
+                               _stream(k_pool))
     _lib.check(rc, "nslg_append_kv")
 
 
@@ -124,9 +124,9 @@ def _append_kv_layer(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: tor
     T = slot_mapping.numel()
     if nk != T or nv != T:
         raise ValueError(f"append_kv: {T} slots for {nk} k rows / {nv} v rows")
-    rc = _lib.load().nslg_append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(),
-                                    T, k_layer.data_ptr(), v_layer.data_ptr(), k_layer.shape[0] * k_layer.shape[1],
-                                    Hkv, D, _DTYPE_CODE[dt], _stream(k_layer))
+    rc = _lib.fast().append_kv(k_new.data_ptr(), v_new.data_ptr(), ks, vs, slot_mapping.data_ptr(), T,
+                               k_layer.data_ptr(), v_layer.data_ptr(), k_layer.shape[0] * k_layer.shape[1], Hkv, D,
+                               _DTYPE_CODE[dt], _stream(k_layer))
     _lib.check(rc, "nslg_append_kv")
 
 
@@ -199,9 +199,8 @@ def zero_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, page_ids: torch.Tenso
     _require_gpu(k_pool, v_pool, page_ids)
     _i32(page_ids, "page_ids")
     L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
-    rc = _lib.load().nslg_zero_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D,
-                                     dtype_code(k_pool.dtype), page_ids.data_ptr(), page_ids.numel(),
-                                     _stream(k_pool))
+    rc = _lib.fast().zero_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D, dtype_code(k_pool.dtype),
+                                page_ids.data_ptr(), page_ids.numel(), _stream(k_pool))
     _lib.check(rc, "nslg_zero_pages")
 
 
@@ -214,9 +213,8 @@ def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_ids: torch.Tensor
     if src_ids.numel() != dst_ids.numel():
         raise ValueError("copy_pages: src/dst length mismatch")
     L, P, ps, Hkv, D = _pool_geom(k_pool, v_pool)
-    rc = _lib.load().nslg_copy_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D,
-                                     dtype_code(k_pool.dtype), src_ids.data_ptr(), dst_ids.data_ptr(),
-                                     src_ids.numel(), _stream(k_pool))
+    rc = _lib.fast().copy_pages(k_pool.data_ptr(), v_pool.data_ptr(), L, P, ps, Hkv, D, dtype_code(k_pool.dtype),
+                                src_ids.data_ptr(), dst_ids.data_ptr(), src_ids.numel(), _stream(k_pool))
     _lib.check(rc, "nslg_copy_pages")
 
 
@@ -474,10 +472,10 @@ def _decode_plan_step(kv_indptr, kv_indices, kv_last_page_len, new_page, page_si
     step's pages), else new tensors (indices exactly this step's pages)."""
     B = kv_indptr.numel() - 1
     if out is not None:
-        rc = _lib.fast().decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                                          kv_last_page_len.data_ptr(), B, int(page_size),
-                                          new_page.ctypes.data if new_page_ptr is None else new_page_ptr,
-                                          *out.ptrs, *pool_args, _stream(kv_indptr))
+        rc = _lib.fast().decode_plan_step(kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B,
+                                          int(page_size),
+                                          new_page.ctypes.data if new_page_ptr is None else new_page_ptr, *out.ptrs,
+                                          *pool_args, _stream(kv_indptr))
         _lib.check(rc, "nslg_decode_plan_step")
         return out.indptr, out.indices, out.lpl, out.slot, out.pos, out.new_pages
     cap = kv_indices.numel() + num_new
@@ -542,10 +540,10 @@ def block_table_csr(tables: torch.Tensor, row_offset: torch.Tensor, pages_have: 
 def _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr,
                      kv_indices, total_pages, B):
     """block_table_csr without the argument checks (the cache manager's own tables)."""
-    rc = _lib.load().nslg_block_table_csr(tables.data_ptr(), tables.numel(), row_offset.data_ptr(),
-                                          pages_have.data_ptr(), synced.data_ptr(), patch_indptr.data_ptr(),
-                                          patch.data_ptr(), int(patch_total), kv_indptr.data_ptr(),
-                                          kv_indices.data_ptr(), int(total_pages), int(B), _stream(tables))
+    rc = _lib.fast().block_table_csr(tables.data_ptr(), tables.numel(), row_offset.data_ptr(), pages_have.data_ptr(),
+                                     synced.data_ptr(), patch_indptr.data_ptr(), patch.data_ptr(), int(patch_total),
+                                     kv_indptr.data_ptr(), kv_indices.data_ptr(), int(total_pages), int(B),
+                                     _stream(tables))
     _lib.check(rc, "nslg_block_table_csr")
 
 
@@ -573,9 +571,9 @@ def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages
     base = buf.data_ptr()
     o1, o2 = 4 * B * iw, 8 * B * iw
     o3 = o2 + 4 * T
-    rc = _lib.load().nslg_forward_plan(kv_indptr.data_ptr(), kv_indices.data_ptr(), start.data_ptr(),
-                                       new_tokens.data_ptr(), input_offsets.data_ptr(), pages_allocated.data_ptr(),
-                                       B, iw, page_size, base, base + o1, base + o2, base + o3, _stream(kv_indptr))
+    rc = _lib.fast().forward_plan(kv_indptr.data_ptr(), kv_indices.data_ptr(), start.data_ptr(),
+                                  new_tokens.data_ptr(), input_offsets.data_ptr(), pages_allocated.data_ptr(), B, iw,
+                                  page_size, base, base + o1, base + o2, base + o3, _stream(kv_indptr))
     _lib.check(rc, "nslg_forward_plan")
     return slot, pos, rows, qo
 
@@ -787,22 +785,22 @@ def _paged_prefill_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int,
                              kv_last_page_len, workspace=workspace, q_rows=q_rows, grid_width=grid_width)
     T, Hq = q.shape[0], q.shape[1]
     out = torch.empty((T, Hq, D), dtype=dt, device=q.device)
-    lib = _lib.load()
+    lib, fast = _lib.load(), _lib.fast()
     ws = workspace.get(int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q))))
     stream = _stream(k_layer)
     scale = 1.0 / math.sqrt(D)
     if q_rows is not None:
-        rc = lib.nslg_paged_prefill_grid(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), q_rows.data_ptr(),
-                                         int(grid_width), int(total_q), int(max_q), k_layer.data_ptr(),
-                                         v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                                         kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale, _DTYPE_CODE[dt],
-                                         out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
+        rc = fast.paged_prefill_grid(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), q_rows.data_ptr(),
+                                     int(grid_width), int(total_q), int(max_q), k_layer.data_ptr(),
+                                     v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                                     kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale, _DTYPE_CODE[dt],
+                                     out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "nslg_paged_prefill_grid")
         return out
-    rc = lib.nslg_paged_prefill(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), int(total_q), int(max_q),
-                                k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
-                                kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale,
-                                _DTYPE_CODE[dt], out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
+    rc = fast.paged_prefill(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), int(total_q), int(max_q),
+                            k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                            kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale, _DTYPE_CODE[dt],
+                            out.data_ptr(), Hq * D, ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "nslg_paged_prefill")
     return out
 

@@ -241,6 +241,6 @@ def test_fast_binding_signatures_match_the_header():
     code = {c_void_p: "p", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
     src = (ROOT / "nanoslg_amd" / "csrc" / "fastcall.c").read_text()
     found = re.findall(r'parse\("(\w+)", "(\w+)"', src)
-    assert len(found) == 6
+    assert len(found) == 13
     for fn, sig in found:
         assert sig == "".join(code[t] for t in _lib.SIGNATURES["nslg_" + fn][1]), fn
