@@ -22,6 +22,9 @@ LIB_PATH = PKG_DIR / "libnslg_kv.so"
 # the CPython fast-call binding of the per-step entry points (links libnslg_kv.so)
 FAST_SRC = CSRC / "fastcall.c"
 FAST_PATH = PKG_DIR / ("_nslg_fast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+# the host-side forward planner (plain C over the CPython API, no GPU code)
+HOST_SRC = CSRC / "host_plan.c"
+HOST_PATH = PKG_DIR / ("_nslg_host" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -83,24 +86,39 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
     _build_fast()
+    _build_host()
     if verbose:
-        print(f"[nanoslg_amd] built {LIB_PATH} from {len(srcs)} sources and {FAST_PATH.name}", file=sys.stderr)
+        print(f"[nanoslg_amd] built {LIB_PATH} from {len(srcs)} sources, {FAST_PATH.name} and {HOST_PATH.name}",
+              file=sys.stderr)
     return LIB_PATH
+
+
+def _cc() -> str:
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler (gcc) for the CPython extensions")
+    return cc
+
+
+def _build_ext(src: Path, out: Path, link: list[str]) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [_cc(), "-O2", "-shared", "-fPIC", "-Wall", "-Wno-unused-parameter",
+           f"-I{sysconfig.get_paths()['include']}", str(src), "-o", str(tmp), *link]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{src.name} failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
 
 
 def _build_fast() -> None:
     """Compile the fast-call binding (host C, the system compiler) against the
     library just linked; it finds the library next to itself at run time."""
-    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
-    if not cc:
-        raise RuntimeError("no C compiler (gcc) for the fast-call binding")
-    tmp = FAST_PATH.with_suffix(".so.tmp")
-    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Wno-unused-parameter", f"-I{sysconfig.get_paths()['include']}",
-           str(FAST_SRC), "-o", str(tmp), f"-L{PKG_DIR}", "-lnslg_kv", "-Wl,-rpath,$ORIGIN"]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"fast-call binding failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, FAST_PATH)
+    _build_ext(FAST_SRC, FAST_PATH, [f"-L{PKG_DIR}", "-lnslg_kv", "-Wl,-rpath,$ORIGIN"])
+
+
+def _build_host() -> None:
+    """Compile the host-side forward planner (host C, no library to link)."""
+    _build_ext(HOST_SRC, HOST_PATH, [])
 
 
 if __name__ == "__main__":

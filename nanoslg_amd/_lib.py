@@ -136,6 +136,24 @@ def fast():
     return _fast
 
 
+_host = None
+
+
+def host():
+    """The host-side forward planner (`_nslg_host`, plain C over the CPython API;
+    built with the library, no GPU calls)."""
+    global _host
+    if _host is not None:
+        return _host
+    try:
+        from . import _nslg_host
+    except ImportError as e:
+        raise KernelLibraryError(f"the host planner extension is not built or does not load ({e}); "
+                                 "run `python -m nanoslg_amd._build` (or __graft_entry__.build()) first") from e
+    _host = _nslg_host
+    return _host
+
+
 def last_error() -> str:
     msg = load().nslg_last_error()
     return msg.decode() if msg else ""

@@ -53,6 +53,11 @@ def _default_kernels():
     return kernels
 
 
+def _host_planner():
+    from . import _lib
+    return _lib.host().plan_forward
+
+
 # --------------------------------------------------------------------------------------
 # configuration
 # --------------------------------------------------------------------------------------
@@ -270,19 +275,36 @@ class _PlanStaging:
                 buf = torch.empty(n, dtype=torch.int32, pin_memory=True)
                 self.host[k], self.host_np[k] = buf, buf.numpy()
 
-    def upload(self, parts: List[np.ndarray], total: int, extra: int = 0) -> torch.Tensor:
-        """The concatenated parts on the device, followed by `extra` entries left
-        uninitialised (device outputs of the same forward)."""
+    def take(self, total: int = 0) -> Tuple[int, np.ndarray]:
+        """The next ring buffer (slot, its numpy view), holding at least `total`
+        entries, free to write: the copy that last read it has completed."""
         k = self.next
         self.next = (k + 1) % self.RING
         if self.pending[k]:
             self.copied[k].synchronize()
+            self.pending[k] = False
+        return k, self.grow(k, total)
+
+    def grow(self, k: int, total: int) -> np.ndarray:
+        """Slot k's buffer, replaced by a larger one if it holds fewer than `total`."""
         buf = self.host[k]
         if buf is None or buf.numel() < total:
             buf = torch.empty(max(total, 1 << 12) * 2, dtype=torch.int32, pin_memory=True)
             self.host[k], self.host_np[k] = buf, buf.numpy()
+        return self.host_np[k]
+
+    def upload(self, parts: List[np.ndarray], total: int, extra: int = 0) -> torch.Tensor:
+        """The concatenated parts on the device, followed by `extra` entries left
+        uninitialised (device outputs of the same forward)."""
+        k, host = self.take(total)
         if total:  # one pass over every part (each cast to int32 as it is written)
-            np.concatenate(parts, out=self.host_np[k][:total], casting="unsafe")
+            np.concatenate(parts, out=host[:total], casting="unsafe")
+        return self.send(k, total, extra)
+
+    def send(self, k: int, total: int, extra: int = 0) -> torch.Tensor:
+        """Slot k's first `total` entries, written by the caller, copied to a new
+        device buffer of total + extra entries."""
+        buf = self.host[k]
         self.pending[k] = True
         size = max(total + extra, 1)
         if 4 * total <= self.SIDE_STREAM_BYTES:
@@ -981,6 +1003,19 @@ class PagedCacheContext(CacheContext):
                 self._plan = plan
                 cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
                 return
+        if not (self._is_decode and iw == 1) and cache.NATIVE_PLAN and hasattr(cache.kernels, "_forward_plan"):
+            T = sum(self.new_token_counts)
+            if T >= self.DEVICE_PLAN_TOKENS:
+                got = cache._plan_forward_native(states, self.new_token_counts, self.input_offsets, iw, T,
+                                                 list(zero_pages) if zero_pages else None)
+                if got is not None:
+                    self._plan, nz = got
+                    self.cow_pairs = []
+                    self._max_q = max(self.new_token_counts)
+                    self._uniform_rows = T == B * iw
+                    if nz:  # zero-on-alloc of the pages this forward's extensions took
+                        cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
+                    return
         # Below, the host works per sequence and per written page only. The CSR block
         # table itself (kv_cache.py:598-615) is built on the device from the cache's
         # device-resident block tables (PagedKVCache._plan_upload).
@@ -1208,10 +1243,67 @@ class PagedKVCache(KVCacheManager):
         self._newp = None  # (batch, int32 [batch] opened-page list, -1 between steps, its address)
         # the block tables on the device (room for every pool page twice before growing)
         self._tables = _BlockTableArena(self.pool.device, 2 * cfg.max_pages + 4096)
+        self._host_plan_buf = np.zeros(1 << 12, np.int32)  # the host planner's output off the GPU
         if self.pool.device.type == "cuda":
             _staging(self.pool.device).reserve(self.STAGING_INTS)
 
     STAGING_INTS = 1 << 16  # pinned plan-upload buffers (int32 each) set up with the cache
+
+    # the host part of a device-planned forward in one native call (False: the numpy
+    # path of PagedCacheContext, which takes every forward the native call declines)
+    NATIVE_PLAN = True
+
+    def _plan_forward_native(self, states, ntoks, offsets, iw, T, zero_pages):
+        """The host part of a forward whose per-token plan is expanded on the device,
+        in one call of the host planner (`_nslg_host.plan_forward`): the written
+        pages' tokens_used, the pages to zero, the CSR pointers and last-page
+        lengths, and the block-table entries the sequences' device rows lack, written
+        straight into the upload buffer; then the upload, nslg_block_table_csr and
+        nslg_forward_plan, as in PagedCacheContext and _plan_upload. Returns (plan,
+        pages to zero), or None when a page the forward writes is shared (copy-on-write
+        takes the numpy path; the call changed nothing then)."""
+        tables, pool, kern = self._tables, self.pool, self.kernels
+        for st in states:
+            tables.place(st)
+        B, ps = len(states), self.cfg.page_size
+        tail = 2 * B * iw + T + B + 1  # forward_plan's outputs: slots, positions, rows, qo_indptr
+        plan_forward = _host_planner()
+        zl = zero_pages if zero_pages else None
+        args = (states, ntoks, offsets, ps, pool.ref_count, pool.tokens_used, pool._mark, zl)
+        cuda = pool.device.type == "cuda"
+        if cuda:
+            stg = _staging(pool.device)
+            k, host = stg.take()
+        else:
+            k, host = -1, self._host_plan_buf
+        res = plan_forward(*args, host)
+        if isinstance(res, int):  # the buffer is too small: nothing was written
+            if cuda:
+                host = stg.grow(k, -res)
+            else:
+                host = self._host_plan_buf = np.zeros(2 * -res, np.int32)
+            res = plan_forward(*args, host)
+        if res is None:
+            return None
+        total, total_pages, npatch, nz = res
+        extra = max(total_pages, 1) + tail
+        if cuda:
+            dev = stg.send(k, total, extra)
+        else:
+            dev = torch.zeros(total + extra, dtype=torch.int32)
+            dev[:total] = torch.from_numpy(host[:total])
+        sizes = [B + 1, B, 0, 0, nz, B, B, B, B, B, B, B, B + 1, max(npatch, 1), max(total_pages, 1), tail]
+        (d_indptr, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch,
+         d_idx, fp_out) = dev.split(sizes)
+        kern._block_table_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch, npatch, d_indptr, d_idx,
+                              total_pages, B)
+        for st in states:
+            st.synced = st.n_pages
+        slot_t, pos_t, rows_t, qo_t = kern._forward_plan(d_indptr, d_idx, d_start, d_n, d_off, d_have, B, iw, ps, T,
+                                                         out=fp_out)
+        plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t, d_cs, d_cd, d_zero,
+                                         total_pages, T)
+        return plan, nz
 
     def _plan_upload(self, states, indptr, parts, tail=0):
         """One upload of a forward's host-built plan arrays (`parts`, after the CSR

@@ -44,6 +44,20 @@ def test_random_serving_traffic_shapes_on_gpu(seed, ps, pages, HQ, HKV, D, dtype
     R.run_traffic(seed, ps, pages, env)
 
 
+@pytest.mark.parametrize("native", [True, False])
+@pytest.mark.parametrize("seed,ps,pages", [(21, 4, 48), (22, 1, 60), (23, 16, 12), (25, 3, 40), (26, 8, 40)])
+def test_random_serving_traffic_device_planned_on_gpu(monkeypatch, seed, ps, pages, native):
+    """The same traffic with every forward that is not a plain decode step planned on
+    the device (nslg_block_table_csr, nslg_forward_plan), its host part from the
+    native planner or from the numpy path."""
+    import test_host_random as R
+    from nanoslg_amd import kv_cache as KC
+    print(f"device-planned traffic seed={seed} ps={ps} pages={pages} native={native}", flush=True)
+    monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", 1)
+    monkeypatch.setattr(KC.PagedKVCache, "NATIVE_PLAN", native)
+    R.run_traffic(seed, ps, pages, GPU)
+
+
 @pytest.mark.parametrize("seed", [1, 2, 3, 4, 5])
 def test_random_contiguous_traffic_on_gpu(seed):
     import test_host_random as R

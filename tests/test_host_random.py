@@ -160,6 +160,17 @@ def test_random_serving_traffic_with_a_small_block_table_arena(seed, ps, pages):
     run_traffic(seed, ps, pages, dict(CPU, arena=16))
 
 
+@pytest.mark.parametrize("native", [True, False])
+@pytest.mark.parametrize("seed,ps,pages", [(21, 4, 48), (22, 1, 60), (23, 16, 12), (25, 3, 40)])
+def test_random_serving_traffic_device_planned(monkeypatch, seed, ps, pages, native):
+    """The same traffic with every forward that is not a plain decode step planned on
+    the device (the token threshold lowered from 256 to 1), its host part from the
+    native planner or from the numpy path."""
+    monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", 1)
+    monkeypatch.setattr(KC.PagedKVCache, "NATIVE_PLAN", native)
+    run_traffic(seed, ps, pages, CPU)
+
+
 def run_traffic(seed, ps, pages, env):
     """One seeded serving run (see the module docstring); env: device (None = the
     CPU stand-in kernels), pool dtype, head shape, output tolerance."""
