@@ -445,6 +445,24 @@ int nslg_forward_plan(const int32_t* kv_indptr, const int32_t* kv_indices, const
                       int32_t* ragged_rows_out, int32_t* qo_indptr_out, nslg_stream_t stream);
 
 /*
+ * nslg_block_table_csr and nslg_forward_plan in one launch (the two device steps of
+ * a forward planned on the device, kv_cache.py:575-615): the arguments of
+ * nslg_block_table_csr, then those of nslg_forward_plan that it lacks, with
+ * pages_have standing for pages_allocated. kv_indices, the arena rows and every
+ * output are bit-identical with the two calls made in order; the plan takes each
+ * page id from the arena and the patch, as the CSR does, so no part waits for
+ * another.
+ */
+int nslg_forward_plan_csr(int32_t* tables, int64_t table_capacity, const int32_t* row_offset,
+                          const int32_t* pages_have, const int32_t* synced, const int32_t* patch_indptr,
+                          const int32_t* patch, int64_t patch_total, const int32_t* kv_indptr,
+                          int32_t* kv_indices, int64_t total_pages, const int32_t* start,
+                          const int32_t* new_tokens, const int32_t* input_offsets, int32_t batch,
+                          int32_t input_width, int32_t page_size, int32_t* slot_mapping_out,
+                          int32_t* positions_out, int32_t* ragged_rows_out, int32_t* qo_indptr_out,
+                          nslg_stream_t stream);
+
+/*
  * Fused rotary position embedding + K/V append. Replaces, per layer, the position
  * gather and the two apply_rotary_emb calls of _attention_forward
  * (nanoslg/models.py:96-103, apply_rotary_emb :69-83) together with the cache write

@@ -72,6 +72,10 @@ SIGNATURES = {
                                        c_int64, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     "nslg_forward_plan": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                     c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "nslg_forward_plan_csr": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+                                        c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p]),
     "nslg_rope_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                    c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64,
                                    c_int32, c_int32, c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),

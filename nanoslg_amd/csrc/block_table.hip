@@ -14,50 +14,12 @@
 // table, kv_cache.py:583-584, 606-607); the uploaded entries are also written
 // into the row for later forwards. Reads and writes stay inside the arena, the
 // upload and the CSR (every index is checked against the sizes passed in).
-#include "nslg_common.h"
+#include "block_table.h"
 
 namespace nslg {
 namespace {
 
-struct TableCsrArgs {
-  int32_t* tables;            // arena
-  int64_t table_capacity;     // entries of the arena
-  const int32_t* row_offset;  // [B] first arena entry of sequence b's row
-  const int32_t* pages_have;  // [B] valid entries of the row
-  const int32_t* synced;      // [B] entries [0, synced) are current in the arena
-  const int32_t* patch_indptr;  // [B+1] uploaded entries [synced_b, pages_have_b) of row b
-  const int32_t* patch;
-  int64_t patch_total;
-  const int32_t* kv_indptr;   // [B+1] CSR pointers of the forward
-  int32_t* kv_indices;        // [kv_indptr[B]] out
-  int64_t total_pages;
-  int32_t batch;
-};
-
-__global__ void __launch_bounds__(256) block_table_csr_kernel(TableCsrArgs a) {
-  const int b = blockIdx.x;
-  const int64_t row = a.row_offset[b];
-  const int have = a.pages_have[b];
-  const int syn = a.synced[b];
-  const int64_t p0 = a.patch_indptr[b];
-  const int64_t seg = a.kv_indptr[b];
-  const int npg = a.kv_indptr[b + 1] - a.kv_indptr[b];
-  for (int i = threadIdx.x; i < npg || i < have; i += blockDim.x) {
-    int pid = 0;
-    if (i < have) {
-      const int64_t at = row + i;
-      const bool in_table = row >= 0 && at < a.table_capacity;
-      if (i >= syn) {
-        const int64_t pk = p0 + (i - syn);
-        pid = pk >= 0 && pk < a.patch_total ? a.patch[pk] : 0;
-        if (in_table) a.tables[at] = pid;
-      } else if (in_table) {
-        pid = a.tables[at];
-      }
-    }
-    if (i < npg && seg + i < a.total_pages) a.kv_indices[seg + i] = pid;
-  }
-}
+__global__ void __launch_bounds__(256) block_table_csr_kernel(TableCsrArgs a) { csr_segment(a, blockIdx.x); }
 
 }  // namespace
 }  // namespace nslg

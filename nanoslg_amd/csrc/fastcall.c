@@ -172,6 +172,16 @@ static PyObject* forward_plan(PyObject* self, PyObject* const* args, Py_ssize_t 
   return PyLong_FromLong(rc);
 }
 
+static PyObject* forward_plan_csr(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("forward_plan_csr", "pqpppppqppqpppiiippppp", args, n, a)) return NULL;
+  const int rc = nslg_forward_plan_csr(a[0].p, a[1].q, a[2].p, a[3].p, a[4].p, a[5].p, a[6].p, a[7].q, a[8].p, a[9].p,
+                                       a[10].q, a[11].p, a[12].p, a[13].p, a[14].i, a[15].i, a[16].i, a[17].p,
+                                       a[18].p, a[19].p, a[20].p, a[21].p);
+  return PyLong_FromLong(rc);
+}
+
 static PyObject* paged_prefill(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   (void)self;
   arg_t a[MAX_ARGS];
@@ -229,6 +239,8 @@ static PyMethodDef methods[] = {
      "nslg_block_table_csr: the entry point's arguments in order; returns its status"},
     {"forward_plan", (PyCFunction)(void (*)(void))forward_plan, METH_FASTCALL,
      "nslg_forward_plan: the entry point's arguments in order; returns its status"},
+    {"forward_plan_csr", (PyCFunction)(void (*)(void))forward_plan_csr, METH_FASTCALL,
+     "nslg_forward_plan_csr: the entry point's arguments in order; returns its status"},
     {"paged_prefill", (PyCFunction)(void (*)(void))paged_prefill, METH_FASTCALL,
      "nslg_paged_prefill: the entry point's arguments in order; returns its status"},
     {"paged_prefill_grid", (PyCFunction)(void (*)(void))paged_prefill_grid, METH_FASTCALL,

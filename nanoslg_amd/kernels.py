@@ -578,6 +578,26 @@ def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages
     return slot, pos, rows, qo
 
 
+def _forward_plan_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr, kv_indices,
+                      total_pages, start, new_tokens, input_offsets, B, iw, page_size, T, out):
+    """_block_table_csr then _forward_plan in one launch (nslg_forward_plan_csr), the
+    cache manager's own tables; `out` as for _forward_plan (required)."""
+    sizes = [B * iw, B * iw, T, B + 1]
+    if out.numel() < sum(sizes) or out.dtype != torch.int32:
+        raise ValueError("forward_plan_csr: the output buffer is too small or not int32")
+    slot, pos, rows, qo = out[:sum(sizes)].split(sizes)
+    base = out.data_ptr()
+    o1, o2 = 4 * B * iw, 8 * B * iw
+    o3 = o2 + 4 * T
+    rc = _lib.fast().forward_plan_csr(tables.data_ptr(), tables.numel(), row_offset.data_ptr(), pages_have.data_ptr(),
+                                      synced.data_ptr(), patch_indptr.data_ptr(), patch.data_ptr(), int(patch_total),
+                                      kv_indptr.data_ptr(), kv_indices.data_ptr(), int(total_pages), start.data_ptr(),
+                                      new_tokens.data_ptr(), input_offsets.data_ptr(), B, iw, page_size, base,
+                                      base + o1, base + o2, base + o3, _stream(tables))
+    _lib.check(rc, "nslg_forward_plan_csr")
+    return slot, pos, rows, qo
+
+
 class DecodeLaunch:
     """Append + split-K decode for every layer of one decode forward.
 

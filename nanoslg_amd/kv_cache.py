@@ -1003,7 +1003,7 @@ class PagedCacheContext(CacheContext):
                 self._plan = plan
                 cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
                 return
-        if not (self._is_decode and iw == 1) and cache.NATIVE_PLAN and hasattr(cache.kernels, "_forward_plan"):
+        if not (self._is_decode and iw == 1) and cache.NATIVE_PLAN and hasattr(cache.kernels, "_forward_plan_csr"):
             T = sum(self.new_token_counts)
             if T >= self.DEVICE_PLAN_TOKENS:
                 got = cache._plan_forward_native(states, self.new_token_counts, self.input_offsets, iw, T,
@@ -1261,7 +1261,8 @@ class PagedKVCache(KVCacheManager):
         straight into the upload buffer; then the upload, nslg_block_table_csr and
         nslg_forward_plan, as in PagedCacheContext and _plan_upload. Returns (plan,
         pages to zero), or None when a page the forward writes is shared (copy-on-write
-        takes the numpy path; the call changed nothing then)."""
+        takes the numpy path; the call changed nothing then). The two device steps go
+        out as one launch (nslg_forward_plan_csr)."""
         tables, pool, kern = self._tables, self.pool, self.kernels
         for st in states:
             tables.place(st)
@@ -1295,12 +1296,11 @@ class PagedKVCache(KVCacheManager):
         sizes = [B + 1, B, 0, 0, nz, B, B, B, B, B, B, B, B + 1, max(npatch, 1), max(total_pages, 1), tail]
         (d_indptr, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch,
          d_idx, fp_out) = dev.split(sizes)
-        kern._block_table_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch, npatch, d_indptr, d_idx,
-                              total_pages, B)
+        slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch, npatch,
+                                                             d_indptr, d_idx, total_pages, d_start, d_n, d_off, B, iw,
+                                                             ps, T, fp_out)
         for st in states:
             st.synced = st.n_pages
-        slot_t, pos_t, rows_t, qo_t = kern._forward_plan(d_indptr, d_idx, d_start, d_n, d_off, d_have, B, iw, ps, T,
-                                                         out=fp_out)
         plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t, d_cs, d_cd, d_zero,
                                          total_pages, T)
         return plan, nz

@@ -262,3 +262,12 @@ def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages
         out[:flat.numel()].copy_(flat)
         flat = out[:flat.numel()]
     return tuple(flat.split([B * iw, B * iw, T, B + 1]))
+
+
+def _forward_plan_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr, kv_indices,
+                      total_pages, start, new_tokens, input_offsets, B, iw, page_size, T, out):
+    """As nanoslg_amd.kernels._forward_plan_csr: the two launches it fuses, in order."""
+    _block_table_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr, kv_indices,
+                     total_pages, B)
+    return _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages_have, B, iw, page_size, T,
+                         out=out)

@@ -151,6 +151,24 @@ def test_block_table_csr_argument_checks():
     assert "block_table_csr" in _lib.last_error()
 
 
+def test_forward_plan_csr_argument_checks():
+    """nslg_forward_plan_csr: the checks of both launches it fuses, on the host (the
+    fast binding returns the same statuses)."""
+    from nanoslg_amd import _lib
+    lib, fast = _lib.load(), _lib.fast()
+    A = 4096
+    ok = (A, 64, A, A, A, A, A, 1, A, A, 4, A, A, A, 2, 8, 16, A, A, A, A, None)
+    zero_batch = ok[:14] + (0,) + ok[15:]
+    assert lib.nslg_forward_plan_csr(*zero_batch) == fast.forward_plan_csr(*zero_batch) == 0
+    for k, bad, what in ((14, -1, "sizes"), (16, 0, "sizes"), (15, -1, "sizes"), (1, -1, "sizes"),
+                         (0, None, "null"), (6, None, "null"), (11, None, "null"), (20, None, "null")):
+        args = ok[:k] + (bad,) + ok[k + 1:]
+        assert lib.nslg_forward_plan_csr(*args) == fast.forward_plan_csr(*args) == -1, k
+        assert "forward_plan_csr" in _lib.last_error() and what in _lib.last_error(), k
+    big = ok[:14] + (1 << 16,) + (1 << 16,) + ok[16:]
+    assert lib.nslg_forward_plan_csr(*big) == -1 and "too large" in _lib.last_error()
+
+
 def test_noalloc_decode_rejects_oversize_on_host():
     """nslg_paged_decode_noalloc refuses a call whose scratch need exceeds its static
     array before any device work (no device is touched here)."""
@@ -241,6 +259,6 @@ def test_fast_binding_signatures_match_the_header():
     code = {c_void_p: "p", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
     src = (ROOT / "nanoslg_amd" / "csrc" / "fastcall.c").read_text()
     found = re.findall(r'parse\("(\w+)", "(\w+)"', src)
-    assert len(found) == 13
+    assert len(found) == 14
     for fn, sig in found:
         assert sig == "".join(code[t] for t in _lib.SIGNATURES["nslg_" + fn][1]), fn

@@ -961,6 +961,69 @@ def test_block_table_csr_bit_exact(B, ps, seed):
     assert np.array_equal(d_arena.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("B,ps,seed", [(37, 16, 11), (5, 1, 12), (300, 16, 13), (8, 16, 14)])
+def test_forward_plan_csr_matches_the_two_launches(B, ps, seed):
+    """nslg_forward_plan_csr (the CSR and the plan of a device-planned forward in one
+    launch) against nslg_block_table_csr then nslg_forward_plan on copies of the same
+    arena: the CSR, the arena rows, slots, positions, ragged rows and qo_indptr
+    bit-identical; rows partly synced, sequences needing pages past their table,
+    empty sequences, input offsets. The two launches are tied to the oracle by
+    test_block_table_csr_bit_exact and the cache tests."""
+    _log(f"forward plan csr B={B} ps={ps}")
+    from nanoslg_amd import kernels as K
+    rng = np.random.default_rng(seed)
+    have = [int(x) for x in rng.integers(0, 80, size=B)]
+    have[0] = 0
+    tables = [rng.integers(1, 1 << 20, size=h).tolist() for h in have]
+    lens, ntok = [], []
+    for b, h in enumerate(have):
+        L = (h + 2) * ps if b % 7 == 3 else (0 if h == 0 else int(rng.integers((h - 1) * ps + 1, h * ps + 1)))
+        lens.append(L)
+        ntok.append(int(rng.integers(0, min(L, 600) + 1)))
+    start = [L - n for L, n in zip(lens, ntok)]
+    offs_in = [int(rng.integers(0, 4)) for _ in range(B)]
+    iw = max(o + n for o, n in zip(offs_in, ntok))
+    T = sum(ntok)
+    synced = [int(rng.integers(0, h + 1)) if h else 0 for h in have]
+    caps = [max(16, h + int(rng.integers(0, 40))) for h in have]
+    rows = np.zeros(B, np.int64)
+    o = 0
+    for b in rng.permutation(B):
+        rows[b] = o
+        o += caps[b] + int(rng.integers(0, 9))
+    arena = rng.integers(-5, 1 << 20, size=o + 64).astype(np.int32)
+    for b in range(B):
+        arena[rows[b]:rows[b] + synced[b]] = tables[b][:synced[b]]
+    patch = [x for b in range(B) for x in tables[b][synced[b]:]] or [0]
+    pip = np.zeros(B + 1, np.int32)
+    np.cumsum([h - s for h, s in zip(have, synced)], out=pip[1:])
+    indptr = np.zeros(B + 1, np.int32)
+    np.cumsum([(L + ps - 1) // ps for L in lens], out=indptr[1:])
+    total = int(indptr[-1])
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)  # noqa: E731
+    args = [t(rows), t(have), t(synced), t(pip), t(patch)]
+    d_indptr, d_start, d_n, d_off = t(indptr), t(start), t(ntok), t(offs_in)
+    outs, idxs, arenas = [], [], []
+    for fused in (False, True):
+        d_arena = t(arena)
+        d_idx = torch.full((max(total, 1),), -7, dtype=torch.int32, device=DEV)
+        out = torch.full((2 * B * iw + T + B + 1,), -9, dtype=torch.int32, device=DEV)
+        if fused:
+            res = K._forward_plan_csr(d_arena, *args, len(patch), d_indptr, d_idx, total, d_start, d_n, d_off, B, iw,
+                                      ps, T, out)
+        else:
+            K._block_table_csr(d_arena, *args, len(patch), d_indptr, d_idx, total, B)
+            res = K._forward_plan(d_indptr, d_idx, d_start, d_n, d_off, args[1], B, iw, ps, T, out=out)
+        torch.cuda.synchronize()
+        outs.append([r.cpu() for r in res])
+        idxs.append(d_idx.cpu())
+        arenas.append(d_arena.cpu())
+    assert torch.equal(idxs[0], idxs[1]) and torch.equal(arenas[0], arenas[1])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert int(outs[1][3][-1]) == T and (outs[1][0] >= -1).all()
+
+
 @pytest.mark.parametrize("B,ps,where", [(64, 16, "device"), (37, 4, "pinned"), (5, 16, "pinned")])
 def test_decode_plan_step_device_list_bit_exact(B, ps, where):
     """nslg_decode_plan_step_device (the planner of a step replayed from a HIP graph:
