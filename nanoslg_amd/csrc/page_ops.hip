@@ -11,50 +11,22 @@
 namespace nslg {
 namespace {
 
-// Workgroup (x, y) moves rows [x * rows_wg, min(T, (x + 1) * rows_wg)) of K (y = 0)
-// or V (y = 1): the rows' vectors flattened over the workgroup's threads,
-// kAppendUnroll vectors per thread per round with all of a round's loads issued
-// before its stores (a workgroup per row, 8192 of them for 4096 rows, left the
-// launch bound by workgroup dispatch). Rows whose slot is negative or outside the
-// pool are skipped.
-constexpr int kAppendUnroll = 4;
 template <typename V>
 __global__ void __launch_bounds__(256)
 append_rows_kernel(const char* __restrict__ k_src, const char* __restrict__ v_src,
                    int64_t k_src_stride, int64_t v_src_stride,  // bytes
-                   const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t rows_wg,
+                   const int32_t* __restrict__ slot_mapping,
                    char* __restrict__ k_pool, char* __restrict__ v_pool,
                    int64_t pool_slots, int32_t row_bytes) {
-  const int t0 = blockIdx.x * rows_wg;
-  const int rows = min(rows_wg, num_tokens - t0);
+  const int t = blockIdx.x;
+  const int32_t slot = slot_mapping[t];
+  if (slot < 0 || (int64_t)slot >= pool_slots) return;
   const bool is_v = blockIdx.y != 0;
-  const char* src = is_v ? v_src : k_src;
-  const int64_t stride = is_v ? v_src_stride : k_src_stride;
-  char* pool = is_v ? v_pool : k_pool;
+  const V* src = reinterpret_cast<const V*>((is_v ? v_src : k_src) +
+                                            (int64_t)t * (is_v ? v_src_stride : k_src_stride));
+  V* dst = reinterpret_cast<V*>((is_v ? v_pool : k_pool) + (int64_t)slot * row_bytes);
   const int nvec = row_bytes / (int)sizeof(V);
-  const int total = rows * nvec;
-  for (int base = threadIdx.x; base < total; base += kAppendUnroll * blockDim.x) {
-    V val[kAppendUnroll];
-    int32_t slot[kAppendUnroll];
-    int vi[kAppendUnroll];
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      const int idx = base + u * blockDim.x;
-      slot[u] = -1;
-      vi[u] = 0;
-      if (idx < total) {
-        const int r = idx / nvec;
-        vi[u] = idx - r * nvec;
-        slot[u] = slot_mapping[t0 + r];
-        val[u] = reinterpret_cast<const V*>(src + (int64_t)(t0 + r) * stride)[vi[u]];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      if (slot[u] >= 0 && (int64_t)slot[u] < pool_slots)
-        stream_store(reinterpret_cast<V*>(pool + (int64_t)slot[u] * row_bytes) + vi[u], val[u]);
-    }
-  }
+  for (int i = threadIdx.x; i < nvec; i += blockDim.x) stream_store(dst + i, src[i]);
 }
 
 // Flat grid over (page list entry, 16-byte word of the page) for one layer
@@ -172,23 +144,18 @@ extern "C" int nslg_append_kv(const void* k_src, const void* v_src, int64_t k_sr
     return fail(NSLG_EINVAL, "append_kv: v source rows overlap (stride %lld)", (long long)v_src_stride);
   const int w = pick_vec({row_bytes, ks, vs, (int64_t)(uintptr_t)k_src, (int64_t)(uintptr_t)v_src,
                           (int64_t)(uintptr_t)k_pool, (int64_t)(uintptr_t)v_pool});
-  // about 16 KB of each of K and V per workgroup
-  int rows_wg = (int)((16 << 10) / row_bytes);
-  rows_wg = rows_wg < 1 ? 1 : (rows_wg > 64 ? 64 : rows_wg);
-  if (rows_wg > num_tokens) rows_wg = num_tokens;
-  const int threads = threads_for((int64_t)rows_wg * (row_bytes / w));
-  dim3 grid((num_tokens + rows_wg - 1) / rows_wg, 2);
+  const int threads = threads_for(row_bytes / w);
+  dim3 grid(num_tokens, 2);
   hipStream_t s = as_stream(stream);
   const char* ksrc = (const char*)k_src;
   const char* vsrc = (const char*)v_src;
   char* kp = (char*)k_pool;
   char* vp = (char*)v_pool;
-  const int rb = (int)row_bytes;
   switch (w) {
-    case 16: append_rows_kernel<u32x4><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, num_tokens, rows_wg, kp, vp, pool_slots, rb); break;
-    case 8: append_rows_kernel<u32x2><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, num_tokens, rows_wg, kp, vp, pool_slots, rb); break;
-    case 4: append_rows_kernel<uint32_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, num_tokens, rows_wg, kp, vp, pool_slots, rb); break;
-    default: append_rows_kernel<uint16_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, num_tokens, rows_wg, kp, vp, pool_slots, rb); break;
+    case 16: append_rows_kernel<u32x4><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
+    case 8: append_rows_kernel<u32x2><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
+    case 4: append_rows_kernel<uint32_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
+    default: append_rows_kernel<uint16_t><<<grid, threads, 0, s>>>(ksrc, vsrc, ks, vs, slot_mapping, kp, vp, pool_slots, (int)row_bytes); break;
   }
   return check_launch("append_kv");
 }
