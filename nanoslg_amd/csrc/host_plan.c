@@ -5,18 +5,21 @@
  * rule set it follows: write plan, tokens_used, CSR pointers, last-page lengths).
  *
  * plan_forward(states, ntoks, offsets, page_size, ref_count, tokens_used, mark,
- *              zero_pages, out)
- *   states      sequence states (objects with num_tokens, n_pages, bt, row, synced;
- *               their device rows already placed)
+ *              zero_pages, out, place)
+ *   states      sequence states (objects with num_tokens, n_pages, bt, row, synced)
  *   ntoks       new tokens per sequence (list of int)
  *   offsets     input offsets per sequence (list of int), or None for zeros
  *   ref_count   int64 [P], tokens_used int64 [P] (updated), mark uint8/bool [P]
  *               (all zero on entry and on return)
  *   zero_pages  list of page ids awaiting zero-on-allocation, or None
  *   out         int32 buffer the plan is written to
+ *   place       called with each state, in order, once the forward is known to be
+ *               planned here (it gives the state its device row: row, synced)
  * Returns None when a page the forward writes is shared (copy-on-write is then the
- * caller's; nothing was changed), -n when `out` holds fewer than n entries (nothing
- * was changed), else (total, total_pages, patch_entries, zero_entries) with out[:total]
+ * caller's; nothing was changed), -n when `out` may need n entries and holds fewer
+ * (nothing was changed), else (total, total_pages, patch_entries, zero_entries,
+ * shared_first) with shared_first true when some sequence's first page has more than
+ * one reference (a decode batch can only have prefix groups then) and out[:total]
  * holding, in order:
  *   kv_indptr [B+1], last_page_len [B], copy sources [0], copy destinations [0],
  *   pages to zero [nz], start [B], new tokens [B], input offsets [B], pages held [B],
@@ -65,8 +68,13 @@ static int get_buf(PyObject* o, Py_buffer* b, int writable, Py_ssize_t itemsize,
 }
 
 static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
-  if (nargs != 9) {
-    PyErr_SetString(PyExc_TypeError, "plan_forward takes 9 arguments");
+  if (nargs != 10) {
+    PyErr_SetString(PyExc_TypeError, "plan_forward takes 10 arguments");
+    return NULL;
+  }
+  PyObject* place = args[9];
+  if (!PyCallable_Check(place)) {
+    PyErr_SetString(PyExc_TypeError, "plan_forward: place must be callable");
     return NULL;
   }
   PyObject *states = args[0], *ntoks = args[1], *offsets = args[2], *zero = args[7];
@@ -108,14 +116,13 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
     goto done;
   }
 
-  /* pass 1: the sequences' numbers, the written pages' sharing, the output size */
-  int64_t npatch = 0, nwritten = 0;
+  /* pass 1: the sequences' numbers and the written pages' sharing */
+  int64_t npatch = 0, held = 0;
+  int shared_first = 0;
   for (Py_ssize_t b = 0; b < B; ++b) {
     PyObject* st = PyList_GET_ITEM(states, b);
     seq_t* s = &sq[b];
-    if (get_i64(st, s_num_tokens, &s->start) < 0 || get_i64(st, s_n_pages, &s->have) < 0 ||
-        get_i64(st, s_row, &s->row) < 0 || get_i64(st, s_synced, &s->syn) < 0)
-      goto done;
+    if (get_i64(st, s_num_tokens, &s->start) < 0 || get_i64(st, s_n_pages, &s->have) < 0) goto done;
     long long n = PyLong_AsLongLong(PyList_GET_ITEM(ntoks, b));
     if (n == -1 && PyErr_Occurred()) goto done;
     s->n_raw = n;
@@ -136,9 +143,7 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
       PyErr_SetString(PyExc_ValueError, "plan_forward: a sequence holds more pages than its table");
       goto done;
     }
-    if (s->syn > s->have) s->syn = s->have;
-    if (s->syn < 0) s->syn = 0;
-    npatch += s->have - s->syn;
+    held += s->have;
     s->p0 = floordiv(s->start, ps);
     s->plast = floordiv(s->start + s->n - 1, ps);
     int64_t c = 0;
@@ -148,6 +153,7 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
     }
     s->cnt = c;
     const int32_t* t = (const int32_t*)s->bt.buf;
+    if (s->have > 0 && t[0] > 0 && t[0] < P && ref[t[0]] > 1) shared_first = 1;
     for (int64_t i = 0; i < c; ++i) {
       const int64_t pid = t[s->p0 + i];
       if (pid < 0 || pid >= P) {
@@ -160,12 +166,13 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
         goto done;
       }
     }
-    nwritten += c;
   }
+  /* the output's size with every table entry in the patch (placing a row can make
+     the whole table due): checked before anything changes */
   const Py_ssize_t nzl = zero == Py_None ? 0 : PyList_GET_SIZE(zero);
-  const int64_t total = (B + 1) + B + nzl + 4 * (int64_t)B + 3 * (int64_t)B + (B + 1) + (npatch > 0 ? npatch : 1);
-  if (ob.len / 4 < total) {
-    result = PyLong_FromLongLong(-(long long)total);
+  const int64_t bound = (B + 1) + B + nzl + 4 * (int64_t)B + 3 * (int64_t)B + (B + 1) + (held > 0 ? held : 1);
+  if (ob.len / 4 < bound) {
+    result = PyLong_FromLongLong(-(long long)bound);
     goto done;
   }
   for (Py_ssize_t j = 0; j < nzl; ++j) { /* check the ids before anything is written */
@@ -175,6 +182,26 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
       PyErr_SetString(PyExc_ValueError, "plan_forward: a page to zero lies outside the pool");
       goto done;
     }
+  }
+
+  /* the forward is planned here: the device rows, then the entries they lack */
+  for (Py_ssize_t b = 0; b < B; ++b) {
+    PyObject* st = PyList_GET_ITEM(states, b);
+    PyObject* r = PyObject_CallOneArg(place, st);
+    if (!r) goto done;
+    Py_DECREF(r);
+    seq_t* s = &sq[b];
+    int64_t have = 0;
+    if (get_i64(st, s_row, &s->row) < 0 || get_i64(st, s_synced, &s->syn) < 0 ||
+        get_i64(st, s_n_pages, &have) < 0)
+      goto done;
+    if (have != s->have) {
+      PyErr_SetString(PyExc_RuntimeError, "plan_forward: place changed a sequence's pages");
+      goto done;
+    }
+    if (s->syn > s->have) s->syn = s->have;
+    if (s->syn < 0) s->syn = 0;
+    npatch += s->have - s->syn;
   }
 
   /* pass 2: tokens_used, the pages written whole, the plan arrays */
@@ -241,8 +268,8 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
     }
   }
   const int64_t used_total = (int64_t)(w - o);
-  result = Py_BuildValue("(LLLn)", (long long)used_total, (long long)indptr[B], (long long)npatch, nz);
-  (void)nwritten;
+  result = Py_BuildValue("(LLLnO)", (long long)used_total, (long long)indptr[B], (long long)npatch, nz,
+                         shared_first ? Py_True : Py_False);
 
 done:
   if (sq) {

@@ -1003,18 +1003,34 @@ class PagedCacheContext(CacheContext):
                 self._plan = plan
                 cache._record_decode_plan(self.seq_ids, plan, self.seq_lens)
                 return
-        if not (self._is_decode and iw == 1) and cache.NATIVE_PLAN and hasattr(cache.kernels, "_forward_plan_csr"):
+        # Every forward with new tokens takes the native planner and one device launch
+        # for its CSR and per-token plan (PagedKVCache._plan_forward_native), unless it
+        # writes a shared page: copy-on-write stays with the numpy path below.
+        if cache.NATIVE_PLAN and hasattr(cache.kernels, "_forward_plan_csr"):
             T = sum(self.new_token_counts)
-            if T >= self.DEVICE_PLAN_TOKENS:
+            if T >= self.NATIVE_PLAN_TOKENS:
                 got = cache._plan_forward_native(states, self.new_token_counts, self.input_offsets, iw, T,
                                                  list(zero_pages) if zero_pages else None)
                 if got is not None:
-                    self._plan, nz = got
+                    self._plan, nz, shared_first = got
                     self.cow_pairs = []
                     self._max_q = max(self.new_token_counts)
                     self._uniform_rows = T == B * iw
+                    if self._is_decode and iw == 1 and shared_first:
+                        # the decode batch's prefix groups (only sequences whose first page
+                        # is shared can form one)
+                        npg = [(n + ps) // ps for n in self.start_positions]  # pages after the step
+                        groups = cache._prefix_groups(states, npg)
+                        if groups is not None:
+                            kern = cache.kernels
+                            (slot,) = _upload_i32([groups[2]], pool.device)
+                            self._plan.group_slot = slot
+                            self._plan.groups = kern.DecodeGroups(B, groups[0], groups[1], pool.device,
+                                                                  seq_group_slot=slot)
                     if nz:  # zero-on-alloc of the pages this forward's extensions took
                         cache.kernels.zero_pages(pool.k, pool.v, self._plan.zero_ids)
+                    if self._is_decode and iw == 1:
+                        cache._record_decode_plan(self.seq_ids, self._plan, self.seq_lens)
                     return
         # Below, the host works per sequence and per written page only. The CSR block
         # table itself (kv_cache.py:598-615) is built on the device from the cache's
@@ -1154,7 +1170,8 @@ class PagedCacheContext(CacheContext):
         if self._is_decode and iw == 1:
             cache._record_decode_plan(self.seq_ids, self._plan, self.seq_lens)
 
-    DEVICE_PLAN_TOKENS = 256  # forwards with at least this many new tokens expand their plan on the device
+    DEVICE_PLAN_TOKENS = 256  # numpy path: forwards with at least this many new tokens expand their plan on the device
+    NATIVE_PLAN_TOKENS = 1  # native path: forwards with at least this many new tokens
 
     # ---- CacheContext -----------------------------------------------------------------
     def get_position_ids(self, S: int) -> torch.Tensor:
@@ -1259,13 +1276,12 @@ class PagedKVCache(KVCacheManager):
         pages' tokens_used, the pages to zero, the CSR pointers and last-page
         lengths, and the block-table entries the sequences' device rows lack, written
         straight into the upload buffer; then the upload, nslg_block_table_csr and
-        nslg_forward_plan, as in PagedCacheContext and _plan_upload. Returns (plan,
-        pages to zero), or None when a page the forward writes is shared (copy-on-write
-        takes the numpy path; the call changed nothing then). The two device steps go
+        nslg_forward_plan, as in PagedCacheContext and _plan_upload (the planner places
+        the sequences' device rows itself, once it knows it plans the forward). Returns
+        (plan, pages to zero), or None when a page the forward writes is shared
+        (copy-on-write takes the numpy path; the call changed nothing then). The two device steps go
         out as one launch (nslg_forward_plan_csr)."""
         tables, pool, kern = self._tables, self.pool, self.kernels
-        for st in states:
-            tables.place(st)
         B, ps = len(states), self.cfg.page_size
         tail = 2 * B * iw + T + B + 1  # forward_plan's outputs: slots, positions, rows, qo_indptr
         plan_forward = _host_planner()
@@ -1277,16 +1293,16 @@ class PagedKVCache(KVCacheManager):
             k, host = stg.take()
         else:
             k, host = -1, self._host_plan_buf
-        res = plan_forward(*args, host)
+        res = plan_forward(*args, host, tables.place)
         if isinstance(res, int):  # the buffer is too small: nothing was written
             if cuda:
                 host = stg.grow(k, -res)
             else:
                 host = self._host_plan_buf = np.zeros(2 * -res, np.int32)
-            res = plan_forward(*args, host)
+            res = plan_forward(*args, host, tables.place)
         if res is None:
             return None
-        total, total_pages, npatch, nz = res
+        total, total_pages, npatch, nz, shared_first = res
         extra = max(total_pages, 1) + tail
         if cuda:
             dev = stg.send(k, total, extra)
@@ -1303,7 +1319,7 @@ class PagedKVCache(KVCacheManager):
             st.synced = st.n_pages
         plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t, d_cs, d_cd, d_zero,
                                          total_pages, T)
-        return plan, nz
+        return plan, nz, shared_first
 
     def _plan_upload(self, states, indptr, parts, tail=0):
         """One upload of a forward's host-built plan arrays (`parts`, after the CSR

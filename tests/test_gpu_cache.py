@@ -285,8 +285,9 @@ def test_factory_on_gpu():
 
 def test_forward_plan_on_device_equals_host_plan(monkeypatch):
     """Multi-token forwards (ragged, with input offsets, over shared prefixes) planned
-    with the per-token arrays expanded on the device equal, entry for entry, the host
-    plan of the same forward; tokens_used, pool bytes and outputs are identical."""
+    with the per-token arrays expanded on the device (the native host planner and
+    nslg_forward_plan_csr) equal, entry for entry, the numpy path's host plan of the
+    same forward; tokens_used, pool bytes and outputs are identical."""
     _log("forward plan device vs host")
     from nanoslg_amd import kv_cache as KC
     g = torch.Generator().manual_seed(17)
@@ -311,8 +312,10 @@ def test_forward_plan_on_device_equals_host_plan(monkeypatch):
                 for i, s in enumerate(ids):
                     m.allocate_sequence(s, token_ids=prompt[:200] + [900 + i] * (5 + i))
         outs, plans = [], []
-        for m, thr in ((host, 10 ** 9), (dev, 1)):
+        # host: the numpy path's host plan; dev: the native planner and the device launch
+        for m, thr, native in ((host, 10 ** 9, False), (dev, 1, True)):
             monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", thr)
+            m.NATIVE_PLAN = native
             c = m.begin_forward(sids, ntok, offs)
             outs.append([c.attend(layer, q, k, v, HQ, HKV) for layer in range(L)])
             plans.append(c.plan)

@@ -616,9 +616,10 @@ def test_decode_batch_with_shared_prefix_forms_groups():
                                       "csr", "attend_rope"])
 def test_forward_plan_expanded_on_the_device_matches(scenario, monkeypatch):
     """The same scenarios with every multi-token forward's per-token plan expanded by
-    the device planner (here its CPU stand-in) instead of the host: the oracle
-    comparisons of each scenario still hold."""
+    the device planner (here its CPU stand-in) from the numpy path's host part (the
+    native planner off): the oracle comparisons of each scenario still hold."""
     monkeypatch.setattr(KC.PagedCacheContext, "DEVICE_PLAN_TOKENS", 2)
+    monkeypatch.setattr(KC.PagedKVCache, "NATIVE_PLAN", False)  # the numpy path's device plan
     FK.CALLS.clear()
     {"prefill_then_decode": test_prefill_then_decode_matches_oracle,
      "cow_order": test_copy_on_write_order_rule,

@@ -160,6 +160,15 @@ def test_random_serving_traffic_with_a_small_block_table_arena(seed, ps, pages):
     run_traffic(seed, ps, pages, dict(CPU, arena=16))
 
 
+@pytest.mark.parametrize("seed,ps,pages", [(1, 4, 48), (5, 1, 60), (8, 8, 40), (10, 16, 12)])
+def test_random_serving_traffic_numpy_planner(monkeypatch, seed, ps, pages):
+    """The same traffic with the native planner off: every forward planned by the numpy
+    path (host plans below 256 new tokens, device plans above), which otherwise only
+    takes the forwards that copy a shared page."""
+    monkeypatch.setattr(KC.PagedKVCache, "NATIVE_PLAN", False)
+    run_traffic(seed, ps, pages, CPU)
+
+
 @pytest.mark.parametrize("native", [True, False])
 @pytest.mark.parametrize("seed,ps,pages", [(21, 4, 48), (22, 1, 60), (23, 16, 12), (25, 3, 40)])
 def test_random_serving_traffic_device_planned(monkeypatch, seed, ps, pages, native):
