@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import itertools
 import math
-from typing import Optional, Tuple
+from typing import Dict, Optional, Tuple
 
 import torch
 
@@ -119,8 +119,12 @@ def _append_kv_layer(k_new: torch.Tensor, v_new: torch.Tensor, slot_mapping: tor
             or k_new.dim() < 2 or v_new.dim() < 2 or k_new.shape[-1] != D or v_new.shape[-1] != D
             or k_new.shape[-2] != Hkv or v_new.shape[-2] != Hkv):
         return append_kv(k_new, v_new, slot_mapping, k_layer, v_layer)
-    nk, ks, _ = _rows(k_new, "k_new")
-    nv, vs, _ = _rows(v_new, "v_new")
+    row = Hkv * D
+    if k_new.is_contiguous() and v_new.is_contiguous():  # the model's own [B, S, Hkv, D] rows
+        nk, ks, nv, vs = k_new.numel() // row, row, v_new.numel() // row, row
+    else:
+        nk, ks, _ = _rows(k_new, "k_new")
+        nv, vs, _ = _rows(v_new, "v_new")
     T = slot_mapping.numel()
     if nk != T or nv != T:
         raise ValueError(f"append_kv: {T} slots for {nk} k rows / {nv} v rows")
@@ -787,6 +791,9 @@ class DecodeLaunch:
         return out
 
 
+_PREFILL_WS: Dict[Tuple[int, int, int, int, int], int] = {}  # nslg_paged_prefill_workspace_size by call shape
+
+
 def _paged_prefill_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
                          k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
                          kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor, workspace: Workspace,
@@ -805,8 +812,14 @@ def _paged_prefill_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int,
                              kv_last_page_len, workspace=workspace, q_rows=q_rows, grid_width=grid_width)
     T, Hq = q.shape[0], q.shape[1]
     out = torch.empty((T, Hq, D), dtype=dt, device=q.device)
-    lib, fast = _lib.load(), _lib.fast()
-    ws = workspace.get(int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q))))
+    fast = _lib.fast()
+    key = (B, Hq, D, int(total_q), int(max_q))
+    need = _PREFILL_WS.get(key)
+    if need is None:  # a pure function of the call shape: asked once per shape
+        need = _PREFILL_WS[key] = int(_lib.load().nslg_paged_prefill_workspace_size(*key))
+        if len(_PREFILL_WS) > 4096:
+            _PREFILL_WS.clear()
+    ws = workspace.get(need)
     stream = _stream(k_layer)
     scale = 1.0 / math.sqrt(D)
     if q_rows is not None:

@@ -332,3 +332,35 @@ def test_forward_plan_on_device_equals_host_plan(monkeypatch):
             assert torch.equal(oa, ob)
         assert np.array_equal(host.pool.tokens_used, dev.pool.tokens_used)
     assert torch.equal(host.pool.k, dev.pool.k) and torch.equal(host.pool.v, dev.pool.v)
+
+
+def test_native_plan_grows_the_upload_buffer():
+    """A forward whose sequences' tables exceed the pinned upload buffer (two sequences
+    of 40,000 pages, each table uploaded whole on its first forward): the native
+    planner asks for a larger buffer, the staging ring grows it, and the CSR, the last
+    page lengths and the decode step's slots and positions equal the block tables'
+    closed form (kv_cache.py:598-615, 575-594)."""
+    _log("native plan: upload buffer growth")
+    from nanoslg_amd import kv_cache as KC
+    ps, pages = 16, 80_100
+    cfg = KC.KVCacheConfig(num_layers=1, num_kv_heads=1, num_qo_heads=1, head_dim=64, page_size=ps,
+                           max_pages=pages, dtype=torch.float16, device=DEV, enable_prefix_caching=False,
+                           backend="paged")
+    mgr = KC.PagedKVCache(cfg)
+    lens = [40_000 * ps - 5, 39_990 * ps]
+    assert sum(-(-n // ps) for n in lens) > mgr.STAGING_INTS
+    for i, n in enumerate(lens):
+        mgr.allocate_sequence(f"s{i}", num_tokens=n)
+        mgr.seqs[f"s{i}"].num_tokens = n
+    ctx = mgr.begin_forward(["s0", "s1"], [1, 1])
+    torch.cuda.synchronize()
+    plan = ctx.plan
+    tabs = [mgr.seqs[f"s{i}"].bt[:mgr.seqs[f"s{i}"].n_pages].astype(np.int64) for i in range(2)]
+    new = [n + 1 for n in lens]
+    npg = [-(-n // ps) for n in new]
+    assert plan.indptr.cpu().tolist() == [0, npg[0], npg[0] + npg[1]]
+    assert np.array_equal(plan.indices[:sum(npg)].cpu().numpy(), np.concatenate([t[:k] for t, k in zip(tabs, npg)]))
+    assert plan.lpl.cpu().tolist() == [n - (k - 1) * ps for n, k in zip(new, npg)]
+    assert plan.slot.cpu().tolist() == [int(t[n // ps]) * ps + n % ps for t, n in zip(tabs, lens)]
+    assert plan.pos_i32.cpu().tolist() == lens
+    mgr.end_forward(ctx)
