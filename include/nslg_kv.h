@@ -287,6 +287,51 @@ int nslg_paged_decode_grouped_append(const void* q, int64_t q_stride,
                                      int64_t layout, nslg_stream_t stream);
 
 /*
+ * nslg_paged_decode_append with the rotary position embedding of the step folded in:
+ * a model's decode layer (the position gather and the two apply_rotary_emb calls of
+ * _attention_forward, nanoslg/models.py:96-103 and :69-83, then attend's write and
+ * decode run, kv_cache.py:661-674 + 650) in one decode launch and its merge. Each
+ * wave rotates its query heads' q at their sequence's position as it loads them, and
+ * the chunk that writes sequence b's new row writes k_new rotated; v_new is written
+ * as given. The rotation is nslg_rope_append's, element for element:
+ *   positions       int32[batch] (device): sequence b's new token's position,
+ *                   clamped into the tables
+ *   cos_table, sin_table   fp32 [table_rows] rows of >= head_dim floats at
+ *                   table_stride, rows 16-byte aligned (the model's tables)
+ * The other arguments are nslg_paged_decode_append's. Outputs and pool bytes are
+ * bit-identical with nslg_rope_append (q rotated into a buffer, the rotated K and V
+ * rows written) followed by nslg_paged_decode on the rotated q. f16/bf16 pools
+ * (f32: NSLG_EUNSUPPORTED; use nslg_rope_append, then nslg_paged_decode).
+ */
+int nslg_paged_decode_rope_append(const void* q, int64_t q_stride, const void* k_new,
+                                  int64_t k_new_stride, const void* v_new, int64_t v_new_stride,
+                                  const int32_t* positions, const float* cos_table,
+                                  const float* sin_table, int64_t table_stride, int64_t table_rows,
+                                  void* k_pool, void* v_pool, int64_t num_pages, int32_t page_size,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices,
+                                  const int32_t* kv_last_page_len, int64_t total_pages,
+                                  int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                  int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                  int64_t layout, nslg_stream_t stream);
+
+/*
+ * The same for a batch with radix-shared prefixes (nslg_paged_decode_grouped_append
+ * with the rotation folded in): each member's query heads are rotated at that
+ * member's position.
+ */
+int nslg_paged_decode_grouped_rope_append(
+    const void* q, int64_t q_stride, const void* k_new, int64_t k_new_stride, const void* v_new,
+    int64_t v_new_stride, const int32_t* positions, const float* cos_table, const float* sin_table,
+    int64_t table_stride, int64_t table_rows, void* k_pool, void* v_pool, int64_t num_pages,
+    int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
+    const int32_t* kv_last_page_len, int64_t total_pages, int32_t batch, int32_t num_qo_heads,
+    int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
+    const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
+    const int32_t* group_members, void* out, int64_t out_stride, void* workspace,
+    size_t workspace_bytes, int64_t layout, nslg_stream_t stream);
+
+/*
  * Paged causal prefill attention over a ragged batch of new tokens whose K/V
  * are already appended to the pool (chunked prefill).
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with

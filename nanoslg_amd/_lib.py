@@ -61,6 +61,17 @@ SIGNATURES = {
                                             c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32, c_int32,
                                             c_int32, c_float, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
                                             c_void_p, c_int64, c_void_p, c_size_t, c_int64, c_void_p]),
+    "nslg_paged_decode_rope_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                                c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                                c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int32,
+                                                c_int32, c_int32, c_float, c_int32, c_void_p, c_int64, c_void_p,
+                                                c_size_t, c_int64, c_void_p]),
+    "nslg_paged_decode_grouped_rope_append": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                                        c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+                                                        c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p,
+                                                        c_int64, c_int32, c_int32, c_int32, c_int32, c_float,
+                                                        c_int32, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                                        c_int64, c_void_p, c_size_t, c_int64, c_void_p]),
     "nslg_decode_plan_step": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p]),

@@ -26,7 +26,7 @@ typedef union {
   float f;
 } arg_t;
 
-#define MAX_ARGS 32
+#define MAX_ARGS 40
 
 /* Convert args[0..n) by the codes of sig into out; 0, or -1 with a Python error. */
 static int parse(const char* name, const char* sig, PyObject* const* args, Py_ssize_t n, arg_t* out) {
@@ -172,6 +172,28 @@ static PyObject* forward_plan(PyObject* self, PyObject* const* args, Py_ssize_t 
   return PyLong_FromLong(rc);
 }
 
+static PyObject* paged_decode_rope_append(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("paged_decode_rope_append", "pqpqpqpppqqppqipppqiiiifipqpzqp", args, n, a)) return NULL;
+  const int rc = nslg_paged_decode_rope_append(
+      a[0].p, a[1].q, a[2].p, a[3].q, a[4].p, a[5].q, a[6].p, a[7].p, a[8].p, a[9].q, a[10].q, a[11].p, a[12].p,
+      a[13].q, a[14].i, a[15].p, a[16].p, a[17].p, a[18].q, a[19].i, a[20].i, a[21].i, a[22].i, a[23].f, a[24].i,
+      a[25].p, a[26].q, a[27].p, a[28].z, a[29].q, a[30].p);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* paged_decode_grouped_rope_append(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("paged_decode_grouped_rope_append", "pqpqpqpppqqppqipppqiiiifipipppqpzqp", args, n, a)) return NULL;
+  const int rc = nslg_paged_decode_grouped_rope_append(
+      a[0].p, a[1].q, a[2].p, a[3].q, a[4].p, a[5].q, a[6].p, a[7].p, a[8].p, a[9].q, a[10].q, a[11].p, a[12].p,
+      a[13].q, a[14].i, a[15].p, a[16].p, a[17].p, a[18].q, a[19].i, a[20].i, a[21].i, a[22].i, a[23].f, a[24].i,
+      a[25].p, a[26].i, a[27].p, a[28].p, a[29].p, a[30].q, a[31].p, a[32].z, a[33].q, a[34].p);
+  return PyLong_FromLong(rc);
+}
+
 static PyObject* forward_plan_csr(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   (void)self;
   arg_t a[MAX_ARGS];
@@ -239,6 +261,10 @@ static PyMethodDef methods[] = {
      "nslg_block_table_csr: the entry point's arguments in order; returns its status"},
     {"forward_plan", (PyCFunction)(void (*)(void))forward_plan, METH_FASTCALL,
      "nslg_forward_plan: the entry point's arguments in order; returns its status"},
+    {"paged_decode_rope_append", (PyCFunction)(void (*)(void))paged_decode_rope_append, METH_FASTCALL,
+     "nslg_paged_decode_rope_append: the entry point's arguments in order; returns its status"},
+    {"paged_decode_grouped_rope_append", (PyCFunction)(void (*)(void))paged_decode_grouped_rope_append, METH_FASTCALL,
+     "nslg_paged_decode_grouped_rope_append: the entry point's arguments in order; returns its status"},
     {"forward_plan_csr", (PyCFunction)(void (*)(void))forward_plan_csr, METH_FASTCALL,
      "nslg_forward_plan_csr: the entry point's arguments in order; returns its status"},
     {"paged_prefill", (PyCFunction)(void (*)(void))paged_prefill, METH_FASTCALL,

@@ -106,6 +106,52 @@ __device__ inline float rows_sum(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- rotary embedding, the eager expression's arithmetic -------------------------
+// out[d] = rnd(rnd(x[d] * c) + rnd(rot[d] * s)) in the storage type T, with c and s
+// the table values rounded to T and rot = cat(-x[D/2:], x[:D/2]). A 16-bit times
+// 16-bit product is exact in fp32 and the sum is done in fp32, as the eager ops do,
+// so results match them bit for bit.
+template <typename T>
+__device__ inline unsigned short rope_elem(float x, float c, float r, float s) {
+  float a = T::to_f32(T::from_f32(x * c));
+  float b = T::to_f32(T::from_f32(r * s));
+  // Both products stay rounded on their own: without this the compiler narrows the
+  // ops to 16 bits and fuses one product into the add (v_fma_f16 / v_fma_mix),
+  // which rounds once where the eager ops round twice.
+  asm volatile("" : "+v"(a), "+v"(b));
+  return T::from_f32(a + b);
+}
+
+__device__ inline void load8f(const float* p, float (&f)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+}
+
+// Rotates the 8 elements at d0 .. d0 + 7 of one head (lo: d0 < D/2, whose partners
+// are at d0 + D/2; else partners at d0 - D/2) at table rows crow / srow: x holds the
+// elements, y their partners.
+template <typename T, typename V8>
+__device__ inline V8 rope8(V8 x, V8 y, const float* crow, const float* srow, int d0, bool lo) {
+  float c[8], sn[8];
+  load8f(crow + d0, c);
+  load8f(srow + d0, sn);
+  V8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xe = T::to_f32(x[e]);
+    const float ye = T::to_f32(y[e]);
+    const float ce = T::to_f32(T::from_f32(c[e]));
+    const float se = T::to_f32(T::from_f32(sn[e]));
+    o[e] = lo ? rope_elem<T>(xe, ce, -ye, se) : rope_elem<T>(xe, ce, ye, se);
+  }
+  return o;
+}
+
 // ---- streaming (non-temporal) vector accesses -----------------------------------
 // Pool pages written by the append / zero / copy kernels are not read again by the
 // writing kernel: stored with the non-temporal hint they go out to HBM instead of

@@ -83,7 +83,23 @@ struct DecodeParams {
   const uint16_t* v_new;
   int64_t k_new_stride;  // elements between batch rows
   int64_t v_new_stride;
+  // Rotary embedding (rope_cos null: none): q and the new K rows are rotated at
+  // sequence b's position rope_pos[b] (clamped into the tables) before use, with the
+  // arithmetic of nslg_rope_append; tables fp32 [rope_rows] rows at rope_stride.
+  const int32_t* rope_pos;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_stride;
+  int64_t rope_rows;
 };
+
+// Table rows of sequence b's position (rope_pos[b], clamped into the tables).
+__device__ inline void rope_rows_of(const DecodeParams& p, int b, const float*& crow, const float*& srow) {
+  int64_t pos = p.rope_pos[b];
+  pos = pos < 0 ? 0 : (pos >= p.rope_rows ? p.rope_rows - 1 : pos);
+  crow = p.rope_cos + pos * p.rope_stride;
+  srow = p.rope_sin + pos * p.rope_stride;
+}
 
 // Prefix groups of a grouped decode call: sequences whose first pages are the same
 // pages (a shared radix prefix). The prefix of a group is one more work unit whose
@@ -487,7 +503,15 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
         const uint16_t* src = (is_v ? p.v_new + (int64_t)b * p.v_new_stride : p.k_new + (int64_t)b * p.k_new_stride) +
                               (int64_t)h * D + e;
         uint16_t* dst = const_cast<uint16_t*>(is_v ? p.v_pool : p.k_pool) + row + e;
-        *reinterpret_cast<u16x8*>(dst) = *reinterpret_cast<const u16x8*>(src);
+        u16x8 val = *reinterpret_cast<const u16x8*>(src);
+        if (!is_v && p.rope_cos != nullptr) {  // the K row rotated at the token's position
+          const bool lo = e < D / 2;
+          const u16x8 partner = *reinterpret_cast<const u16x8*>(src + (lo ? D / 2 : -D / 2));
+          const float *crow, *srow;
+          rope_rows_of(p, b, crow, srow);
+          val = rope8<T>(val, partner, crow, srow, e, lo);
+        }
+        *reinterpret_cast<u16x8*>(dst) = val;
       }
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the compiler from moving loads above the store
@@ -516,6 +540,18 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
     const uint16_t* qrow = p.q + (int64_t)col_seq * p.q_stride + (int64_t)hq * D;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) qb[s] = *reinterpret_cast<const u16x8*>(qrow + 32 * s + 8 * gq);
+    if (p.rope_cos != nullptr) {
+      // rotated at the column's sequence's position: element d = 32s + 8gq + e of
+      // qb[s] (s < kSteps / 2) pairs with d + D/2 in qb[s + kSteps / 2], the same lane
+      const float *crow, *srow;
+      rope_rows_of(p, col_seq, crow, srow);
+#pragma unroll
+      for (int s = 0; s < kSteps / 2; ++s) {
+        const u16x8 lo = qb[s], hi = qb[s + kSteps / 2];
+        qb[s] = rope8<T>(lo, hi, crow, srow, 32 * s + 8 * gq, true);
+        qb[s + kSteps / 2] = rope8<T>(hi, lo, crow, srow, 32 * s + 8 * gq + D / 2, false);
+      }
+    }
   } else {
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) qb[s] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -1051,6 +1087,12 @@ struct NewRows {
   const void* v = nullptr;
   int64_t k_stride = 0;  // elements between batch rows
   int64_t v_stride = 0;
+  // rotary embedding of q and the new K rows (cos null: none)
+  const int32_t* pos = nullptr;
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  int64_t table_stride = 0;  // floats between table rows
+  int64_t table_rows = 0;
 };
 
 template <bool kGrouped>
@@ -1080,6 +1122,16 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
     if ((int64_t)((uintptr_t)nr.k % align) || (int64_t)((uintptr_t)nr.v % align) || (nr.k_stride * eb) % align ||
         (nr.v_stride * eb) % align)
       return fail(NSLG_EINVAL, "paged_decode_append: new rows must be %lld-byte aligned", (long long)align);
+  }
+  if (nr.cos) {
+    if (!nr.k || !nr.sin || !nr.pos) return fail(NSLG_EINVAL, "paged_decode_rope_append: null table, positions or rows");
+    if (dtype == NSLG_F32)
+      return fail(NSLG_EUNSUPPORTED, "paged_decode_rope_append: f16/bf16 pools (f32: nslg_rope_append, then decode)");
+    if (nr.table_rows <= 0 || nr.table_stride < head_dim)
+      return fail(NSLG_EINVAL, "paged_decode_rope_append: tables of %lld rows at stride %lld for head_dim %d",
+                  (long long)nr.table_rows, (long long)nr.table_stride, head_dim);
+    if (((uintptr_t)nr.cos | (uintptr_t)nr.sin) & 15 || (nr.table_stride * 4) % 16)
+      return fail(NSLG_EINVAL, "paged_decode_rope_append: table rows must be 16-byte aligned");
   }
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_decode: GQA group %d > 16", group);
@@ -1203,6 +1255,11 @@ int decode_impl(const void* q, int64_t q_stride, const void* k_pool, const void*
   p.v_new = (const uint16_t*)nr.v;
   p.k_new_stride = nr.k_stride;
   p.v_new_stride = nr.v_stride;
+  p.rope_pos = nr.pos;
+  p.rope_cos = nr.cos;
+  p.rope_sin = nr.sin;
+  p.rope_stride = nr.table_stride;
+  p.rope_rows = nr.table_rows;
   char* ws = (char*)workspace;
   p.part_o = (float*)ws;
   p.part_ml = p.part_o + mc * slot_members * num_qo_heads * head_dim;
@@ -1375,6 +1432,31 @@ extern "C" int nslg_paged_decode_append(const void* q, int64_t q_stride, const v
                             dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, nr, layout);
 }
 
+extern "C" int nslg_paged_decode_rope_append(
+    const void* q, int64_t q_stride, const void* k_new, int64_t k_new_stride, const void* v_new,
+    int64_t v_new_stride, const int32_t* positions, const float* cos_table, const float* sin_table,
+    int64_t table_stride, int64_t table_rows, void* k_pool, void* v_pool, int64_t num_pages, int32_t page_size,
+    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_last_page_len, int64_t total_pages,
+    int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
+    void* out, int64_t out_stride, void* workspace, size_t workspace_bytes, int64_t layout, nslg_stream_t stream) {
+  if (batch > 0 && (!k_new || !v_new || !cos_table))
+    return fail(NSLG_EINVAL, "paged_decode_rope_append: null k_new, v_new or tables");
+  NewRows nr;
+  nr.k = k_new;
+  nr.v = v_new;
+  nr.k_stride = k_new_stride;
+  nr.v_stride = v_new_stride;
+  nr.pos = positions;
+  nr.cos = cos_table;
+  nr.sin = sin_table;
+  nr.table_stride = table_stride;
+  nr.table_rows = table_rows;
+  GroupArgs<false> ga;
+  return decode_impl<false>(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices,
+                            kv_last_page_len, total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale,
+                            dtype, out, out_stride, ga, 0, 1, workspace, workspace_bytes, stream, nr, layout);
+}
+
 namespace {
 
 int grouped_impl(const void* q, int64_t q_stride, const void* k_pool, const void* v_pool, int64_t num_pages,
@@ -1465,6 +1547,33 @@ extern "C" int nslg_paged_decode_grouped_append(
   nr.v = v_new;
   nr.k_stride = k_new_stride;
   nr.v_stride = v_new_stride;
+  return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
+                      total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
+                      num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,
+                      stream, nr, layout);
+}
+
+extern "C" int nslg_paged_decode_grouped_rope_append(
+    const void* q, int64_t q_stride, const void* k_new, int64_t k_new_stride, const void* v_new,
+    int64_t v_new_stride, const int32_t* positions, const float* cos_table, const float* sin_table,
+    int64_t table_stride, int64_t table_rows, void* k_pool, void* v_pool, int64_t num_pages, int32_t page_size,
+    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* kv_last_page_len, int64_t total_pages,
+    int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, float sm_scale, int32_t dtype,
+    const int32_t* seq_group_slot, int32_t num_groups, const int32_t* group_prefix_pages,
+    const int32_t* group_members, void* out, int64_t out_stride, void* workspace, size_t workspace_bytes,
+    int64_t layout, nslg_stream_t stream) {
+  if (batch > 0 && (!k_new || !v_new || !cos_table))
+    return fail(NSLG_EINVAL, "paged_decode_grouped_rope_append: null k_new, v_new or tables");
+  NewRows nr;
+  nr.k = k_new;
+  nr.v = v_new;
+  nr.k_stride = k_new_stride;
+  nr.v_stride = v_new_stride;
+  nr.pos = positions;
+  nr.cos = cos_table;
+  nr.sin = sin_table;
+  nr.table_stride = table_stride;
+  nr.table_rows = table_rows;
   return grouped_impl(q, q_stride, k_pool, v_pool, num_pages, page_size, kv_indptr, kv_indices, kv_last_page_len,
                       total_pages, batch, num_qo_heads, num_kv_heads, head_dim, sm_scale, dtype, seq_group_slot,
                       num_groups, group_prefix_pages, group_members, out, out_stride, workspace, workspace_bytes,

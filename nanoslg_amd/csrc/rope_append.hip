@@ -47,27 +47,6 @@ struct RopeArgs {
   int32_t num_kv_heads;
 };
 
-template <typename T>
-__device__ inline unsigned short rope_elem(float x, float c, float r, float s) {
-  float a = T::to_f32(T::from_f32(x * c));
-  float b = T::to_f32(T::from_f32(r * s));
-  // Both products stay rounded on their own: without this the compiler narrows the
-  // ops to 16 bits and fuses one product into the add (v_fma_f16 / v_fma_mix),
-  // which rounds once where the eager ops round twice.
-  asm volatile("" : "+v"(a), "+v"(b));
-  return T::from_f32(a + b);
-}
-
-__device__ inline void load8f(const float* p, float (&f)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    f[e] = a[e];
-    f[4 + e] = b[e];
-  }
-}
-
 template <typename T, int D>
 __global__ void __launch_bounds__(256) rope_append_kernel(RopeArgs a) {
   constexpr int H = D / 2;

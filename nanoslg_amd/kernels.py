@@ -330,8 +330,30 @@ def paged_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tenso
                    sm_scale, out, workspace, groups, layout)
 
 
+def paged_decode_rope_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, positions: torch.Tensor,
+                             cos: torch.Tensor, sin: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                             kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                             total_pages: int, sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                             workspace: Optional[Workspace] = None, groups: Optional[DecodeGroups] = None,
+                             layout: int = 0) -> torch.Tensor:
+    """paged_decode_append with the rotary embedding folded in
+    (nslg_paged_decode_rope_append / _grouped_rope_append): q is rotated at each
+    sequence's `positions` entry (int32 [B]) as the decode loads it, and row b of k_new
+    is written into the pool rotated at the same position; cos/sin are the model's
+    [max_positions, >= D] tables. Same result, bit for bit, as rope_append of q, k_new
+    and v_new at those positions into the sequences' new slots followed by
+    paged_decode of the rotated q. f16/bf16 pools."""
+    _require_gpu(positions, cos, sin)
+    _i32(positions, "positions")
+    if positions.numel() != q.shape[0] or not positions.is_contiguous():
+        raise ValueError("paged_decode_rope_append: one position per sequence, contiguous")
+    cos, sin = _rope_tables(cos, sin, q.shape[-1])
+    return _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages,
+                   sm_scale, out, workspace, groups, layout, rope=(positions, cos, sin))
+
+
 def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len, total_pages, sm_scale,
-            out, workspace, groups, layout=0):
+            out, workspace, groups, layout=0, rope=None):
     _require_gpu(q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
     for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
         _i32(t, n)
@@ -362,9 +384,23 @@ def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
             if n != B or h != Hkv or t.shape[-1] != D:
                 raise ValueError(f"paged_decode_append: {name} must hold {B} rows of [{Hkv}, {D}]")
             rows += [t.data_ptr(), stride]
+    if rope is not None:
+        if rows is None:
+            raise ValueError("paged_decode_rope_append: needs the step's new rows")
+        pos, cos, sin = rope
+        rows += [pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]]
     if groups is None:
         need = int(lib.nslg_paged_decode_workspace_size(B, Hq, Hkv, D, int(total_pages), ps, dtype_code(q.dtype)))
         ws = (workspace or Workspace(q.device)).get(need)
+        if rope is not None:
+            rc = lib.nslg_paged_decode_rope_append(q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(),
+                                                   v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                                                   kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                                                   int(total_pages), B, Hq, Hkv, D, scale, dtype_code(q.dtype),
+                                                   out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), layout,
+                                                   _stream(q))
+            _lib.check(rc, "nslg_paged_decode_rope_append")
+            return out
         if rows is not None:
             rc = lib.nslg_paged_decode_append(q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(),
                                               v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
@@ -388,6 +424,15 @@ def _decode(q, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_pa
     if need == 0:
         raise ValueError("paged_decode: unsupported grouped decode shape")
     ws = (workspace or Workspace(q.device)).get(need)
+    if rope is not None:
+        rc = lib.nslg_paged_decode_grouped_rope_append(
+            q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+            kv_indices.data_ptr(), kv_last_page_len.data_ptr(), int(total_pages), B, Hq, Hkv, D, scale,
+            dtype_code(q.dtype), groups.seq_group_slot.data_ptr(), groups.num_groups,
+            groups.prefix_pages_np.ctypes.data, groups.members_np.ctypes.data, out.data_ptr(), out.stride(0),
+            ws.data_ptr(), ws.numel(), layout, _stream(q))
+        _lib.check(rc, "nslg_paged_decode_grouped_rope_append")
+        return out
     if rows is not None:
         rc = lib.nslg_paged_decode_grouped_append(
             q.data_ptr(), q.stride(0), *rows, k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
@@ -610,8 +655,10 @@ class DecodeLaunch:
     each call checks that layer's tensors and issues, on the current stream, one
     nslg_paged_decode_append (each sequence's new row written by the decode chunk
     that reads it; rows that are not 16-byte aligned, 4-byte for fp32, take
-    nslg_append_kv then the decode), or nslg_rope_append then the decode. Same
-    results as append_kv followed by paged_decode on the layer's pool slices.
+    nslg_append_kv then the decode), or with RoPE one nslg_paged_decode_rope_append
+    (q and the new K rows rotated in the decode launch; fp32 pools and unaligned
+    rows or tables: nslg_rope_append then the decode). Same results as append_kv
+    (rope_append) followed by paged_decode on the layer's pool slices.
 
     A launcher can be re-bound to the next forward's plan (rebind) when the pools,
     batch size and head count stay: the pool geometry is then not checked again.
@@ -633,6 +680,7 @@ class DecodeLaunch:
         fast = _lib.fast()
         self._f_decode_append, self._f_grouped_append = fast.paged_decode_append, fast.paged_decode_grouped_append
         self._f_decode, self._f_grouped, self._f_rope = fast.paged_decode, fast.paged_decode_grouped, fast.rope_append
+        self._f_decode_rope, self._f_grouped_rope = fast.paged_decode_rope_append, fast.paged_decode_grouped_rope_append
         self.device, self.dtype = k_pool.device, k_pool.dtype
         self.dev_index = k_pool.get_device()
         self.code = dtype_code(k_pool.dtype)
@@ -708,8 +756,9 @@ class DecodeLaunch:
         """q [B, Hq, D] (rows may be strided), k_new/v_new [B, ..., Hkv, D] rows of one
         token each; returns [B, Hq, D] for pool layer `layer` (q [B, 1, Hq, D]: returns
         [B, 1, Hq * D], the layout of a forward's attention output). With rope = (cos, sin,
-        positions int32 [B]) q and k_new are first rotated (nslg_rope_append replaces
-        nslg_append_kv)."""
+        positions int32 [B]) q and k_new are first rotated: in the decode launch itself
+        (nslg_paged_decode_rope_append; 16-bit pools, rows and table rows 16-byte
+        aligned), else by nslg_rope_append ahead of the decode."""
         if not 0 <= layer < self.L:
             raise IndexError(f"layer {layer} out of range [0, {self.L})")
         dt, di = self.dtype, self.dev_index
@@ -769,6 +818,27 @@ class DecodeLaunch:
             cos, sin = _rope_tables(cos, sin, D)
             if cos.get_device() != di:
                 raise ValueError(f"DecodeLaunch: rope tables must be on {self.device}")
+            kn, vn = k_new.data_ptr(), v_new.data_ptr()
+            cp, sp, cst = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+            if (self.code != _DTYPE_CODE[torch.float32] and not (kn | vn | (ks | vs) * self.esize) & self.row_align
+                    and not (cp | sp | cst * 4) & 15):
+                # one launch: q rotated as the decode loads it, each new K row rotated by
+                # the chunk that writes it
+                if grp is None:
+                    rc = self._f_decode_rope(q.data_ptr(), qst[0], kn, ks, vn, vs, pos.data_ptr(), cp, sp, cst,
+                                             cos.shape[0], kp, vp, self.P, self.ps, self.indptr, self.indices,
+                                             self.lpl, self.total_pages, B, Hq, self.Hkv, D, self.scale, self.code,
+                                             out.data_ptr(), Hq * D, self.ws.data_ptr(), self.ws.numel(), lay, stream)
+                    _lib.check(rc, "nslg_paged_decode_rope_append")
+                else:
+                    rc = self._f_grouped_rope(
+                        q.data_ptr(), qst[0], kn, ks, vn, vs, pos.data_ptr(), cp, sp, cst, cos.shape[0], kp, vp,
+                        self.P, self.ps, self.indptr, self.indices, self.lpl, self.total_pages, B, Hq, self.Hkv, D,
+                        self.scale, self.code, grp.seq_group_slot.data_ptr(), grp.num_groups,
+                        grp.prefix_pages_np.ctypes.data, grp.members_np.ctypes.data, out.data_ptr(), Hq * D,
+                        self.ws.data_ptr(), self.ws.numel(), lay, stream)
+                    _lib.check(rc, "nslg_paged_decode_grouped_rope_append")
+                return out
             q_rot = torch.empty((B, Hq, D), dtype=self.dtype, device=self.device)
             rc = self._f_rope(q.data_ptr(), q.stride(0), q_rot.data_ptr(), Hq * D, k_new.data_ptr(), ks,
                               v_new.data_ptr(), vs, pos.data_ptr(), self.slots, B, cos.data_ptr(), sin.data_ptr(),

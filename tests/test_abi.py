@@ -151,6 +151,47 @@ def test_block_table_csr_argument_checks():
     assert "block_table_csr" in _lib.last_error()
 
 
+def test_decode_rope_append_argument_checks():
+    """nslg_paged_decode_rope_append / _grouped_rope_append: the rotary tables and
+    positions are checked on the host (present, rows 16-byte aligned and at least
+    head_dim wide, 16-bit pools only) before any launch; ctypes and the fast binding
+    return the same statuses."""
+    from nanoslg_amd import _lib
+    lib, fast = _lib.load(), _lib.fast()
+    A = 4096
+    # q, k_new, v_new (rows aligned) | positions, cos, sin, stride, rows | pools .. sm_scale, dtype | out .. stream
+    head = (A, 4096, A, 1024, A, 1024)
+    geo = (A, A, 100, 16, A, A, A, 10, 2, 32, 8, 128, 0.1, 0)
+    tail = (A, 4096, None, 0, 0, None)
+
+    def both(rope, dtype=0):
+        args = head + rope + geo[:-1] + (dtype,) + tail
+        a, b = lib.nslg_paged_decode_rope_append(*args), fast.paged_decode_rope_append(*args)
+        assert a == b
+        return a
+
+    assert both((A, None, A, 128, 100)) == -1                  # no cos table
+    assert "tables" in _lib.last_error()
+    assert both((None, A, A, 128, 100)) == -1                  # no positions
+    assert both((A, A, A, 64, 100)) == -1                      # rows narrower than head_dim
+    assert "stride" in _lib.last_error()
+    assert both((A, A, A, 128, 0)) == -1                       # no rows
+    assert both((A, A + 4, A, 128, 100)) == -1                 # table not 16-byte aligned
+    assert "aligned" in _lib.last_error()
+    assert both((A, A, A, 130, 100)) == -1                     # row stride not 16-byte aligned
+    assert both((A, A, A, 128, 100), dtype=2) == -2            # fp32 pools: rope_append, then decode
+    assert "f16/bf16" in _lib.last_error()
+    # past the rope checks: the workspace is missing
+    assert both((A, A, A, 128, 100)) == -4
+    members = (ctypes.c_int32 * 16)(0, 1, *([-1] * 14))
+    prefix = (ctypes.c_int32 * 1)(4)
+    grp = (A, 1, ctypes.addressof(prefix), ctypes.addressof(members))
+    args = head + (A, None, A, 128, 100) + geo + grp + tail
+    assert lib.nslg_paged_decode_grouped_rope_append(*args) == fast.paged_decode_grouped_rope_append(*args) == -1
+    zero_batch = head + (A, A, A, 128, 100) + geo[:8] + (0,) + geo[9:] + tail
+    assert lib.nslg_paged_decode_rope_append(*zero_batch) == 0
+
+
 def test_forward_plan_csr_argument_checks():
     """nslg_forward_plan_csr: the checks of both launches it fuses, on the host (the
     fast binding returns the same statuses)."""
@@ -259,6 +300,6 @@ def test_fast_binding_signatures_match_the_header():
     code = {c_void_p: "p", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
     src = (ROOT / "nanoslg_amd" / "csrc" / "fastcall.c").read_text()
     found = re.findall(r'parse\("(\w+)", "(\w+)"', src)
-    assert len(found) == 14
+    assert len(found) == 16
     for fn, sig in found:
         assert sig == "".join(code[t] for t in _lib.SIGNATURES["nslg_" + fn][1]), fn

@@ -139,3 +139,61 @@ def test_attention_forward_fused_equals_model_sequence(backend):
         assert torch.equal(a.pool.k, b.pool.k) and torch.equal(a.pool.v, b.pool.v)
     else:
         assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+
+
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("Hq,Hkv,D,ps", [(32, 8, 128, 16), (8, 8, 64, 16), (16, 2, 256, 16), (16, 4, 128, 5),
+                                         (4, 1, 64, 1)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_rope_append_equals_rope_append_then_decode(dtype, Hq, Hkv, D, ps, grouped):
+    """nslg_paged_decode_rope_append (q rotated as the decode loads it, the new K rows
+    rotated by the chunks that write them) against nslg_rope_append into the new
+    slots followed by nslg_paged_decode of the rotated q, on copies of one pool:
+    outputs and pool bytes bit-identical. Positions anywhere in the tables (one past
+    the end, clamped); with `grouped`, sequences 0..3 share their first pages as a
+    prefix group (each member's q rotated at its own position)."""
+    _log(f"decode rope append dtype={dtype} Hq={Hq} Hkv={Hkv} D={D} ps={ps} grouped={grouped}")
+    from nanoslg_amd import kernels as K
+    G = Hq // Hkv
+    B, R, prefix = 6, 4096, 8
+    members = list(range(min(4, 16 // G))) if grouped else []
+    rng = np.random.default_rng(1000 * D + 10 * Hq + ps + grouped)
+    g = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
+    lens = [int(rng.integers((prefix + 2) * ps + 1, (prefix + 2) * ps + 400)) for _ in range(B)]
+    npg = [-(-n // ps) for n in lens]
+    P = sum(npg) + prefix + 8
+    ids = rng.permutation(np.arange(1, P)).astype(np.int32)
+    tables, o = [], 0
+    shared = ids[:prefix]
+    o = prefix
+    for b in range(B):
+        own = npg[b] - (prefix if b in members else 0)
+        t = np.concatenate([shared, ids[o:o + own]]) if b in members else ids[o:o + own]
+        o += own
+        tables.append(t)
+    assert o <= P - 1
+    indptr = np.zeros(B + 1, np.int32)
+    np.cumsum(npg, out=indptr[1:])
+    lpl = np.array([n - (k - 1) * ps for n, k in zip(lens, npg)], np.int32)
+    slots = np.array([int(t[(n - 1) // ps]) * ps + (n - 1) % ps for t, n in zip(tables, lens)], np.int32)
+    pos = rng.integers(0, R, size=B).astype(np.int32)
+    pos[0], pos[1] = R, 0  # one past the tables (clamped to the last row), the first row
+    cos, sin = O.rope_tables(D, R, 500000.0, LLAMA3)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)  # noqa: E731
+    d_indptr, d_idx, d_lpl, d_slots, d_pos = t(indptr), t(np.concatenate(tables)), t(lpl), t(slots), t(pos)
+    k_pool = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    v_pool = torch.randn(P, ps, Hkv, D, generator=g).to(dtype).to(DEV)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype).to(DEV)
+    kv = torch.randn(B, 2, Hkv, D, generator=g).to(dtype).to(DEV)  # k and v as strided views
+    k_new, v_new = kv[:, 0], kv[:, 1]
+    grp = K.DecodeGroups(B, [members], [prefix], DEV) if grouped else None
+    kp_a, vp_a, kp_b, vp_b = k_pool.clone(), v_pool.clone(), k_pool.clone(), v_pool.clone()
+    q_rot = K.rope_append(q, k_new, v_new, d_pos, d_slots, cos, sin, kp_a, vp_a)
+    out_a = K.paged_decode(q_rot, kp_a, vp_a, d_indptr, d_idx, d_lpl, sum(npg), groups=grp)
+    out_b = K.paged_decode_rope_append(q, k_new, v_new, d_pos, cos, sin, kp_b, vp_b, d_indptr, d_idx, d_lpl,
+                                       sum(npg), groups=grp)
+    torch.cuda.synchronize()
+    assert torch.equal(kp_a, kp_b) and torch.equal(vp_a, vp_b)
+    assert torch.equal(out_a, out_b)
+    assert not torch.equal(kp_b, k_pool)  # the rows were written
