@@ -978,6 +978,93 @@ def _eager_rope(x, cos, sin, pos_ids):
     return x * c + torch.cat((-x[..., half:], x[..., :half]), dim=-1) * s
 
 
+def _graph_kernel_us(torch, dev, fn, steps):
+    """Kernel time of fn: 10 calls captured in a HIP graph, replayed with events around
+    the replays (no host overhead in the figure)."""
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.current_stream(dev).synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(10):
+                fn()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // 10)
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    del graph
+    return round(e0.elapsed_time(e1) / (reps * 10) * 1e3, 2)
+
+
+def _rope_decode_layer(args, kernels, cos, sin, rng, g):
+    """A RoPE model's decode layer at the small-batch shape (4 sequences of 1-4k
+    tokens, fp16, pages 16): nslg_rope_append then nslg_paged_decode (the rotated q
+    through memory, two launches and the merge) against nslg_paged_decode_rope_append
+    (q and the new K rows rotated in the decode launch). Time per call from a loop of
+    `--steps` calls (host included) and graph-timed kernel time; outputs and pool
+    bytes compared."""
+    import torch
+    dev = torch.device("cuda:0")
+    B = 4
+    lens = [int(x) for x in rng.integers(1024, 4097, size=B)]
+    npg = [-(-n // PS) for n in lens]
+    P = sum(npg) + 64
+    ids = rng.permutation(np.arange(1, P)).astype(np.int32)
+    tabs, o = [], 0
+    for n in npg:
+        tabs.append(ids[o:o + n])
+        o += n
+    i32 = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(dev)  # noqa: E731
+    indptr = i32(np.concatenate([[0], np.cumsum(npg)]))
+    indices = i32(np.concatenate(tabs))
+    lpl = i32([n - (k - 1) * PS for n, k in zip(lens, npg)])
+    slots = i32([int(t[(n - 1) // PS]) * PS + (n - 1) % PS for t, n in zip(tabs, lens)])
+    pos = i32([n - 1 for n in lens])
+    k_pool = torch.randn(P, PS, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    v_pool = torch.randn(P, PS, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn(B, HQ, D, generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn(B, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn(B, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    total = sum(npg)
+    ws_a, ws_b = kernels.Workspace(dev), kernels.Workspace(dev)
+    q_rot, out_a, out_b = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+
+    def two_launch():
+        kernels.rope_append(q, k, v, pos, slots, cos, sin, k_pool, v_pool, q_out=q_rot)
+        return kernels.paged_decode(q_rot, k_pool, v_pool, indptr, indices, lpl, total, out=out_a, workspace=ws_a)
+
+    def fused():
+        return kernels.paged_decode_rope_append(q, k, v, pos, cos, sin, k_pool, v_pool, indptr, indices, lpl, total,
+                                                out=out_b, workspace=ws_b)
+
+    a = two_launch().clone()
+    pool_a = k_pool.clone()
+    b = fused()
+    torch.cuda.synchronize()
+    res = {"sequences": B, "contexts": lens, "bit_exact": bool(torch.equal(a, b) and torch.equal(pool_a, k_pool))}
+    for label, fn in (("rope_append_then_decode", two_launch), ("decode_rope_append", fused)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        res[f"{label}_us"] = round((time.perf_counter() - t0) / args.steps * 1e6, 2)
+        res[f"{label}_kernel_us"] = _graph_kernel_us(torch, dev, fn, args.steps)
+    _log(f"decode_layer_b4: {res}")
+    return res
+
+
 def run_rope(args):
     """Fused rotary embedding + K/V append (nslg_rope_append) against the model's
     sequence it replaces (gather cos/sin at the positions, eager rotation of q and
@@ -1076,6 +1163,7 @@ def run_rope(args):
         res["speedup"] = round(res["eager_us"] / res["fused_us"], 2)
         _log(f"{name}: {res}")
         out[name] = res
+    out["decode_layer_b4"] = _rope_decode_layer(args, kernels, cos, sin, rng, g)
     big = out["prefill_8x512"]
     return {
         "metric": "fused RoPE + K/V append: achieved HBM GB/s (prefill chunk) and us per layer",
