@@ -41,12 +41,12 @@ HBM_PEAK_GBS = 8000.0
 # (profiles/paged_decode_hbm_traffic_kv_pressure_b64.md). `traffic` in the JSON line is
 # this ratio times the algorithmic bytes of the run being reported.
 TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0113}
-# The same for the chunked-prefill kernel over the 8 chunks of a batch (q, out, the
-# K/V of every visible key once and the page ids): FETCH_SIZE and WRITE_SIZE of
-# `bench.py --workload prefill --steps 4 --warmup 8`, scaled as above
-# (profiles/paged_prefill_chunked_b8x4096.md). Above 1 because the row tiles of one
-# KV head re-fetch its K/V once it leaves the XCD's L2.
-PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE = 1.472
+# The same for the chunked-prefill launch over the 8 chunks of a batch (q, out, the
+# K/V of every visible key once, the chunk's K/V rows written once and the page
+# ids): FETCH_SIZE and WRITE_SIZE of `bench.py --workload prefill --steps 4
+# --warmup 8`, scaled as above (profiles/paged_prefill_chunked_b8x4096.md). Above 1
+# because the row tiles of one KV head re-fetch its K/V once it leaves the XCD's L2.
+PREFILL_TRAFFIC_PER_ALGORITHMIC_BYTE = 1.424
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
@@ -292,6 +292,9 @@ class EventTimedKernels:
 
     def _paged_prefill_layer(self, *args, **kw):  # the cache manager's prefill launch
         return self._timed(self._k._paged_prefill_layer, *args, **kw)
+
+    def _paged_prefill_append_layer(self, *args, **kw):  # the same with the chunk's K/V write inside
+        return self._timed(self._k._paged_prefill_append_layer, *args, **kw)
 
     def mean_ms(self):
         return float(np.mean([a.elapsed_time(b) for a, b in self.events]))
@@ -853,13 +856,15 @@ def prefill_flops(B, L, Hq, D, start=0, n=None):
 
 
 def prefill_bytes(B, L, CH, Hq, Hkv, D, ps):
-    """Algorithmic HBM bytes of the prefill kernel over the L // CH chunks of a batch
+    """Algorithmic HBM bytes of the prefill launch over the L // CH chunks of a batch
     (fp16): per chunk q read and out written once, the K and V of every key the chunk
-    sees (its own and the earlier chunks') read once, and their page ids."""
+    sees (its own and the earlier chunks') read once, the chunk's own K/V rows written
+    into their pages once (the write is inside the launch), and the page ids."""
     total = 0
     for c in range(L // CH):
         keys = (c + 1) * CH
-        total += 2 * B * CH * Hq * D * 2 + B * keys * Hkv * D * 2 * 2 + 4 * B * (keys // ps)
+        total += (2 * B * CH * Hq * D * 2 + B * keys * Hkv * D * 2 * 2 + B * CH * Hkv * D * 2 * 2
+                  + 4 * B * (keys // ps))
     return total
 
 
@@ -954,7 +959,7 @@ def run_prefill(args):
         "flops_per_step": flops,
         "roofline": {
             "bound": "mfma",
-            "kernel": "nslg_paged_prefill (8 chunk launches per step)",
+            "kernel": "nslg_paged_prefill_append (8 chunk launches per step, each writing its chunk's K/V)",
             "timing": f"HIP events around each of {len(timed.events)} prefill calls in a second pass",
             "achieved": round(achieved, 2),
             "peak": MFMA_F16_PEAK_TFLOPS,

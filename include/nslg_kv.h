@@ -391,6 +391,44 @@ int nslg_paged_prefill_grid(const void* q, int64_t q_stride, const int32_t* qo_i
                             nslg_stream_t stream);
 
 /*
+ * The multi-token forward of one layer (prefill chunks, ragged batches): the new
+ * tokens' K/V rows written into the pool, then causal attention of their queries,
+ * in one launch. Replaces the write of FlashInferCacheContext.attend (_write_kv,
+ * nanoslg/kv_cache.py:661-674, slots of :575-594) together with the prefill run
+ * (:657-659), which the reference issues back to back for one forward (:639-659).
+ * Same result as nslg_append_kv of the rows followed by nslg_paged_prefill (q_rows
+ * null) or nslg_paged_prefill_grid (q_rows set), bit for bit.
+ *
+ *   k_new, v_new   rows of Hkv*D elements at element strides k_new_stride,
+ *                  v_new_stride (device, the pool's dtype, 16-byte aligned rows),
+ *                  laid out as q's rows: token t of sequence b is row
+ *                  qo_indptr[b] + t (q_rows null) or q_rows[qo_indptr[b]] + t of
+ *                  the batch x grid_width grid
+ *   other arguments as nslg_paged_prefill_grid (q_rows may be null: ragged rows)
+ * Token t of sequence b is position L_b - n_b + t; its K/V rows go to that
+ * position's page slot through the block table (a position past the table: slot 0
+ * of page 0, the null page of the reference's slot mapping), so no slot mapping is
+ * passed. Keys at the new positions are read from k_new / v_new, so no workgroup
+ * waits for another's writes. Precondition, which the reference's copy-on-write
+ * rule gives: no other sequence of the call reads a row being written. A row whose
+ * page id is out of the pool is not written. f16 and bf16 pools (EUNSUPPORTED for
+ * f32: append, then nslg_paged_prefill); k_new / v_new spanning >= 4 GiB:
+ * EUNSUPPORTED.
+ */
+int nslg_paged_prefill_append(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                              const int32_t* q_rows, int32_t grid_width, int64_t total_q,
+                              int32_t max_q, const void* k_new, int64_t k_new_stride,
+                              const void* v_new, int64_t v_new_stride,
+                              void* k_pool, void* v_pool, int64_t num_pages,
+                              int32_t page_size, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                              int32_t head_dim, float sm_scale, int32_t dtype,
+                              void* out, int64_t out_stride,
+                              void* workspace, size_t workspace_bytes,
+                              nslg_stream_t stream);
+
+/*
  * Device-side plan of one decode step in which every sequence gains one token:
  * the CSR block table, slot mapping and positions of the next step from those of
  * this one. Replaces, for a steady decode batch, the per-step rebuild of the CSR

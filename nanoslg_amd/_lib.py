@@ -99,6 +99,11 @@ SIGNATURES = {
                                           c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,
                                           c_void_p, c_int32, c_int32, c_int32, c_int32, c_float, c_int32,
                                           c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+    "nslg_paged_prefill_append": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int64, c_int32,
+                                            c_void_p, c_int64, c_void_p, c_int64,
+                                            c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p,
+                                            c_void_p, c_int32, c_int32, c_int32, c_int32, c_float, c_int32,
+                                            c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
 }
 
 _lib = None

@@ -224,6 +224,17 @@ static PyObject* paged_prefill_grid(PyObject* self, PyObject* const* args, Py_ss
   return PyLong_FromLong(rc);
 }
 
+static PyObject* paged_prefill_append(PyObject* self, PyObject* const* args, Py_ssize_t n) {
+  (void)self;
+  arg_t a[MAX_ARGS];
+  if (parse("paged_prefill_append", "pqppiqipqpqppqipppiiiifipqpzp", args, n, a)) return NULL;
+  const int rc = nslg_paged_prefill_append(a[0].p, a[1].q, a[2].p, a[3].p, a[4].i, a[5].q, a[6].i, a[7].p, a[8].q,
+                                           a[9].p, a[10].q, a[11].p, a[12].p, a[13].q, a[14].i, a[15].p, a[16].p,
+                                           a[17].p, a[18].i, a[19].i, a[20].i, a[21].i, a[22].f, a[23].i, a[24].p,
+                                           a[25].q, a[26].p, a[27].z, a[28].p);
+  return PyLong_FromLong(rc);
+}
+
 static PyObject* zero_pages(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   (void)self;
   arg_t a[MAX_ARGS];
@@ -271,6 +282,8 @@ static PyMethodDef methods[] = {
      "nslg_paged_prefill: the entry point's arguments in order; returns its status"},
     {"paged_prefill_grid", (PyCFunction)(void (*)(void))paged_prefill_grid, METH_FASTCALL,
      "nslg_paged_prefill_grid: the entry point's arguments in order; returns its status"},
+    {"paged_prefill_append", (PyCFunction)(void (*)(void))paged_prefill_append, METH_FASTCALL,
+     "nslg_paged_prefill_append: the entry point's arguments in order; returns its status"},
     {"zero_pages", (PyCFunction)(void (*)(void))zero_pages, METH_FASTCALL,
      "nslg_zero_pages: the entry point's arguments in order; returns its status"},
     {"copy_pages", (PyCFunction)(void (*)(void))copy_pages, METH_FASTCALL,

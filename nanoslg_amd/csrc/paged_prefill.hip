@@ -86,7 +86,27 @@ struct PrefillParams {
   int32_t pad_work;
   int32_t by_round;   // > 0: longest-first rounds of this many tiles per sequence (see below)
   int32_t rows_wg;    // query rows per workgroup (the kernel's tile shape)
+  // The forward's new K/V rows (k_new null: already in the pool). Token t of sequence
+  // b is row r_b + t of k_new / v_new, r_b the row of its first token (q's row map);
+  // keys at positions >= start_b are read from these rows, and the workgroup holding
+  // a token's first query row writes its K/V rows of the workgroup's KV head into the
+  // token's page slot (slot 0 of page 0 past the table), as nslg_append_kv would.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t k_new_stride;  // elements between rows
+  int64_t v_new_stride;
+  uint32_t k_new_bytes;  // bytes of k_new's rows (the grid's or total_q), < 4 GiB
+  uint32_t v_new_bytes;
 };
+
+// Word 3 of a raw (untyped, unswizzled) buffer resource on CDNA: 32-bit data format,
+// no index stride; num_records (word 2) bounds the byte offset of each load.
+constexpr int kBufferWord3 = 0x00020000;
+
+template <typename V>
+__device__ inline u32x4 u32x4_of(V v) {
+  return __builtin_bit_cast(u32x4, v);
+}
 
 template <int N>
 struct Vec {
@@ -193,6 +213,7 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKeys * kPitch];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKeys * kVPitch];
   __shared__ int32_t page_lds[kPageWin];
+  __shared__ uint8_t page_st[kPageWin];  // per window entry: 0 a page of the pool, 1 past the table, 2 bad id
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -235,7 +256,29 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
   const int row_bytes = p.num_kv_heads * D * 2;
   const char* kpool = reinterpret_cast<const char*>(p.k_pool) + h * D * 2;
   const char* vpool = reinterpret_cast<const char*>(p.v_pool) + h * D * 2;
-
+  // keys from new_from on are this forward's rows of k_new / v_new (none: no fused append)
+  const int new_from = p.k_new != nullptr ? start : 0x7fffffff;
+  // row of k_new / v_new holding the sequence's first new token (its rows are
+  // contiguous; a row map outside the grid reads zeros: the loads are range-checked)
+  int new_row0 = q0;
+  if (p.k_new != nullptr && p.q_rows && n_new > 0) new_row0 = __builtin_amdgcn_readfirstlane(p.q_rows[q0]);
+  // keys of this workgroup's own tokens (those whose first query row is in its row
+  // tile: each token has one such workgroup per KV head), [own_lo, own_hi), are
+  // written into the pool as they are staged
+  int own_lo = 0x7fffffff, own_hi = 0;
+  if (p.k_new != nullptr) {
+    own_lo = start + (row0_wg + G - 1) / G;
+    own_hi = start + min((row0_wg + kRowsPerWG + G - 1) / G, n_new);
+  }
+  // k_new / v_new through buffer resources: the new-row loads take one 32-bit offset
+  // register (the pool's take a 64-bit address) and are range-checked by the hardware
+  // (based at the workgroup's head: the offsets are those of the pool's loads within a row)
+  const __amdgpu_buffer_rsrc_t knew_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.k_new) + h * D, (short)0, (int)(p.k_new_bytes - h * D * 2), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vnew_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.v_new) + h * D, (short)0, (int)(p.v_new_bytes - h * D * 2), kBufferWord3);
+  const uint32_t knew_row_bytes = (uint32_t)p.k_new_stride * 2u;
+  const uint32_t vnew_row_bytes = (uint32_t)p.v_new_stride * 2u;
   const int r = lane & 15;
   const int gq = lane >> 4;
 
@@ -302,12 +345,14 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
     // page ids for keys [first_key, first_key + kPageWin*ps), one window
     const int pg0 = first_key / ps;
     for (int i = tid; i < kPageWin; i += kThreads) {
-      int v = 0;
+      int v = 0, st = 1;
       if (pg0 + i < np_seq) {
         v = idx[pg0 + i];
-        if (v < 0 || (int64_t)v >= p.num_pages) v = 0;
+        st = 0;
+        if (v < 0 || (int64_t)v >= p.num_pages) v = 0, st = 2;
       }
       page_lds[i] = v;
+      page_st[i] = (uint8_t)st;
     }
     win_base = pg0;
   };
@@ -317,12 +362,8 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
   const bool ps_pow2 = (ps & (ps - 1)) == 0;
   const int ps_shift = __builtin_ctz((unsigned)ps);
   const uint32_t page_bytes = (uint32_t)ps * (uint32_t)row_bytes;  // < 2^32 (checked by the host)
-  auto fetch_half = [&](int kt, int half) {
-    const int key0 = kt * kKeys + half * kHalf;
-#pragma unroll
-    for (int i = 0; i < kPerThreadH; ++i) {
-      int kabs = key0 + f_key + (kThreads / kChunks) * i;
-      kabs = kabs < kv_end ? kabs : kv_end - 1;
+  // key kabs from the pool, through the page-id window
+  auto fetch_pool = [&](int i, int kabs) {
       int pg, slot;
       if (ps_pow2) {
         pg = kabs >> ps_shift;
@@ -336,6 +377,30 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
       const uint64_t off = (uint64_t)pid * page_bytes + (uint32_t)(slot * row_bytes + f_ch16);
       kreg[i] = *reinterpret_cast<const u32x4*>(kpool + off);
       vreg[i] = *reinterpret_cast<const u32x4*>(vpool + off);
+  };
+  auto fetch_half = [&](int kt, int half) {
+    const int key0 = kt * kKeys + half * kHalf;
+    if (key0 + kHalf <= new_from) {  // uniform: every key of this half is in the pool
+#pragma unroll
+      for (int i = 0; i < kPerThreadH; ++i) {
+        const int kabs = key0 + f_key + (kThreads / kChunks) * i;
+        fetch_pool(i, kabs < kv_end ? kabs : kv_end - 1);
+      }
+      return;
+    }
+    // a half with keys of this forward: those from k_new / v_new (32-bit offsets from
+    // uniform bases: the rows span < 4 GiB, checked by the host), the rest from the pool
+#pragma unroll
+    for (int i = 0; i < kPerThreadH; ++i) {
+      int kabs = key0 + f_key + (kThreads / kChunks) * i;
+      kabs = kabs < kv_end ? kabs : kv_end - 1;
+      if (kabs >= new_from) {
+        const uint32_t nr = (uint32_t)(new_row0 + (kabs - start));
+        kreg[i] = u32x4_of(__builtin_amdgcn_raw_buffer_load_b128(knew_rsrc, (int)(nr * knew_row_bytes + f_ch16), 0, 0));
+        vreg[i] = u32x4_of(__builtin_amdgcn_raw_buffer_load_b128(vnew_rsrc, (int)(nr * vnew_row_bytes + f_ch16), 0, 0));
+      } else {
+        fetch_pool(i, kabs);
+      }
     }
   };
   auto stash_half = [&](int stage, int half) {
@@ -344,6 +409,33 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
       const int key = half * kHalf + f_key + (kThreads / kChunks) * i;
       *reinterpret_cast<u32x4*>(&k_lds[stage][key * kPitch + f_ch16 / 2]) = kreg[i];
       *reinterpret_cast<u32x4*>(&v_lds[stage][key * kVPitch + f_ch16 / 2]) = vreg[i];
+    }
+  };
+  // The keys of this workgroup's own tokens in tile kt (staged in LDS stage `stage`,
+  // the page-id window covering the tile) into their page slots: slot 0 of page 0 past
+  // the table, not at all for an id outside the pool. Taken from LDS at the end of the
+  // tile's iteration, where the block pipeline holds no registers, so the forward's
+  // K/V rows are written with no load of their own.
+  auto write_own = [&](int stage, int kt) {
+    // the thread's key and chunk through an empty asm: the compiler cannot hoist the
+    // addresses below out of the tile loop (registers held across the loop spill)
+    int fk = f_key, fc = f_ch16;
+    asm volatile("" : "+v"(fk), "+v"(fc));
+#pragma unroll
+    for (int i = 0; i < 2 * kPerThreadH; ++i) {
+      const int key = fk + (kThreads / kChunks) * i;
+      const int kabs = kt * kKeys + key;
+      if (kabs < own_lo || kabs >= own_hi) continue;
+      const int pg = kabs / ps;
+      const int st = page_st[pg - win_base];
+      if (st == 2) continue;
+      const uint64_t off = st == 0 ? (uint64_t)(uint32_t)page_lds[pg - win_base] * page_bytes +
+                                         (uint32_t)((kabs - pg * ps) * row_bytes + fc)
+                                   : (uint64_t)fc;
+      stream_store(reinterpret_cast<u32x4*>(const_cast<char*>(kpool) + off),
+                   *reinterpret_cast<const u32x4*>(&k_lds[stage][key * kPitch + fc / 2]));
+      stream_store(reinterpret_cast<u32x4*>(const_cast<char*>(vpool) + off),
+                   *reinterpret_cast<const u32x4*>(&v_lds[stage][key * kVPitch + fc / 2]));
     }
   };
   // first key of the window holding tile kt must cover the whole tile
@@ -569,13 +661,18 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
         }
       }
     }
+    // this tile's own keys go out after the next tile's loads have been waited for (the
+    // wait counter covers stores too), under the page-id window of this tile
+    const bool own_tile = kt * kKeys + kKeys > own_lo && kt * kKeys < own_hi;  // uniform
     if (staged) {
       if (!half1_done) {
         stash_half(stage ^ 1, 0);
         fetch_half(kt + 1, 1);
       }
       stash_half(stage ^ 1, 1);
+      if (own_tile) write_own(stage, kt);
     } else if (more) {
+      if (own_tile) write_own(stage, kt);
       // the next tile crosses the page-id window: reload it (every thread is done
       // reading page ids of the current window once all reach the barrier)
       __syncthreads();
@@ -585,6 +682,8 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
       stash_half(stage ^ 1, 0);
       fetch_half(kt + 1, 1);
       stash_half(stage ^ 1, 1);
+    } else if (own_tile) {
+      write_own(stage, kt);  // the last tile
     }
     __syncthreads();
   }
@@ -648,7 +747,8 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
                  int64_t num_pages, int32_t page_size, const int32_t* kv_indptr, const int32_t* kv_indices,
                  const int32_t* kv_last_page_len, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                  int32_t head_dim, float sm_scale, int32_t dtype, void* out, int64_t out_stride,
-                 nslg_stream_t stream) {
+                 nslg_stream_t stream, const void* k_new = nullptr, int64_t k_new_stride = 0,
+                 const void* v_new = nullptr, int64_t v_new_stride = 0) {
   if (batch < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
       num_pages <= 0 || total_q < 0)
     return fail(NSLG_EINVAL, "paged_prefill: bad sizes");
@@ -665,6 +765,8 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
     return fail(NSLG_EINVAL, "paged_prefill: Hq=%d not a multiple of Hkv=%d", num_qo_heads, num_kv_heads);
   const int group = num_qo_heads / num_kv_heads;
   if (group > 16) return fail(NSLG_EUNSUPPORTED, "paged_prefill: GQA group %d > 16", group);
+  if (k_new && dtype != NSLG_F16 && dtype != NSLG_BF16)
+    return fail(NSLG_EUNSUPPORTED, "paged_prefill_append: dtype %d (f16 or bf16 pools)", dtype);
   if (dtype == NSLG_F32) {
     // fp32 pools: the VALU attention kernel, ragged rows, bottom-right causal
     if (q_stride < (int64_t)num_qo_heads * head_dim || out_stride < (int64_t)num_qo_heads * head_dim)
@@ -706,6 +808,17 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) & 15 ||
       (q_stride * 2) % 16 || (out_stride * 2) % 16)
     return fail(NSLG_EINVAL, "paged_prefill: q/pool/out must be 16-byte aligned");
+  if (k_new) {
+    if (!v_new) return fail(NSLG_EINVAL, "paged_prefill_append: null v_new");
+    if (k_new_stride < (int64_t)num_kv_heads * head_dim || v_new_stride < (int64_t)num_kv_heads * head_dim)
+      return fail(NSLG_EINVAL, "paged_prefill_append: k/v row stride smaller than Hkv*D");
+    if (((uintptr_t)k_new | (uintptr_t)v_new) & 15 || (k_new_stride * 2) % 16 || (v_new_stride * 2) % 16)
+      return fail(NSLG_EINVAL, "paged_prefill_append: k_new/v_new rows must be 16-byte aligned");
+    // the kernel addresses k_new / v_new rows with 32-bit byte offsets
+    const int64_t rows = q_rows ? (int64_t)batch * grid_width : total_q;
+    if (rows * (k_new_stride > v_new_stride ? k_new_stride : v_new_stride) * 2 > (int64_t)0xffffffff)
+      return fail(NSLG_EUNSUPPORTED, "paged_prefill_append: k_new/v_new rows span >= 4 GiB");
+  }
   if (num_pages * (int64_t)page_size >= ((int64_t)1 << 31))
     return fail(NSLG_EUNSUPPORTED, "paged_prefill: pool has >= 2^31 token slots");
   if ((int64_t)page_size * num_kv_heads * head_dim * 2 > (int64_t)0xffffffff)
@@ -751,6 +864,16 @@ int prefill_impl(const void* q, int64_t q_stride, const int32_t* qo_indptr, cons
   p.pad_work = q_rows ? batch : 0;
   if ((int64_t)p.num_work + p.pad_work > 0x7fffffff - 8) return fail(NSLG_EUNSUPPORTED, "paged_prefill: too many rows");
   p.per_xcd = (p.num_work + p.pad_work + 7) / 8;
+  p.k_new = (const uint16_t*)k_new;
+  p.v_new = (const uint16_t*)v_new;
+  p.k_new_stride = k_new_stride;
+  p.v_new_stride = v_new_stride;
+  p.k_new_bytes = p.v_new_bytes = 0;
+  if (k_new) {
+    const int64_t rows = q_rows ? (int64_t)batch * grid_width : total_q;
+    p.k_new_bytes = (uint32_t)(rows * k_new_stride * 2);
+    p.v_new_bytes = (uint32_t)(rows * v_new_stride * 2);
+  }
   hipStream_t s = as_stream(stream);
   if (dtype == NSLG_F16) {
     switch (head_dim) {
@@ -798,4 +921,22 @@ extern "C" int nslg_paged_prefill_grid(const void* q, int64_t q_stride, const in
   return prefill_impl(q, q_stride, qo_indptr, q_rows, grid_width, total_q, max_q, k_pool, v_pool, num_pages,
                       page_size, kv_indptr, kv_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads,
                       head_dim, sm_scale, dtype, out, out_stride, stream);
+}
+
+extern "C" int nslg_paged_prefill_append(const void* q, int64_t q_stride, const int32_t* qo_indptr,
+                                         const int32_t* q_rows, int32_t grid_width, int64_t total_q,
+                                         int32_t max_q, const void* k_new, int64_t k_new_stride,
+                                         const void* v_new, int64_t v_new_stride, void* k_pool, void* v_pool,
+                                         int64_t num_pages, int32_t page_size, const int32_t* kv_indptr,
+                                         const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                         int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, float sm_scale, int32_t dtype, void* out,
+                                         int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                         nslg_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (batch > 0 && total_q > 0 && (!k_new || !v_new)) return fail(NSLG_EINVAL, "paged_prefill_append: null k_new/v_new");
+  return prefill_impl(q, q_stride, qo_indptr, q_rows, grid_width, total_q, max_q, k_pool, v_pool, num_pages,
+                      page_size, kv_indptr, kv_indices, kv_last_page_len, batch, num_qo_heads, num_kv_heads,
+                      head_dim, sm_scale, dtype, out, out_stride, stream, k_new, k_new_stride, v_new, v_new_stride);
 }

@@ -908,6 +908,100 @@ def _paged_prefill_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int,
     return out
 
 
+def _paged_prefill_append_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
+                                k_new: torch.Tensor, v_new: torch.Tensor, k_layer: torch.Tensor,
+                                v_layer: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                                kv_last_page_len: torch.Tensor, workspace: Workspace,
+                                q_rows: Optional[torch.Tensor] = None, grid_width: int = 0
+                                ) -> Optional[torch.Tensor]:
+    """nslg_paged_prefill_append for the cache manager (its pool layer, plan and
+    workspace taken as they are): the forward's K/V rows written and its queries
+    attended in one launch. None, with nothing launched, where the one launch does not
+    apply (fp32 pools, or q / k_new / v_new not the contiguous rows of a 16-bit
+    forward): the caller then appends and runs _paged_prefill_layer, whose checks
+    raise any error."""
+    dev, dt = k_layer.get_device(), k_layer.dtype
+    if dt == torch.float32:
+        return None
+    P, ps, Hkv, D = k_layer.shape
+    B = kv_indptr.numel() - 1
+    n = q.shape[0] if q.dim() == 3 else -1
+    for x in (k_new, v_new):
+        if (x.get_device() != dev or x.dtype != dt or not x.is_contiguous() or x.dim() < 2
+                or x.shape[-1] != D or x.shape[-2] != Hkv or x.numel() != n * Hkv * D):
+            return None
+    if (q.get_device() != dev or q.dtype != dt or q.stride(2) != 1 or q.stride(1) != D or n < total_q
+            or q.shape[2] != D or (q_rows is not None and (grid_width < 1 or n != B * grid_width))):
+        return None
+    Hq = q.shape[1]
+    out = torch.empty((n, Hq, D), dtype=dt, device=q.device)
+    key = (B, Hq, D, int(total_q), int(max_q))
+    need = _PREFILL_WS.get(key)
+    if need is None:
+        need = _PREFILL_WS[key] = int(_lib.load().nslg_paged_prefill_workspace_size(*key))
+        if len(_PREFILL_WS) > 4096:
+            _PREFILL_WS.clear()
+    ws = workspace.get(need)
+    rc = _lib.fast().paged_prefill_append(
+        q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), None if q_rows is None else q_rows.data_ptr(),
+        int(grid_width), int(total_q), int(max_q), k_new.data_ptr(), Hkv * D, v_new.data_ptr(), Hkv * D,
+        k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
+        kv_last_page_len.data_ptr(), B, Hq, Hkv, D, 1.0 / math.sqrt(D), _DTYPE_CODE[dt], out.data_ptr(), Hq * D,
+        ws.data_ptr(), ws.numel(), _stream(k_layer))
+    _lib.check(rc, "nslg_paged_prefill_append")
+    return out
+
+
+def paged_prefill_append(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
+                         k_new: torch.Tensor, v_new: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                         kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+                         sm_scale: Optional[float] = None, workspace: Optional[Workspace] = None,
+                         q_rows: Optional[torch.Tensor] = None, grid_width: int = 0) -> torch.Tensor:
+    """append_kv of the forward's new rows followed by paged_prefill, in one launch
+    (nslg_paged_prefill_append; 16-bit pools). k_new / v_new: [..., Hkv, D] with q's
+    rows (ragged [T] rows, or the B * grid_width grid rows with q_rows): token t of
+    sequence b is written to position L_b - n_b + t through the block table. Returns
+    paged_prefill's result; the pool holds the rows, as after append_kv."""
+    _require_gpu(q, qo_indptr, k_new, v_new, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len)
+    for t, name in ((qo_indptr, "qo_indptr"), (kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"),
+                    (kv_last_page_len, "kv_last_page_len")):
+        _i32(t, name)
+    if q_rows is not None:
+        _require_gpu(q, q_rows)
+        _i32(q_rows, "q_rows")
+        if q_rows.numel() < total_q or grid_width < 1 or q.shape[0] != (kv_indptr.numel() - 1) * grid_width:
+            raise ValueError("paged_prefill_append: a grid of B x grid_width rows of q and one q_rows entry per token")
+    P, ps, Hkv, D = _layer_geom(k_layer, v_layer)
+    if q.dim() != 3 or q.shape[2] != D or q.stride(2) != 1 or q.stride(1) != D:
+        raise ValueError(f"paged_prefill_append: q must be [T, Hq, {D}] with a contiguous [Hq, D] block")
+    if q.dtype != k_layer.dtype or k_new.dtype != k_layer.dtype or v_new.dtype != k_layer.dtype:
+        raise TypeError("paged_prefill_append: q, k_new and v_new dtypes must match the pool")
+    if tuple(k_new.shape[-2:]) != (Hkv, D) or tuple(v_new.shape[-2:]) != (Hkv, D):
+        raise ValueError("paged_prefill_append: k_new/v_new trailing dims must be [Hkv, D] of the pool")
+    nk, ks, _ = _rows(k_new, "k_new")
+    nv, vs, _ = _rows(v_new, "v_new")
+    T, Hq, _ = q.shape
+    if nk != T or nv != T:
+        raise ValueError(f"paged_prefill_append: {nk} k rows / {nv} v rows for {T} q rows")
+    B = kv_indptr.numel() - 1
+    if qo_indptr.numel() != B + 1 or T < total_q:
+        raise ValueError("paged_prefill_append: qo_indptr must have B+1 entries and q at least total_q rows")
+    out = torch.empty((T, Hq, D), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    need = int(lib.nslg_paged_prefill_workspace_size(B, Hq, D, int(total_q), int(max_q)))
+    ws = (workspace or Workspace(q.device)).get(need)
+    scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    rc = lib.nslg_paged_prefill_append(q.data_ptr(), q.stride(0), qo_indptr.data_ptr(),
+                                       None if q_rows is None else q_rows.data_ptr(), int(grid_width),
+                                       int(total_q), int(max_q), k_new.data_ptr(), ks, v_new.data_ptr(), vs,
+                                       k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(),
+                                       kv_indices.data_ptr(), kv_last_page_len.data_ptr(), B, Hq, Hkv, D, scale,
+                                       dtype_code(q.dtype), out.data_ptr(), out.stride(0), ws.data_ptr(),
+                                       ws.numel(), _stream(q))
+    _lib.check(rc, "nslg_paged_prefill_append")
+    return out
+
+
 def paged_prefill(q: torch.Tensor, qo_indptr: torch.Tensor, total_q: int, max_q: int,
                   k_layer: torch.Tensor, v_layer: torch.Tensor, kv_indptr: torch.Tensor,
                   kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,

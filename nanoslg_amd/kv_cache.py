@@ -1192,6 +1192,9 @@ class PagedCacheContext(CacheContext):
                 launch = self._decode_launch = cache._decode_launcher(plan, q.shape[2])
             return launch(layer_idx, q, k_new, v_new)
         k_layer, v_layer = pool.layer(layer_idx)
+        o = self._prefill(q, k_layer, v_layer, k_new, v_new)  # the write and the attention in one launch
+        if o is not None:
+            return o
         kern._append_kv_layer(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         return self._prefill(q, k_layer, v_layer)
 
@@ -1217,13 +1220,22 @@ class PagedCacheContext(CacheContext):
         q_rot = kern.rope_append(q, k_new, v_new, pos, plan.slots_for(S), cos, sin, k_layer, v_layer)
         return self._prefill(q_rot, k_layer, v_layer)
 
-    def _prefill(self, q, k_layer, v_layer):
-        """Causal attention of the forward's rows (K/V already written)."""
+    def _prefill(self, q, k_layer, v_layer, k_new=None, v_new=None):
+        """Causal attention of the forward's rows (K/V already written). With k_new and
+        v_new ([B, S, Hkv, D], the forward's rows): their write into the pages in the
+        same launch (16-bit pools), or None where that launch does not apply."""
         cache, plan = self.cache, self._plan
         kern = cache.kernels
         B, S = q.shape[0], q.shape[1]
         Hq, D = q.shape[2], q.shape[3]
         q_grid = q.reshape(B * S, Hq, D)
+        if k_new is not None:
+            uniform = self._uniform_rows and S == self._iw
+            o = kern._paged_prefill_append_layer(
+                q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_new, v_new, k_layer, v_layer, plan.indptr,
+                plan.indices, plan.lpl, cache.workspace, q_rows=None if uniform else plan.rows_for(S),
+                grid_width=0 if uniform else S)
+            return None if o is None else o.view(B, S, Hq * D)
         if self._uniform_rows and S == self._iw:  # every grid row is a token: the ragged rows themselves
             o = kern._paged_prefill_layer(q_grid, plan.qo_indptr, plan.total_q, self._max_q, k_layer, v_layer,
                                           plan.indptr, plan.indices, plan.lpl, cache.workspace)
@@ -1807,7 +1819,17 @@ class ContiguousCacheContext(CacheContext):
     def attend(self, layer_idx, q, k_new, v_new, n_heads, n_kv_heads):
         cache, plan = self.cache, self._plan
         k_layer, v_layer = cache.paged_view(layer_idx)
-        cache.kernels.append_kv(k_new, v_new, plan.slots_for(q.shape[1]), k_layer, v_layer)
+        B, S = q.shape[0], q.shape[1]
+        if not (self._is_decode and S == 1):
+            # the write and the attention in one launch (a sequence's slot is its one page)
+            uniform = self._uniform_rows and S == self._iw
+            o = cache.kernels._paged_prefill_append_layer(
+                q.reshape(B * S, q.shape[2], q.shape[3]), plan.qo_indptr, plan.total_q, self._max_q, k_new, v_new,
+                k_layer, v_layer, plan.indptr, plan.indices, plan.lpl, cache.workspace,
+                q_rows=None if uniform else plan.rows_for(S), grid_width=0 if uniform else S)
+            if o is not None:
+                return o.view(B, S, -1)
+        cache.kernels.append_kv(k_new, v_new, plan.slots_for(S), k_layer, v_layer)
         return self._attend_written(q, k_layer, v_layer)
 
     def attend_rope(self, layer_idx, q, k_new, v_new, cos, sin, n_heads, n_kv_heads):

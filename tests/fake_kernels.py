@@ -114,6 +114,40 @@ def _append_kv_layer(k_new, v_new, slot_mapping, k_layer, v_layer):
     append_kv(k_new, v_new, slot_mapping, k_layer, v_layer)
 
 
+FUSED_PREFILL_APPEND = True  # False: decline the one-launch write + attention, as for fp32 pools on the GPU
+
+
+def _paged_prefill_append_layer(q, qo_indptr, total_q, max_q, k_new, v_new, k_layer, v_layer, kv_indptr,
+                                kv_indices, kv_last_page_len, workspace, q_rows=None, grid_width=0):
+    """The contract of nslg_paged_prefill_append, by its own rule (no slot mapping):
+    token t of sequence b, row qo_indptr[b] + t (or q_rows[qo_indptr[b]] + t) of
+    k_new / v_new, goes to position L_b - n_b + t through the block table (slot 0 of
+    page 0 past the table); then paged_prefill."""
+    if not FUSED_PREFILL_APPEND:
+        return None
+    CALLS.append(("paged_prefill_append", int(total_q)))
+    ps, Hkv, D = k_layer.shape[1], k_layer.shape[2], k_layer.shape[3]
+    kr, vr = k_new.reshape(-1, Hkv, D), v_new.reshape(-1, Hkv, D)
+    kp, vp = k_layer.view(-1, Hkv, D), v_layer.view(-1, Hkv, D)
+    qo, ip, idx, lpl = (t.tolist() for t in (qo_indptr, kv_indptr, kv_indices, kv_last_page_len))
+    rows = None if q_rows is None else q_rows.tolist()
+    for b in range(len(ip) - 1):
+        n, npg = qo[b + 1] - qo[b], ip[b + 1] - ip[b]
+        L = (npg - 1) * ps + lpl[b] if npg > 0 else 0
+        r0 = qo[b] if rows is None else (rows[qo[b]] if n > 0 else 0)
+        for t in range(n):
+            pos = L - n + t
+            pi = pos // ps
+            pid = idx[ip[b] + pi] if pi < npg else 0
+            if not 0 <= pid < k_layer.shape[0]:
+                continue
+            slot = pid * ps + pos % ps if pi < npg else 0
+            kp[slot] = kr[r0 + t]
+            vp[slot] = vr[r0 + t]
+    return _paged_prefill_layer(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices,
+                                kv_last_page_len, workspace, q_rows=q_rows, grid_width=grid_width)
+
+
 def _paged_prefill_layer(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,
                          workspace, q_rows=None, grid_width=0):
     return paged_prefill(q, qo_indptr, total_q, max_q, k_layer, v_layer, kv_indptr, kv_indices, kv_last_page_len,

@@ -117,6 +117,36 @@ def test_prefill_grid_argument_checks():
     assert "grid" in _lib.last_error()
 
 
+def test_prefill_append_argument_checks():
+    """nslg_paged_prefill_append: the new rows' pointers, strides and alignment, and the
+    pool dtype, are checked on the host before any launch; the fast-call binding
+    returns the same statuses."""
+    from nanoslg_amd import _lib
+    lib, fast = _lib.load(), _lib.fast()
+    A = 4096
+
+    def call(k=A, ks=1024, v=A, vs=1024, dt=0, q_rows=None, width=0, D=128):
+        args = (A, 4096, A, q_rows, width, 10, 8, k, ks, v, vs, A, A, 100, 16, A, A, A, 2, 32, 8, D, 0.1, dt,
+                A, 4096, None, 0, None)
+        rc = lib.nslg_paged_prefill_append(*args)
+        assert fast.paged_prefill_append(*args) == rc
+        return rc
+
+    assert call(k=None) == -1 and "k_new" in _lib.last_error()
+    assert call(v=None) == -1 and "k_new" in _lib.last_error()
+    assert call(ks=1000) == -1 and "stride" in _lib.last_error()      # < Hkv * D
+    assert call(vs=1028) == -1 and "16-byte" in _lib.last_error()     # rows not 16-byte aligned
+    assert call(k=A + 8) == -1 and "16-byte" in _lib.last_error()
+    assert call(dt=2) == -2 and "f16 or bf16" in _lib.last_error()   # fp32 pools: append, then prefill
+    assert call(D=96) == -2 and "head_dim" in _lib.last_error()
+    # rows spanning 4 GiB: 10 ragged rows at a 2^28-element stride
+    assert call(ks=1 << 28) == -2 and "4 GiB" in _lib.last_error()
+    assert call(q_rows=A, width=0) == -1 and "grid" in _lib.last_error()
+    zero = (A, 4096, A, None, 0, 0, 0, None, 0, None, 0, A, A, 100, 16, A, A, A, 2, 32, 8, 128, 0.1, 0,
+            A, 4096, None, 0, None)
+    assert lib.nslg_paged_prefill_append(*zero) == 0  # no token: nothing to read, write or launch
+
+
 def test_rope_append_argument_checks():
     from nanoslg_amd import _lib
     lib = _lib.load()
@@ -300,6 +330,6 @@ def test_fast_binding_signatures_match_the_header():
     code = {c_void_p: "p", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
     src = (ROOT / "nanoslg_amd" / "csrc" / "fastcall.c").read_text()
     found = re.findall(r'parse\("(\w+)", "(\w+)"', src)
-    assert len(found) == 16
+    assert len(found) == 17
     for fn, sig in found:
         assert sig == "".join(code[t] for t in _lib.SIGNATURES["nslg_" + fn][1]), fn
