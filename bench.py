@@ -66,6 +66,8 @@ def _parse():
                          "one forward attends every layer, as a model's decode step does)")
     ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128, 256],
                     help="prefill workload: head dim (heads scaled to keep Hq*D = 4096, Hkv*D = 1024)")
+    ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
+                    help="prefill workload: the pool's and Q/K/V's dtype")
     return ap.parse_args()
 
 
@@ -883,16 +885,17 @@ def run_prefill(args):
     HQ, HKV = 4096 // D, 1024 // D
     nchunks = L // CH
     dev = torch.device("cuda:0")
+    dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     cfg = KVCacheConfig(num_layers=1, num_kv_heads=HKV, num_qo_heads=HQ, head_dim=D, page_size=PS,
-                        max_pages=B * L // PS + 64, dtype=torch.float16, device=dev,
+                        max_pages=B * L // PS + 64, dtype=dt, device=dev,
                         enable_prefix_caching=False, backend="paged")
     mgr = PagedKVCache(cfg)
     timed = EventTimedKernels(kernels)
     mgr.kernels = timed
     g = torch.Generator(device=dev).manual_seed(args.seed)
-    q = torch.randn(nchunks, B, CH, HQ, D, generator=g, device=dev, dtype=torch.float16)
-    k = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=torch.float16)
-    v = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn(nchunks, B, CH, HQ, D, generator=g, device=dev, dtype=dt)
+    k = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=dt)
+    v = torch.randn(nchunks, B, CH, HKV, D, generator=g, device=dev, dtype=dt)
     ids = [f"p{b}" for b in range(B)]
 
     def admit():
@@ -951,7 +954,7 @@ def run_prefill(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 (fp32 accumulate)",
+        "dtype": f"{args.dtype} (fp32 accumulate)",
         "data": "synthetic: Q/K/V ~ N(0,1), seeded",
         "config": {"workload": "chunked_prefill", "batch": B, "tokens_per_seq": L, "chunk": CH,
                    "page_size": PS, "heads": f"{HQ}q/{HKV}kv", "head_dim": D, "layers": 1},

@@ -447,7 +447,19 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
 
   // ---- per-block pieces ------------------------------------------------------------
   // K operands of a 32-key block: keys kbase + 16t + r, columns 32s + 8gq .. +7
+  // The lane's (r, gq) for the LDS operand addresses. bf16 (two MFMAs per P tile, 8
+  // more registers) recomputes them per block from the lane id through an empty asm,
+  // so they are not held across the loop: held, they spilled, and each reload's wait
+  // on the vector memory counter also waited for the next tile's loads.
+  auto lane_rg = [&](int& rr, int& gg) {
+    int ln = lane;
+    if constexpr (kSplitP) asm volatile("" : "+v"(ln));
+    rr = ln & 15;
+    gg = ln >> 4;
+  };
   auto load_k = [&](int stage, int kb, u16x8 (&ka)[2][kSteps]) {
+    int r, gq;
+    lane_rg(r, gq);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const uint16_t* krow = &k_lds[stage][(32 * kb + 16 * t + r) * kPitch + 8 * gq];
@@ -474,6 +486,8 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
   // 8 + a and 12 + a. Lane r addresses keys kbase + 4gq + r/4 (then + 16), columns
   // 16n + 4(r%4) .. +3, so it receives keys kbase + 4gq + 0..3 (+ 16) at d = 16n + r.
   auto load_v = [&](int stage, int kb, u16x8 (&va)[NT]) {
+    int r, gq;
+    lane_rg(r, gq);
     const uint16_t* vsrc = &v_lds[stage][(32 * kb + 4 * gq + (r >> 2)) * kVPitch + 4 * (r & 3)];
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -688,11 +702,15 @@ __global__ void __launch_bounds__(64 * PrefillTile<D>::kWaves) paged_prefill_ker
     __syncthreads();
   }
   // ---- epilogue: normalise and store rows ----------------------------------------
+  // The rows' output addresses are found again here (the lane index through an empty
+  // asm, so the compiler cannot keep the prologue's values alive across the tile loop)
+  int er = r;
+  asm volatile("" : "+v"(er));
 #pragma unroll
   for (int cb = 0; cb < kCB; ++cb) {
     const float l_tot = lsum[cb][0];
-    if (!row_ok[cb]) continue;
-    const int row = row0_wg + wave * kRowsPerWave + cb * 16 + r;
+    const int row = row0_wg + wave * kRowsPerWave + cb * 16 + er;
+    if (row >= nrows) continue;
     const int t = row / G;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int64_t orr = grid_row(p, q0 + t);
