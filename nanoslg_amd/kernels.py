@@ -647,6 +647,32 @@ def _forward_plan_csr(tables, row_offset, pages_have, synced, patch_indptr, patc
     return slot, pos, rows, qo
 
 
+def _forward_plan_csr_at(tables, buf, mid, npatch, total_pages, B, iw, page_size, T, out):
+    """_forward_plan_csr with its inputs at fixed places of one int32 upload buffer
+    (the cache's native plan): from entry `mid` on, start, new tokens, offsets, pages
+    held, row offset, pages held, synced (B each), the patch pointers (B + 1) and the
+    patch entries (at least one); before them, at 0, the CSR pointers (B + 1); the
+    CSR indices follow the patch. Pointers are computed here instead of views (each
+    costs the host ~0.5 us)."""
+    sizes = [B * iw, B * iw, T, B + 1]
+    if out.numel() < sum(sizes) or out.dtype != torch.int32 or buf.dtype != torch.int32:
+        raise ValueError("forward_plan_csr: the output buffer is too small or not int32")
+    slot, pos, rows, qo = out[:sum(sizes)].split(sizes)
+    a = buf.data_ptr()
+    m = a + 4 * mid
+    patch = m + 4 * (8 * B + 1)
+    idx = patch + 4 * max(npatch, 1)
+    base = out.data_ptr()
+    o1, o2 = 4 * B * iw, 8 * B * iw
+    o3 = o2 + 4 * T
+    rc = _lib.fast().forward_plan_csr(tables.data_ptr(), tables.numel(), m + 16 * B, m + 20 * B, m + 24 * B,
+                                      m + 28 * B, patch, int(npatch), a, idx, int(total_pages), m, m + 4 * B,
+                                      m + 8 * B, B, iw, page_size, base, base + o1, base + o2, base + o3,
+                                      _stream(tables))
+    _lib.check(rc, "nslg_forward_plan_csr")
+    return slot, pos, rows, qo
+
+
 class DecodeLaunch:
     """Append + split-K decode for every layer of one decode forward.
 

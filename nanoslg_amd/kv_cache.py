@@ -1321,15 +1321,25 @@ class PagedKVCache(KVCacheManager):
         else:
             dev = torch.zeros(total + extra, dtype=torch.int32)
             dev[:total] = torch.from_numpy(host[:total])
-        sizes = [B + 1, B, 0, 0, nz, B, B, B, B, B, B, B, B + 1, max(npatch, 1), max(total_pages, 1), tail]
-        (d_indptr, d_lpl, d_cs, d_cd, d_zero, d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch,
-         d_idx, fp_out) = dev.split(sizes)
-        slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch, npatch,
-                                                             d_indptr, d_idx, total_pages, d_start, d_n, d_off, B, iw,
-                                                             ps, T, fp_out)
+        # the buffer: indptr (B+1), last-page lengths (B), the pages to zero (nz), then
+        # start, new tokens, offsets, pages held, row, pages held, synced (B each), the
+        # patch pointers (B+1) and entries, the CSR indices, forward_plan's outputs;
+        # views only of what the plan keeps (each view costs the host ~0.5 us)
+        n_mid = 8 * B + 1 + max(npatch, 1)
+        d_indptr, d_lpl, d_zero, _, d_idx, fp_out = dev.split([B + 1, B, nz, n_mid, max(total_pages, 1), tail])
+        if hasattr(kern, "_forward_plan_csr_at"):
+            slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr_at(tables.dev, dev, 2 * B + 1 + nz, npatch, total_pages,
+                                                                    B, iw, ps, T, fp_out)
+        else:
+            (d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch) = _.split(
+                [B, B, B, B, B, B, B, B + 1, max(npatch, 1)])
+            slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch,
+                                                                 npatch, d_indptr, d_idx, total_pages, d_start, d_n,
+                                                                 d_off, B, iw, ps, T, fp_out)
         for st in states:
             st.synced = st.n_pages
-        plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t, d_cs, d_cd, d_zero,
+        none = d_zero[:0]  # no page copies in this forward
+        plan = _ForwardPlan.from_tensors(B, iw, slot_t, pos_t, d_indptr, d_idx, d_lpl, qo_t, rows_t, none, none, d_zero,
                                          total_pages, T)
         return plan, nz, shared_first
 

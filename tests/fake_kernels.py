@@ -298,6 +298,19 @@ def _forward_plan(kv_indptr, kv_indices, start, new_tokens, input_offsets, pages
     return tuple(flat.split([B * iw, B * iw, T, B + 1]))
 
 
+def _forward_plan_csr_at(tables, buf, mid, npatch, total_pages, B, iw, page_size, T, out):
+    """As nanoslg_amd.kernels._forward_plan_csr_at: the inputs found at the same places
+    of the upload buffer, then _forward_plan_csr."""
+    m = buf[mid:]
+    start, n, off, _, row, have, syn = (m[i * B:(i + 1) * B] for i in range(7))
+    pip = m[7 * B:8 * B + 1]
+    patch = m[8 * B + 1:8 * B + 1 + max(npatch, 1)]
+    idx_at = mid + 8 * B + 1 + max(npatch, 1)
+    idx = buf[idx_at:idx_at + max(total_pages, 1)]
+    return _forward_plan_csr(tables, row, have, syn, pip, patch, npatch, buf[:B + 1], idx, total_pages, start, n, off,
+                             B, iw, page_size, T, out)
+
+
 def _forward_plan_csr(tables, row_offset, pages_have, synced, patch_indptr, patch, patch_total, kv_indptr, kv_indices,
                       total_pages, start, new_tokens, input_offsets, B, iw, page_size, T, out):
     """As nanoslg_amd.kernels._forward_plan_csr: the two launches it fuses, in order."""
