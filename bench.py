@@ -664,16 +664,20 @@ def run_radix(args):
     wctx.attend(0, randn(2, 5, HQ, D), randn(2, 5, HKV, D), randn(2, 5, HKV, D), HQ, HKV)
     scratch.end_forward(wctx)
     del scratch, wctx
-    # suffix prefill with copy-on-write of the shared page
+    # suffix prefill with copy-on-write of the shared page (the collector settled and
+    # paused as around the decode steps: a full collection walks every object of the
+    # process, 15-36 ms here, and had landed in this forward in some runs)
     S = max(suffix)
     q, k, v = randn(B, S, HQ, D), randn(B, S, HKV, D), randn(B, S, HKV, D)
+    _settle_gc()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ctx = mgr.begin_forward(ids, suffix)
-    ctx.attend(0, q, k, v, HQ, HKV)
-    mgr.end_forward(ctx)
-    torch.cuda.synchronize()
-    suffix_ms = (time.perf_counter() - t0) * 1e3
+    with _GcPaused():
+        t0 = time.perf_counter()
+        ctx = mgr.begin_forward(ids, suffix)
+        ctx.attend(0, q, k, v, HQ, HKV)
+        mgr.end_forward(ctx)
+        torch.cuda.synchronize()
+        suffix_ms = (time.perf_counter() - t0) * 1e3
     cow = len(ctx.cow_pairs)
     assert cow == B and all(mgr.seqs[s].bt[full] != owner_pages[full] for s in ids)
     # decode
@@ -912,6 +916,7 @@ def run_prefill(args):
         for sid in ids:
             mgr.release_sequence(sid)
 
+    _settle_gc()
     for _ in range(max(1, args.warmup // 8)):
         admit()
         prefill()
@@ -919,14 +924,15 @@ def run_prefill(args):
     torch.cuda.synchronize()
     steps = args.steps
     wall = 0.0
-    for _ in range(steps):
-        admit()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        prefill()
-        torch.cuda.synchronize()
-        wall += time.perf_counter() - t0
-        release()
+    with _GcPaused():
+        for _ in range(steps):
+            admit()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            prefill()
+            torch.cuda.synchronize()
+            wall += time.perf_counter() - t0
+            release()
     ms_step = wall / steps * 1e3
     flops = prefill_flops(B, L, HQ, D)
     tflops = flops / (wall / steps) / 1e12
@@ -1132,11 +1138,12 @@ def run_rope(args):
             for _ in range(args.warmup):
                 fn()
             torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                fn()
-            torch.cuda.synchronize()
-            res[f"{label}_us"] = round((time.perf_counter() - t0) / args.steps * 1e6, 2)
+            with _GcPaused():
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    fn()
+                torch.cuda.synchronize()
+                res[f"{label}_us"] = round((time.perf_counter() - t0) / args.steps * 1e6, 2)
         # kernel-only time of the fused launch: 20 launches captured in a HIP graph
         # (the launch itself allocates nothing and sets no memory), replayed with events
         # around the replays on the replay stream, so host overhead does not show
