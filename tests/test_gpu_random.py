@@ -34,6 +34,9 @@ def test_random_serving_traffic_on_gpu(seed, ps, pages):
     (504, 4, 50, 8, 8, 64, torch.bfloat16),     # G = 1
     (505, 1, 70, 16, 2, 64, torch.float16),     # G = 8, one-token pages
     (506, 16, 24, 32, 8, 128, torch.bfloat16),
+    (507, 16, 40, 12, 2, 256, torch.bfloat16),  # G = 6 at head_dim 256
+    (508, 5, 60, 24, 8, 64, torch.float16),     # G = 3, pages of 5 tokens
+    (509, 16, 40, 16, 1, 128, torch.float16),   # G = 16
 ])
 def test_random_serving_traffic_shapes_on_gpu(seed, ps, pages, HQ, HKV, D, dtype):
     """The same traffic at other head shapes and in bf16, on the same bar."""
