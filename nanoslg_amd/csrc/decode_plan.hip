@@ -91,8 +91,10 @@ __device__ void zero_part(const PlanStepArgs<N>& a, int z) {
 // Pages of sequence s before the step, and whether this step opens one.
 template <int N>
 __device__ inline void seq_step(const PlanStepArgs<N>& a, int s, int& np_in, int& lpl_in, bool& opens) {
-  np_in = a.indptr_in[s + 1] - a.indptr_in[s];
-  lpl_in = np_in > 0 ? a.last_len_in[s] : a.page_size;
+  // all three loads issued at once (the length is read whether or not it is used)
+  const int ip0 = a.indptr_in[s], ip1 = a.indptr_in[s + 1], lpl = a.last_len_in[s];
+  np_in = ip1 - ip0;
+  lpl_in = np_in > 0 ? lpl : a.page_size;
   lpl_in = lpl_in < 1 ? 1 : (lpl_in > a.page_size ? a.page_size : lpl_in);
   opens = lpl_in == a.page_size;
 }
@@ -110,14 +112,19 @@ __global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs<N> a
   // opened by sequences before b (its index in the zero list); the first wave
   // computes both, the other waves only copy
   __shared__ int seg_out_sh, new_before_sh;
+  // this sequence's own numbers first: their loads overlap the prefix's below
+  int np_in, lpl_in;
+  bool opens;
+  seq_step(a, b, np_in, lpl_in, opens);
+  const int seg_in = a.indptr_in[b];
   if (tid < 64) {
     int pages = 0, opened = 0;
     for (int s = lane; s < b; s += 64) {
-      int np_in, lpl_in;
-      bool opens;
-      seq_step(a, s, np_in, lpl_in, opens);
-      pages += np_in + (opens ? 1 : 0);
-      opened += opens ? 1 : 0;
+      int np_s, lpl_s;
+      bool opens_s;
+      seq_step(a, s, np_s, lpl_s, opens_s);
+      pages += np_s + (opens_s ? 1 : 0);
+      opened += opens_s ? 1 : 0;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -131,10 +138,6 @@ __global__ void __launch_bounds__(256) decode_plan_step_kernel(PlanStepArgs<N> a
   }
   __syncthreads();
   const int seg_out = seg_out_sh;
-  int np_in, lpl_in;
-  bool opens;
-  seq_step(a, b, np_in, lpl_in, opens);
-  const int seg_in = a.indptr_in[b];
   for (int i = tid; i < np_in; i += blockDim.x) a.indices_out[seg_out + i] = a.indices_in[seg_in + i];
   if (tid == 0) {
     int page;  // the page the new token goes to
