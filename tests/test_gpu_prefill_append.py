@@ -104,3 +104,36 @@ def test_prefill_append_equals_append_then_prefill(shape, dtype, grid):
     torch.cuda.synchronize()
     assert torch.equal(kf, kr) and torch.equal(vf, vr), "pool rows differ"
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), (out.float() - ref.float()).abs().max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("grid", [False, True])
+def test_prefill_append_strided_rows(grid):
+    """k_new / v_new as the K and V halves of one [rows, 2, Hkv, D] projection output
+    (row strides of 2 * Hkv * D elements, different base addresses), against append
+    then prefill on the same rows."""
+    from nanoslg_amd import kernels as K
+    B, Hq, Hkv, D, ps = SHAPES[0]
+    c = _case(720, B, Hq, Hkv, D, ps, grid)
+    print(f"prefill_append strided grid={grid} T={c['T']}", flush=True)
+    sys.stdout.flush()
+    g = torch.Generator().manual_seed(720)
+    P, n_rows = c["P"], c["n_rows"]
+    k_pool = torch.randn(P, ps, Hkv, D, generator=g).half().to(DEV)
+    v_pool = torch.randn(P, ps, Hkv, D, generator=g).half().to(DEV)
+    q = torch.randn(n_rows, Hq, D, generator=g).half().to(DEV)
+    kv = torch.randn(n_rows, 2, Hkv, D, generator=g).half().to(DEV)
+    k_new, v_new = kv[:, 0], kv[:, 1]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(DEV)  # noqa: E731
+    qo, ip, idx, lpl, slots = t(c["qo"]), t(c["indptr"]), t(c["indices"]), t(c["lpl"]), t(c["slots"])
+    rows = t(c["rows"][:max(c["T"], 1)]) if grid else None
+    W = c["W"] if grid else 0
+    kr, vr = k_pool.clone(), v_pool.clone()
+    K.append_kv(k_new, v_new, slots, kr, vr)
+    ref = K.paged_prefill(q, qo, c["T"], max(c["news"]), kr, vr, ip, idx, lpl, q_rows=rows, grid_width=W)
+    kf, vf = k_pool.clone(), v_pool.clone()
+    out = K.paged_prefill_append(q, qo, c["T"], max(c["news"]), k_new, v_new, kf, vf, ip, idx, lpl, q_rows=rows,
+                                 grid_width=W)
+    torch.cuda.synchronize()
+    assert torch.equal(kf, kr) and torch.equal(vf, vr), "pool rows differ"
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
