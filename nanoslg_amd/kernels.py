@@ -943,8 +943,8 @@ def _paged_prefill_append_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_
     """nslg_paged_prefill_append for the cache manager (its pool layer, plan and
     workspace taken as they are): the forward's K/V rows written and its queries
     attended in one launch. None, with nothing launched, where the one launch does not
-    apply (fp32 pools, or q / k_new / v_new not the contiguous rows of a 16-bit
-    forward): the caller then appends and runs _paged_prefill_layer, whose checks
+    apply (fp32 pools, q / k_new / v_new not rows of a 16-bit forward at one 16-byte
+    stride each): the caller then appends and runs _paged_prefill_layer, whose checks
     raise any error."""
     dev, dt = k_layer.get_device(), k_layer.dtype
     if dt == torch.float32:
@@ -952,10 +952,21 @@ def _paged_prefill_append_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_
     P, ps, Hkv, D = k_layer.shape
     B = kv_indptr.numel() - 1
     n = q.shape[0] if q.dim() == 3 else -1
+    strides = []
     for x in (k_new, v_new):
-        if (x.get_device() != dev or x.dtype != dt or not x.is_contiguous() or x.dim() < 2
-                or x.shape[-1] != D or x.shape[-2] != Hkv or x.numel() != n * Hkv * D):
+        if (x.get_device() != dev or x.dtype != dt or x.dim() < 2 or x.shape[-1] != D or x.shape[-2] != Hkv
+                or x.numel() != n * Hkv * D or x.data_ptr() % 16):
             return None
+        if x.is_contiguous():  # the model's own [B, S, Hkv, D] rows
+            strides.append(Hkv * D)
+            continue
+        try:  # rows at one stride, e.g. the K and V halves of one projection output
+            _, st, _ = _rows(x, "k_new/v_new")
+        except ValueError:
+            return None
+        if (st * x.element_size()) % 16:
+            return None
+        strides.append(st)
     if (q.get_device() != dev or q.dtype != dt or q.stride(2) != 1 or q.stride(1) != D or n < total_q
             or q.shape[2] != D or (q_rows is not None and (grid_width < 1 or n != B * grid_width))):
         return None
@@ -970,7 +981,7 @@ def _paged_prefill_append_layer(q: torch.Tensor, qo_indptr: torch.Tensor, total_
     ws = workspace.get(need)
     rc = _lib.fast().paged_prefill_append(
         q.data_ptr(), q.stride(0), qo_indptr.data_ptr(), None if q_rows is None else q_rows.data_ptr(),
-        int(grid_width), int(total_q), int(max_q), k_new.data_ptr(), Hkv * D, v_new.data_ptr(), Hkv * D,
+        int(grid_width), int(total_q), int(max_q), k_new.data_ptr(), strides[0], v_new.data_ptr(), strides[1],
         k_layer.data_ptr(), v_layer.data_ptr(), P, ps, kv_indptr.data_ptr(), kv_indices.data_ptr(),
         kv_last_page_len.data_ptr(), B, Hq, Hkv, D, 1.0 / math.sqrt(D), _DTYPE_CODE[dt], out.data_ptr(), Hq * D,
         ws.data_ptr(), ws.numel(), _stream(k_layer))

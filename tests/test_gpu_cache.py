@@ -115,6 +115,41 @@ def test_prefill_attend_checks_the_callers_tensors():
     check_state(mgr, ref, ids)
 
 
+def test_prefill_attend_takes_strided_kv_rows(monkeypatch):
+    """K/V given as the strided halves of one [B, S, 2, Hkv, D] projection output go
+    through the same one-launch write + prefill as contiguous rows, with the same
+    output and pool bytes."""
+    _log("cache: prefill attend with strided K/V rows")
+    from nanoslg_amd import kernels as K
+    taken = []
+    orig = K._paged_prefill_append_layer
+
+    def spy(*a, **k):
+        r = orig(*a, **k)
+        taken.append(r is not None)
+        return r
+    monkeypatch.setattr(K, "_paged_prefill_append_layer", spy)
+    g = torch.Generator().manual_seed(12)
+    S = 40
+    q = torch.randn(2, S, HQ, D, generator=g).half().to(DEV)
+    kv = torch.randn(2, S, 2, HKV, D, generator=g).half().to(DEV)
+    res = []
+    for strided in (False, True):
+        mgr, _ = make(prefix=False)
+        for sid in ("a", "b"):
+            mgr.allocate_sequence(sid)
+        k, v = kv[:, :, 0], kv[:, :, 1]
+        if not strided:
+            k, v = k.contiguous(), v.contiguous()
+        c = mgr.begin_forward(["a", "b"], [S, S])
+        o = c.attend(0, q, k, v, HQ, HKV)
+        mgr.end_forward(c)
+        torch.cuda.synchronize()
+        res.append((o, mgr.pool.k.clone(), mgr.pool.v.clone()))
+    assert taken == [True, True]
+    assert all(torch.equal(x, y) for x, y in zip(*res))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_head_dim_256_prefill_then_decode(dtype):
     """A 16-bit cache at head_dim 256: a ragged prefill and a chunk over cached
