@@ -27,7 +27,8 @@
  *   patch pointers [B+1], patch (the table entries the device rows lack) [max(np, 1)]
  * and tokens_used raised for every written page to its last written slot + 1. Pages
  * to zero are those of zero_pages that the forward does not write in every slot
- * (a page written whole needs no zeroing: the append leaves the same bytes).
+ * (a page written whole needs no zeroing: the forward's own write of its rows leaves
+ * the same bytes).
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -141,6 +142,12 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
     ++nbt;
     if (s->have < 0 || s->have > s->bt.len / 4) {
       PyErr_SetString(PyExc_ValueError, "plan_forward: a sequence holds more pages than its table");
+      goto done;
+    }
+    /* the plan is int32: positions and lengths below 2^31 */
+    if (s->start < 0 || s->start > 0x7fffffffLL || s->n_raw > 0x7fffffffLL || s->start + s->n > 0x7fffffffLL ||
+        s->off < -0x7fffffffLL || s->off > 0x7fffffffLL) {
+      PyErr_SetString(PyExc_ValueError, "plan_forward: a sequence's tokens, new tokens or offset out of range");
       goto done;
     }
     held += s->have;

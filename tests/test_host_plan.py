@@ -273,3 +273,19 @@ def test_native_plan_rejects_bad_arguments():
         plan([], [], None, 4, rc, tu, mk, None, np.zeros(8, np.int32), None)  # place must be callable
     with pytest.raises(TypeError):
         plan([], [], None, 4, rc, tu, mk, None, np.zeros(8, np.int32))  # 9 arguments
+
+
+def test_native_plan_rejects_out_of_range_sequences():
+    """A state whose token count is negative, or whose tokens would not fit the plan's
+    int32 positions, is refused before anything is read or written."""
+    import types
+    plan = _lib.host().plan_forward
+    rc, tu, mk = np.zeros(8, np.int64), np.zeros(8, np.int64), np.zeros(8, bool)
+    out = np.zeros(256, np.int32)
+    placed = []
+    for num_tokens, n in ((-1, 4), (0, 1 << 31), ((1 << 31) - 2, 4)):
+        st = types.SimpleNamespace(num_tokens=num_tokens, n_pages=1, bt=np.array([1, 0], np.int32), row=-1,
+                                   synced=0)
+        with pytest.raises(ValueError, match="out of range"):
+            plan([st], [n], None, 4, rc, tu, mk, None, out, placed.append)
+    assert not placed and not tu.any() and not out.any()
