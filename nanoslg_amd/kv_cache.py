@@ -1326,12 +1326,12 @@ class PagedKVCache(KVCacheManager):
         # patch pointers (B+1) and entries, the CSR indices, forward_plan's outputs;
         # views only of what the plan keeps (each view costs the host ~0.5 us)
         n_mid = 8 * B + 1 + max(npatch, 1)
-        d_indptr, d_lpl, d_zero, _, d_idx, fp_out = dev.split([B + 1, B, nz, n_mid, max(total_pages, 1), tail])
+        d_indptr, d_lpl, d_zero, d_mid, d_idx, fp_out = dev.split([B + 1, B, nz, n_mid, max(total_pages, 1), tail])
         if hasattr(kern, "_forward_plan_csr_at"):
             slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr_at(tables.dev, dev, 2 * B + 1 + nz, npatch, total_pages,
                                                                     B, iw, ps, T, fp_out)
         else:
-            (d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch) = _.split(
+            (d_start, d_n, d_off, d_have, d_row, d_have2, d_syn, d_pip, d_patch) = d_mid.split(
                 [B, B, B, B, B, B, B, B + 1, max(npatch, 1)])
             slot_t, pos_t, rows_t, qo_t = kern._forward_plan_csr(tables.dev, d_row, d_have2, d_syn, d_pip, d_patch,
                                                                  npatch, d_indptr, d_idx, total_pages, d_start, d_n,
