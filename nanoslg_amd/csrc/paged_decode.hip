@@ -300,6 +300,12 @@ __device__ inline V kv_load(const char* p) {
 // tile's first row (head offset included); rows past `last` repeat row `last`.
 //   K: lane l reads row l%16, 16 B at d = 32 s + 8 (l/16)
 //   V: lane l reads rows 4 (l/16) + j, D/16 elements at d = (D/16) (l%16)
+// Page-aligned tiles load K as whole rows and turn them into MFMA operands through
+// LDS at head dims up to 128; at 256 the stage's operand registers would cost the
+// kernel its second wave per SIMD, and K keeps the operand layout in memory.
+template <int D>
+constexpr bool kKRows = D <= 128;
+
 template <int D, bool kStream>
 __device__ inline void load_tile_rows(const char* kbase, const char* vbase, int row_bytes, int last,
                                       Tile<D>& t) {
@@ -308,14 +314,64 @@ __device__ inline void load_tile_rows(const char* kbase, const char* vbase, int 
   const int gq = lane >> 4;
   constexpr int NT = D / 16;
   typedef typename RowVec<NT>::type VT;
-  const char* kp = kbase + (r < last ? r : last) * row_bytes + 16 * gq;
+  if constexpr (kKRows<D>) {
+    // K as whole rows: load s takes tokens kTokPerLoad*s .. +kTokPerLoad-1, D/8 lanes
+    // per token, 16 bytes each (as the V loads below, each instruction reads whole
+    // 2D-byte rows; 16 tokens x 64 bytes per instruction streamed 3.5 % slower at
+    // batch 64). The MFMA operand layout comes from the wave's stage in LDS.
+    constexpr int kLanesPerTok = D / 8;
+    constexpr int kTokPerLoad = 64 / kLanesPerTok;
+    const int k_tok = lane / kLanesPerTok;
+    const int k_ch = lane % kLanesPerTok;
 #pragma unroll
-  for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = kv_load<u16x8, kStream>(kp + 64 * s);
+    for (int s = 0; s < Tile<D>::kSteps; ++s) {
+      const int kr = kTokPerLoad * s + k_tok;
+      t.k[s] = kv_load<u16x8, kStream>(kbase + (kr < last ? kr : last) * row_bytes + 16 * k_ch);
+    }
+  } else {  // the MFMA operand layout straight from memory
+    const char* kp = kbase + (r < last ? r : last) * row_bytes + 16 * gq;
+#pragma unroll
+    for (int s = 0; s < Tile<D>::kSteps; ++s) t.k[s] = kv_load<u16x8, kStream>(kp + 64 * s);
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int vr = 4 * gq + j;
     t.v[j] = kv_load<VT, kStream>(vbase + (vr < last ? vr : last) * row_bytes + 2 * NT * r);
   }
+}
+
+// Per-wave LDS stage of one K tile (16 tokens x D, rows padded by 8 elements: the
+// 16-byte operand reads of 8 consecutive tokens hit distinct bank groups). The rows
+// arrive from load_tile_rows one token per D/8 lanes; the QK MFMA wants lane
+// r + 16 gq to hold token r, elements 32 ks + 8 gq .. +7.
+template <int D>
+struct KStage {
+  static constexpr int kPitch = D + 8;
+  uint16_t e[16 * kPitch];
+};
+
+template <int D>
+__device__ inline void k_operands_from_rows(KStage<D>& st, const Tile<D>& t, u16x8 (&ka)[Tile<D>::kSteps]) {
+  constexpr int kLanesPerTok = D / 8;
+  constexpr int kTokPerLoad = 64 / kLanesPerTok;
+  constexpr int kPitch = KStage<D>::kPitch;
+  const int lane = threadIdx.x & 63;
+  const int k_tok = lane / kLanesPerTok;
+  const int k_ch = lane % kLanesPerTok;
+  const int r = lane & 15;
+  const int gq = lane >> 4;
+  // the wave's previous reads of the stage come before these writes, and the writes
+  // before the reads below: one wave's LDS operations complete in order, and the
+  // fences keep the compiler from moving a lane's access across another lane's
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+  for (int s = 0; s < Tile<D>::kSteps; ++s)
+    *reinterpret_cast<u16x8*>(&st.e[(kTokPerLoad * s + k_tok) * kPitch + 8 * k_ch]) = t.k[s];
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+  for (int ks = 0; ks < Tile<D>::kSteps; ++ks)
+    ka[ks] = *reinterpret_cast<const u16x8*>(&st.e[r * kPitch + 32 * ks + 8 * gq]);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Same operand positions, each lane resolving its own token's page (page sizes that
@@ -563,10 +619,20 @@ paged_decode_kernel(DecodeParams p, GroupArgs<kGrouped> ga) {
 #pragma unroll
   for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // K tiles of the page-aligned path arrive as rows (head dims up to 128) and are
+  // turned into operands in LDS
+  __shared__ KStage<D> k_stage[kTileInPage && kKRows<D> ? kMaxWaves : 1];
   auto process = [&](const Tile<D>& cur, int t0) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kTileInPage && kKRows<D>) {
+      u16x8 ka[kSteps];
+      k_operands_from_rows<D>(k_stage[wave], cur, ka);
 #pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(cur.k[ks], qb[ks], s);
+      for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(ka[ks], qb[ks], s);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < kSteps; ++ks) s = T::mma_k32(cur.k[ks], qb[ks], s);
+    }
     float sv[4];
     if (t0 + 16 <= t_end) {
 #pragma unroll
