@@ -40,7 +40,7 @@ HBM_PEAK_GBS = 8000.0
 # copy of known size, over that pass's algorithmic bytes
 # (profiles/paged_decode_hbm_traffic_kv_pressure_b64.md). `traffic` in the JSON line is
 # this ratio times the algorithmic bytes of the run being reported.
-TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0113}
+TRAFFIC_PER_ALGORITHMIC_BYTE = {"kv_pressure": 1.0056}
 # The same for the chunked-prefill launch over the 8 chunks of a batch (q, out, the
 # K/V of every visible key once, the chunk's K/V rows written once and the page
 # ids): FETCH_SIZE and WRITE_SIZE of `bench.py --workload prefill --steps 4
