@@ -295,14 +295,16 @@ __device__ inline V kv_load(const char* p) {
     return *reinterpret_cast<const V*>(p);
 }
 
-// Loads of one tile whose 16 token rows are consecutive in one page, for the
-// lane's MFMA operand positions. kbase/vbase: wave-uniform byte address of the
-// tile's first row (head offset included); rows past `last` repeat row `last`.
-//   K: lane l reads row l%16, 16 B at d = 32 s + 8 (l/16)
+// Loads of one tile whose 16 token rows are consecutive in one page. kbase/vbase:
+// wave-uniform byte address of the tile's first row (head offset included); rows
+// past `last` repeat row `last`.
+//   K, D <= 128: load s, lane l reads row (64 / (D/8)) s + l / (D/8), 16 B at
+//                d = 8 (l % (D/8)): whole rows, turned into MFMA operands through
+//                the wave's LDS stage (k_operands_from_rows)
+//   K, D = 256:  lane l reads row l%16, 16 B at d = 32 s + 8 (l/16), the operand
+//                itself (the stage's operand registers would cost the kernel its
+//                second wave per SIMD at this head dim)
 //   V: lane l reads rows 4 (l/16) + j, D/16 elements at d = (D/16) (l%16)
-// Page-aligned tiles load K as whole rows and turn them into MFMA operands through
-// LDS at head dims up to 128; at 256 the stage's operand registers would cost the
-// kernel its second wave per SIMD, and K keeps the operand layout in memory.
 template <int D>
 constexpr bool kKRows = D <= 128;
 
@@ -374,8 +376,9 @@ __device__ inline void k_operands_from_rows(KStage<D>& st, const Tile<D>& t, u16
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Same operand positions, each lane resolving its own token's page (page sizes that
-// are not a multiple of 16, where a tile can straddle pages).
+// The MFMA operand positions (K as for D = 256 above, V as above), each lane
+// resolving its own token's page (page sizes that are not a multiple of 16, where a
+// tile can straddle pages).
 template <int D, bool kStream>
 __device__ inline void load_tile_any(const DecodeParams& p, const int32_t* idx, int head_off, int t0,
                                      int t_last, Tile<D>& t) {
