@@ -6,15 +6,18 @@
  *
  * plan_forward(states, ntoks, offsets, page_size, ref_count, tokens_used, mark,
  *              zero_pages, out, place)
- *   states      sequence states (objects with num_tokens, n_pages, bt, row, synced)
+ *   states      sequence states (objects with num_tokens, n_pages, bt, row, row_cap,
+ *               synced)
  *   ntoks       new tokens per sequence (list of int)
  *   offsets     input offsets per sequence (list of int), or None for zeros
  *   ref_count   int64 [P], tokens_used int64 [P] (updated), mark uint8/bool [P]
  *               (all zero on entry and on return)
  *   zero_pages  list of page ids awaiting zero-on-allocation, or None
  *   out         int32 buffer the plan is written to
- *   place       called with each state, in order, once the forward is known to be
- *               planned here (it gives the state its device row: row, synced)
+ *   place       called, in order, with each state whose device row is missing
+ *               (row < 0) or shorter than its table (row_cap < n_pages), once the
+ *               forward is known to be planned here (it gives the state its device
+ *               row: row, row_cap, synced)
  * Returns None when a page the forward writes is shared (copy-on-write is then the
  * caller's; nothing was changed), -n when `out` may need n entries and holds fewer
  * (nothing was changed), else (total, total_pages, patch_entries, zero_entries,
@@ -35,7 +38,7 @@
 #include <stdint.h>
 #include <string.h>
 
-static PyObject *s_num_tokens, *s_n_pages, *s_bt, *s_row, *s_synced;
+static PyObject *s_num_tokens, *s_n_pages, *s_bt, *s_row, *s_row_cap, *s_synced;
 
 static int get_i64(PyObject* obj, PyObject* name, int64_t* out) {
   PyObject* v = PyObject_GetAttr(obj, name);
@@ -191,21 +194,26 @@ static PyObject* plan_forward(PyObject* self, PyObject* const* args, Py_ssize_t 
     }
   }
 
-  /* the forward is planned here: the device rows, then the entries they lack */
+  /* the forward is planned here: the device rows (placed where a state has none or
+     one too short), then the entries they lack */
   for (Py_ssize_t b = 0; b < B; ++b) {
     PyObject* st = PyList_GET_ITEM(states, b);
-    PyObject* r = PyObject_CallOneArg(place, st);
-    if (!r) goto done;
-    Py_DECREF(r);
     seq_t* s = &sq[b];
-    int64_t have = 0;
-    if (get_i64(st, s_row, &s->row) < 0 || get_i64(st, s_synced, &s->syn) < 0 ||
-        get_i64(st, s_n_pages, &have) < 0)
-      goto done;
-    if (have != s->have) {
-      PyErr_SetString(PyExc_RuntimeError, "plan_forward: place changed a sequence's pages");
-      goto done;
+    int64_t row0 = 0, cap0 = 0;
+    if (get_i64(st, s_row, &row0) < 0 || get_i64(st, s_row_cap, &cap0) < 0) goto done;
+    s->row = row0;
+    if (row0 < 0 || cap0 < s->have) {
+      PyObject* r = PyObject_CallOneArg(place, st);
+      if (!r) goto done;
+      Py_DECREF(r);
+      int64_t have = 0;
+      if (get_i64(st, s_row, &s->row) < 0 || get_i64(st, s_n_pages, &have) < 0) goto done;
+      if (have != s->have) {
+        PyErr_SetString(PyExc_RuntimeError, "plan_forward: place changed a sequence's pages");
+        goto done;
+      }
     }
+    if (get_i64(st, s_synced, &s->syn) < 0) goto done;
     if (s->syn > s->have) s->syn = s->have;
     if (s->syn < 0) s->syn = 0;
     npatch += s->have - s->syn;
@@ -303,7 +311,8 @@ PyMODINIT_FUNC PyInit__nslg_host(void) {
   s_n_pages = PyUnicode_InternFromString("n_pages");
   s_bt = PyUnicode_InternFromString("bt");
   s_row = PyUnicode_InternFromString("row");
+  s_row_cap = PyUnicode_InternFromString("row_cap");
   s_synced = PyUnicode_InternFromString("synced");
-  if (!s_num_tokens || !s_n_pages || !s_bt || !s_row || !s_synced) return NULL;
+  if (!s_num_tokens || !s_n_pages || !s_bt || !s_row || !s_row_cap || !s_synced) return NULL;
   return PyModule_Create(&module);
 }

@@ -289,3 +289,40 @@ def test_native_plan_rejects_out_of_range_sequences():
         with pytest.raises(ValueError, match="out of range"):
             plan([st], [n], None, 4, rc, tu, mk, None, out, placed.append)
     assert not placed and not tu.any() and not out.any()
+
+
+def test_native_plan_places_only_rows_that_are_missing_or_short():
+    """The planner calls `place` for a state without a device row or with one shorter
+    than its table, and for no other: a steady forward makes no callback."""
+    c = _cache(4, 64, True)
+    for s in ("a", "b"):
+        c.allocate_sequence(s)
+    c.extend_sequence("a", 8)
+    c.extend_sequence("b", 3)
+    sa, sb = c.seqs["a"], c.seqs["b"]
+    plan = _lib.host().plan_forward
+    calls = []
+
+    def place(st):
+        calls.append(st.seq_id)
+        c._tables.place(st)
+
+    def run(states, ntoks):
+        out = np.zeros(4096, np.int32)
+        res = plan(states, ntoks, None, 4, c.pool.ref_count, c.pool.tokens_used, c.pool._mark, None, out, place)
+        assert isinstance(res, tuple)
+        for st in states:  # what the cache does after the plan's upload
+            st.synced = st.n_pages
+        return res
+
+    run([sa, sb], [8, 3])  # no rows yet: both placed
+    assert calls == ["a", "b"] and sa.row >= 0 and sb.row >= 0
+    for st, n in ((sa, 8), (sb, 3)):
+        st.num_tokens += n
+    del calls[:]
+    run([sa, sb], [1, 1])  # the rows hold the tables: no callback
+    assert calls == []
+    cap = sb.row_cap
+    c.extend_sequence("b", 4 * cap)  # b's table outgrows its row
+    run([sa, sb], [0, 4 * cap])
+    assert calls == ["b"] and sb.row_cap >= sb.n_pages
